@@ -1,0 +1,372 @@
+"""gotransformers_amd: MI355X (gfx950) mixture-of-experts forward for GoTransformers.
+
+Python bindings (ctypes) of libgtmoe.so, the C ABI declared in include/gtmoe.h.
+The classes mirror the reference's mixtureofexperts.MixtureOfExperts
+(mixtureofexperts/mixtureofexperts.go:14-31) and its lowprecision.Rows format
+(lowprecision/rows.go:8-18).  There is no CPU fallback: if libgtmoe.so is
+missing or no gfx950 device is present, the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from types import SimpleNamespace
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgtmoe.so")
+
+FLOAT64, FLOAT32, INT8, FP4 = 0, 1, 2, 3
+PATH_AUTO, PATH_FP32, PATH_BF16 = 0, 1, 2
+
+ROLE_ROUTER = 0
+ROLES = {("shared", "gate"): 1, ("shared", "up"): 2, ("shared", "down"): 3,
+         ("routed", "gate"): 4, ("routed", "up"): 5, ("routed", "down"): 6}
+
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOT_READY, ERR_OUT_OF_MEMORY = range(6)
+
+EXPORTED = [
+    "gtmoe_abi_version", "gtmoe_device_count", "gtmoe_open", "gtmoe_close", "gtmoe_last_error",
+    "gtmoe_encode_rows", "gtmoe_layer_create", "gtmoe_layer_destroy", "gtmoe_upload_rows",
+    "gtmoe_set_balance_biases", "gtmoe_get_balance_biases", "gtmoe_set_norm_weights", "gtmoe_forward",
+    "gtmoe_forward_device", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
+    "gtmoe_route_from_logits", "gtmoe_stack_forward", "gtmoe_stack_forward_device", "gtmoe_timing_enable",
+    "gtmoe_timing_reset", "gtmoe_timing_read", "gtmoe_last_path",
+]
+
+
+class GtmoeError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(f"gtmoe error {code}: {message}")
+        self.code = code
+
+
+class InvalidArgument(GtmoeError, ValueError):
+    """The reference would panic on this call."""
+
+
+class LayerDesc(C.Structure):
+    _fields_ = [("vector_size", C.c_int32), ("expert_hidden_size", C.c_int32), ("shared_experts", C.c_int32),
+                ("routed_experts", C.c_int32), ("experts_per_token", C.c_int32), ("precision", C.c_int32),
+                ("use_hash_routing", C.c_int32), ("reserved", C.c_int32), ("clamp_limit", C.c_double)]
+
+
+class RowsStruct(C.Structure):
+    _fields_ = [("precision", C.c_int32), ("rows", C.c_int32), ("width", C.c_int32), ("reserved", C.c_int32),
+                ("values", C.c_void_p), ("values_bytes", C.c_size_t), ("scales", C.c_void_p),
+                ("scale_count", C.c_size_t)]
+
+
+_lib = None
+
+
+def library():
+    """Load libgtmoe.so (built by gotransformers_amd/build.py)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() or gotransformers_amd/build.py")
+    L = C.CDLL(LIB_PATH)
+    P, i32, u32, dbl = C.c_void_p, C.c_int32, C.c_uint32, C.c_double
+    sig = {
+        "gtmoe_abi_version": ([], i32),
+        "gtmoe_device_count": ([P], i32),
+        "gtmoe_open": ([i32, P], i32),
+        "gtmoe_close": ([P], i32),
+        "gtmoe_last_error": ([P], C.c_char_p),
+        "gtmoe_encode_rows": ([i32, i32, i32, P, P, P], i32),
+        "gtmoe_layer_create": ([P, C.POINTER(LayerDesc), P], i32),
+        "gtmoe_layer_destroy": ([P], i32),
+        "gtmoe_upload_rows": ([P, i32, i32, C.POINTER(RowsStruct), P], i32),
+        "gtmoe_set_balance_biases": ([P, P], i32),
+        "gtmoe_get_balance_biases": ([P, P], i32),
+        "gtmoe_set_norm_weights": ([P, P], i32),
+        "gtmoe_forward": ([P, i32, P, P, P, u32], i32),
+        "gtmoe_forward_device": ([P, i32, P, P, P, u32, P], i32),
+        "gtmoe_last_routing": ([P, P, P, P, P, P, P], i32),
+        "gtmoe_last_expert_load": ([P, P], i32),
+        "gtmoe_update_balance": ([P, dbl], i32),
+        "gtmoe_route_from_logits": ([P, i32, P, P, P, P, P, P], i32),
+        "gtmoe_stack_forward": ([P, i32, i32, P, P, u32, P, P], i32),
+        "gtmoe_stack_forward_device": ([P, i32, i32, P, P, u32, P], i32),
+        "gtmoe_timing_enable": ([P, i32], i32),
+        "gtmoe_timing_reset": ([P], i32),
+        "gtmoe_timing_read": ([P, i32, P, P, P, P], i32),
+        "gtmoe_last_path": ([P, P], i32),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _check(code, ctx_handle=None):
+    if code == OK:
+        return
+    msg = library().gtmoe_last_error(ctx_handle)
+    msg = msg.decode() if msg else ""
+    if code == ERR_INVALID_ARGUMENT:
+        raise InvalidArgument(code, msg)
+    raise GtmoeError(code, msg)
+
+
+def device_count():
+    n = C.c_int32(0)
+    _check(library().gtmoe_device_count(C.byref(n)))
+    return n.value
+
+
+# --------------------------------------------------------------------------
+# lowprecision rows
+# --------------------------------------------------------------------------
+
+def encode_rows(precision, values):
+    """lowprecision.Rows.Append over every row of a float64 matrix
+    (lowprecision/rows.go:38-79), computed by libgtmoe's host encoder.
+    Returns a namespace (precision, rows, width, values, scales) in the
+    reference's RowsSnapshot storage."""
+    values = np.ascontiguousarray(np.atleast_2d(values), dtype=np.float64)
+    rows, width = values.shape
+    scales = None
+    if precision == FLOAT64:
+        out = np.empty((rows, width), np.float64)
+    elif precision == FLOAT32:
+        out = np.empty((rows, width), np.float32)
+    elif precision == INT8:
+        out = np.empty((rows, width), np.int8)
+        scales = np.empty((rows, (width + 15) // 16), np.float32)
+    elif precision == FP4:
+        out = np.empty((rows, (width + 1) // 2), np.uint8)
+        scales = np.empty((rows, (width + 15) // 16), np.float32)
+    else:
+        raise ValueError(f"unknown precision {precision}")
+    _check(library().gtmoe_encode_rows(precision, rows, width, values.ctypes.data, out.ctypes.data, _ptr(scales)))
+    return SimpleNamespace(precision=precision, rows=rows, width=width, values=out, scales=scales)
+
+
+def _rows_struct(r):
+    v = r.values
+    s = r.scales
+    return RowsStruct(int(r.precision), int(r.rows), int(r.width), 0, v.ctypes.data, v.nbytes,
+                      None if s is None else s.ctypes.data, 0 if s is None else s.size)
+
+
+# --------------------------------------------------------------------------
+# context
+# --------------------------------------------------------------------------
+
+class Context:
+    """One GPU: gtmoe_open / gtmoe_close (replaces gpu.Open, gpu/device.go:90-130)."""
+
+    def __init__(self, device=0):
+        h = C.c_void_p()
+        _check(library().gtmoe_open(device, C.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            library().gtmoe_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def check(self, code):
+        _check(code, self.handle)
+
+    # per-kernel HIP-event timing
+    def timing(self, enabled=True):
+        self.check(library().gtmoe_timing_enable(self.handle, 1 if enabled else 0))
+
+    def timing_reset(self):
+        self.check(library().gtmoe_timing_reset(self.handle))
+
+    def timing_read(self):
+        cap = 64
+        names = C.create_string_buffer(64 * cap)
+        ms = np.zeros(cap, np.float64)
+        launches = np.zeros(cap, np.int32)
+        n = C.c_int32(0)
+        self.check(library().gtmoe_timing_read(self.handle, cap, names, ms.ctypes.data, launches.ctypes.data,
+                                                C.byref(n)))
+        out = {}
+        for i in range(min(n.value, cap)):
+            name = names.raw[64 * i:64 * i + 64].split(b"\0", 1)[0].decode()
+            out[name] = (float(ms[i]), int(launches[i]))
+        return out
+
+
+# --------------------------------------------------------------------------
+# MixtureOfExperts
+# --------------------------------------------------------------------------
+
+class MixtureOfExperts:
+    """A mixtureofexperts.MixtureOfExperts whose weights live in HBM.
+
+    Method names follow the reference: forward (Forward), last_expert_load
+    (LastExpertLoad), update_balance (UpdateBalance), balance_biases
+    (BalanceBiases)."""
+
+    def __init__(self, ctx, vector_size, expert_hidden_size, shared_experts, routed_experts, experts_per_token,
+                 precision=INT8, clamp_limit=0.0, use_hash_routing=False):
+        self.ctx = ctx
+        self.vector_size = vector_size
+        self.expert_hidden_size = expert_hidden_size
+        self.shared_experts = shared_experts
+        self.routed_experts = routed_experts
+        self.experts_per_token = experts_per_token
+        self.precision = precision
+        self.use_hash_routing = use_hash_routing
+        desc = LayerDesc(vector_size, expert_hidden_size, shared_experts, routed_experts, experts_per_token,
+                         precision, 1 if use_hash_routing else 0, 0, float(clamp_limit))
+        h = C.c_void_p()
+        ctx.check(library().gtmoe_layer_create(ctx.handle, C.byref(desc), C.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def from_spec(cls, ctx, spec):
+        """Build and upload a layer from a namespace with the reference's
+        structure (shared/routed experts with gate/up/down layers, a router
+        layer and balance biases)."""
+        m = cls(ctx, spec.vector_size, spec.hidden_size, len(spec.shared), len(spec.routed), spec.experts_per_token,
+                spec.precision, getattr(spec, "clamp_limit", 0.0), spec.use_hash_routing)
+        for kind, experts in (("shared", spec.shared), ("routed", spec.routed)):
+            for i, e in enumerate(experts):
+                for which in ("gate", "up", "down"):
+                    layer = getattr(e, which)
+                    m.upload(kind, i, which, layer.weights, layer.biases)
+        if not spec.use_hash_routing:
+            m.upload_router(spec.router.weights, spec.router.biases)
+        m.balance_biases = spec.balance_biases
+        return m
+
+    def destroy(self):
+        if self.handle:
+            library().gtmoe_layer_destroy(self.handle)
+            self.handle = None
+
+    def upload(self, kind, index, which, rows, biases):
+        b = np.ascontiguousarray(biases, np.float64)
+        s = _rows_struct(rows)
+        self.ctx.check(library().gtmoe_upload_rows(self.handle, ROLES[(kind, which)], index, C.byref(s), b.ctypes.data))
+
+    def upload_router(self, rows, biases):
+        b = np.ascontiguousarray(biases, np.float64)
+        s = _rows_struct(rows)
+        self.ctx.check(library().gtmoe_upload_rows(self.handle, ROLE_ROUTER, 0, C.byref(s), b.ctypes.data))
+
+    @property
+    def balance_biases(self):
+        out = np.empty(self.routed_experts, np.float64)
+        self.ctx.check(library().gtmoe_get_balance_biases(self.handle, out.ctypes.data))
+        return out
+
+    @balance_biases.setter
+    def balance_biases(self, values):
+        v = np.ascontiguousarray(values, np.float64)
+        if v.shape != (self.routed_experts,):
+            raise ValueError(f"has {self.routed_experts} routed experts but {v.size} balance biases")
+        self.ctx.check(library().gtmoe_set_balance_biases(self.handle, v.ctypes.data))
+
+    def set_norm_weights(self, weights):
+        w = np.ascontiguousarray(weights, np.float64)
+        self.ctx.check(library().gtmoe_set_norm_weights(self.handle, w.ctypes.data))
+
+    def forward(self, inputs, token_ids=None, path=PATH_AUTO):
+        """MixtureOfExperts.Forward: float64 T x d in, float64 T x d out."""
+        x = np.ascontiguousarray(np.atleast_2d(inputs), np.float64)
+        if x.shape[1] != self.vector_size:
+            raise InvalidArgument(ERR_INVALID_ARGUMENT,
+                                  f"each row has {x.shape[1]} values but the experts take {self.vector_size}")
+        ids = None
+        if token_ids is not None:
+            ids = np.ascontiguousarray(token_ids, np.int64)
+            if ids.shape != (x.shape[0],):
+                raise InvalidArgument(ERR_INVALID_ARGUMENT, f"got {ids.size} token IDs for {x.shape[0]} rows")
+        out = np.empty_like(x)
+        self.ctx.check(library().gtmoe_forward(self.handle, x.shape[0], x.ctypes.data, _ptr(ids), out.ctypes.data,
+                                                path))
+        return out
+
+    def forward_device(self, tokens, inputs_ptr, outputs_ptr, token_ids_ptr=None, path=PATH_AUTO, stream=None):
+        """Forward over device-resident fp32 buffers (raw device addresses)."""
+        self.ctx.check(library().gtmoe_forward_device(self.handle, tokens, inputs_ptr, token_ids_ptr, outputs_ptr,
+                                                       path, stream))
+
+    def last_routing(self):
+        T = C.c_int32(0)
+        self.ctx.check(library().gtmoe_last_routing(self.handle, C.byref(T), None, None, None, None, None))
+        T = T.value
+        k, E = self.experts_per_token, self.routed_experts
+        chosen = np.empty((T, k), np.int32)
+        gates = np.empty((T, k), np.float64)
+        load = np.empty(E, np.int32)
+        rows = np.empty(T * k, np.int32)
+        offsets = np.empty(E + 1, np.int32)
+        self.ctx.check(library().gtmoe_last_routing(self.handle, None, chosen.ctypes.data, gates.ctypes.data,
+                                                     load.ctypes.data, rows.ctypes.data, offsets.ctypes.data))
+        return SimpleNamespace(chosen=chosen, gates=gates, load=load, rows=rows, offsets=offsets)
+
+    def last_expert_load(self):
+        load = np.empty(self.routed_experts, np.int32)
+        self.ctx.check(library().gtmoe_last_expert_load(self.handle, load.ctypes.data))
+        return load
+
+    def update_balance(self, rate):
+        self.ctx.check(library().gtmoe_update_balance(self.handle, float(rate)))
+
+    def route_from_logits(self, logits):
+        lg = np.ascontiguousarray(np.atleast_2d(logits), np.float64)
+        T = lg.shape[0]
+        k, E = self.experts_per_token, self.routed_experts
+        chosen = np.empty((T, k), np.int32)
+        gates = np.empty((T, k), np.float64)
+        load = np.empty(E, np.int32)
+        rows = np.empty(T * k, np.int32)
+        offsets = np.empty(E + 1, np.int32)
+        self.ctx.check(library().gtmoe_route_from_logits(self.handle, T, lg.ctypes.data, chosen.ctypes.data,
+                                                          gates.ctypes.data, load.ctypes.data, rows.ctypes.data,
+                                                          offsets.ctypes.data))
+        return SimpleNamespace(chosen=chosen, gates=gates, load=load, rows=rows, offsets=offsets)
+
+    @property
+    def last_path(self):
+        p = C.c_int32(0)
+        self.ctx.check(library().gtmoe_last_path(self.handle, C.byref(p)))
+        return p.value
+
+
+def _layer_array(layers):
+    arr = (C.c_void_p * len(layers))(*[m.handle.value for m in layers])
+    return arr
+
+
+def stack_forward(layers, x, token_ids=None, path=PATH_AUTO, with_routing=False):
+    """x <- x + MoE_l(RMSNorm_l(x)) over the layers (transformer/block.go:71-77)."""
+    ctx = layers[0].ctx
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float64).copy()
+    ids = None if token_ids is None else np.ascontiguousarray(token_ids, np.int64)
+    T, k = x.shape[0], layers[0].experts_per_token
+    chosen = np.empty((len(layers), T, k), np.int32) if with_routing else None
+    gates = np.empty((len(layers), T, k), np.float64) if with_routing else None
+    ctx.check(library().gtmoe_stack_forward(_layer_array(layers), len(layers), T, x.ctypes.data, _ptr(ids), path,
+                                            _ptr(chosen), _ptr(gates)))
+    return (x, chosen, gates) if with_routing else x
+
+
+def stack_forward_device(layers, tokens, x_ptr, token_ids_ptr=None, path=PATH_AUTO, stream=None):
+    ctx = layers[0].ctx
+    ctx.check(library().gtmoe_stack_forward_device(_layer_array(layers), len(layers), tokens, x_ptr, token_ids_ptr,
+                                                   path, stream))

@@ -1,0 +1,1053 @@
+// C ABI of libgtmoe: contexts, layers resident in HBM, and the forward
+// orchestration.  The host-side object mirrors mixtureofexperts.MixtureOfExperts
+// (mixtureofexperts/mixtureofexperts.go:14-31): weights per role, balance
+// biases, and the routing state of the last forward for LastExpertLoad and
+// UpdateBalance.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "gtmoe.h"
+
+using namespace gtmoe;
+
+namespace {
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxK = 8;
+constexpr int kMaxGemvK = 4096;
+// AUTO takes the dequant-GEMV path while routed tokens per expert stay at or
+// below this many (decode batches); above it the MFMA grouped GEMM.
+constexpr int kGemvTokensPerExpert = 8;
+
+thread_local std::string g_open_error;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+struct TimingRecord {
+    std::string name;
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
+struct gtmoe_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::recursive_mutex mu;
+    std::string error;
+    bool timing = false;
+    std::vector<TimingRecord> pending;
+    std::vector<hipEvent_t> spare_events;
+    std::map<std::string, std::pair<double, int>> totals;
+};
+
+namespace {
+
+int32_t fail(gtmoe_context *ctx, int32_t code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->error = buf;
+    else g_open_error = buf;
+    return code;
+}
+
+#define HIP_TRY(ctx, call)                                                                              \
+    do {                                                                                                \
+        hipError_t e_ = (call);                                                                         \
+        if (e_ != hipSuccess)                                                                           \
+            return fail((ctx), e_ == hipErrorOutOfMemory ? GTMOE_ERR_OUT_OF_MEMORY : GTMOE_ERR_DEVICE, \
+                        "%s: %s", #call, hipGetErrorString(e_));                                        \
+    } while (0)
+
+hipEvent_t take_event(gtmoe_context *ctx)
+{
+    if (!ctx->spare_events.empty()) {
+        hipEvent_t e = ctx->spare_events.back();
+        ctx->spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Launch one kernel through `fn`, bracketed by events when timing is on.
+template <class F>
+int32_t run(gtmoe_context *ctx, hipStream_t s, const char *name, F &&fn)
+{
+    hipEvent_t a = nullptr, b = nullptr;
+    if (ctx->timing) {
+        a = take_event(ctx);
+        if (a) (void)hipEventRecord(a, s);
+    }
+    hipError_t e = fn();
+    if (ctx->timing && a) {
+        b = take_event(ctx);
+        if (b) {
+            (void)hipEventRecord(b, s);
+            ctx->pending.push_back({name, a, b});
+        } else {
+            ctx->spare_events.push_back(a);
+        }
+    }
+    if (e != hipSuccess) return fail(ctx, GTMOE_ERR_DEVICE, "kernel %s: %s", name, hipGetErrorString(e));
+    return GTMOE_OK;
+}
+
+#define RUN(ctx, s, name, expr)                                      \
+    do {                                                             \
+        int32_t rc_ = run((ctx), (s), (name), [&]() { return (expr); }); \
+        if (rc_ != GTMOE_OK) return rc_;                             \
+    } while (0)
+
+}  // namespace
+
+// Device buffers a forward needs, sized for `cap` tokens.
+struct Workspace {
+    int cap = -1;
+    void *base = nullptr;
+    double *x64 = nullptr;   // [T][d] host-API staging
+    double *y64 = nullptr;   // [T][d]
+    float *xf = nullptr;     // [T][dp]
+    uint16_t *xb = nullptr;  // [T][dp] bf16
+    float *xs = nullptr;     // [T][d] residual stream of a host-API stack
+    double *logits = nullptr;
+    int32_t *chosen = nullptr;
+    double *gates = nullptr;
+    float *gates32 = nullptr;
+    int64_t *ids = nullptr;
+    int32_t *load = nullptr;
+    int32_t *offsets = nullptr;
+    int32_t *rows = nullptr;
+    int32_t *pos = nullptr;
+    int32_t *goff = nullptr;
+    int32_t *tile_off = nullptr;
+    int32_t *tok = nullptr;
+    float *hidden32 = nullptr;    // [P][hp]
+    uint16_t *hidden16 = nullptr;  // [P][hp] bf16
+    float *slot_out = nullptr;    // [P][d]
+};
+
+struct gtmoe_layer {
+    gtmoe_context *ctx = nullptr;
+    gtmoe_layer_desc desc{};
+    int d = 0, h = 0, S = 0, E = 0, k = 0, G = 0, dp = 0, hp = 0;
+    DeviceMatrix gate, up, down;
+    float *router_w = nullptr;  // [E][dp]
+    double *router_b = nullptr;  // [E]
+    double *balance = nullptr;   // [E]
+    std::vector<double> balance_host;
+    float *norm_w = nullptr;  // [d]
+    bool has_norm = false;
+    std::vector<char> uploaded;  // per (role, index)
+    Workspace ws;
+    // state of the last forward
+    int last_T = -1;
+    int last_path = GTMOE_PATH_FP32;
+    hipStream_t last_stream = nullptr;
+    std::vector<int32_t> last_load;
+    bool load_on_host = false;
+};
+
+namespace {
+
+int role_slot(const gtmoe_layer *L, int role, int index)
+{
+    switch (role) {
+    case GTMOE_ROLE_ROUTER: return 0;
+    case GTMOE_ROLE_SHARED_GATE:
+    case GTMOE_ROLE_SHARED_UP:
+    case GTMOE_ROLE_SHARED_DOWN: return 1 + (role - GTMOE_ROLE_SHARED_GATE) * L->G + index;
+    default: return 1 + (role - GTMOE_ROLE_ROUTED_GATE) * L->G + L->S + index;
+    }
+}
+
+int32_t alloc_matrix(gtmoe_context *ctx, DeviceMatrix &m, int precision, int rows, int width, int groups)
+{
+    m.precision = precision;
+    m.rows = rows;
+    m.width = width;
+    m.kp = pad_k(width);
+    m.nblocks = m.kp / kValuesPerScale;
+    m.row_bytes = precision == kInt8 ? m.kp : precision == kFP4 ? m.kp / 2 : m.kp * 4;
+    m.groups = groups;
+    const size_t vb = (size_t)groups * m.group_value_bytes();
+    HIP_TRY(ctx, hipMalloc(&m.values, vb));
+    HIP_TRY(ctx, hipMemset(m.values, 0, vb));
+    if (precision != kFloat32) {
+        const size_t sb = (size_t)groups * m.group_scales() * sizeof(float);
+        HIP_TRY(ctx, hipMalloc(&m.scales, sb));
+        HIP_TRY(ctx, hipMemset(m.scales, 0, sb));
+    }
+    const size_t bb = (size_t)groups * rows * sizeof(float);
+    HIP_TRY(ctx, hipMalloc(&m.biases, bb));
+    HIP_TRY(ctx, hipMemset(m.biases, 0, bb));
+    return GTMOE_OK;
+}
+
+void free_matrix(DeviceMatrix &m)
+{
+    if (m.values) (void)hipFree(m.values);
+    if (m.scales) (void)hipFree(m.scales);
+    if (m.biases) (void)hipFree(m.biases);
+    m.values = nullptr;
+    m.scales = nullptr;
+    m.biases = nullptr;
+}
+
+// Check a Rows snapshot like RowsFromSnapshot (lowprecision/rows.go:172-203).
+int32_t check_rows(gtmoe_context *ctx, const gtmoe_rows *r, int rows, int width)
+{
+    if (!r) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "rows are null");
+    if (r->rows != rows || r->width != width)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "got %dx%d weights but the layer holds %dx%d", r->rows, r->width,
+                    rows, width);
+    const size_t blocks = (size_t)(width + 15) / 16;
+    size_t want_values = 0, want_scales = 0;
+    switch (r->precision) {
+    case GTMOE_FLOAT64: want_values = (size_t)rows * width * 8; break;
+    case GTMOE_FLOAT32: want_values = (size_t)rows * width * 4; break;
+    case GTMOE_INT8:
+        want_values = (size_t)rows * width;
+        want_scales = (size_t)rows * blocks;
+        break;
+    case GTMOE_FP4:
+        want_values = (size_t)rows * ((width + 1) / 2);
+        want_scales = (size_t)rows * blocks;
+        break;
+    default: return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown precision %d", r->precision);
+    }
+    if (r->values_bytes != want_values || r->scale_count != want_scales)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                    "rows snapshot for %d rows of width %d at precision %d has the wrong amount of data", rows, width,
+                    r->precision);
+    if (want_values && !r->values) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "values are null");
+    if (want_scales && !r->scales) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "scales are null");
+    return GTMOE_OK;
+}
+
+// Decoded float64 value i of row `row` (Rows.Row, lowprecision/rows.go:87-119).
+double decoded_value(const gtmoe_rows *r, int row, int i)
+{
+    static const double kFp4[8] = {0, 0.5, 1, 1.5, 2, 3, 4, 6};
+    const size_t blocks = (size_t)(r->width + 15) / 16;
+    switch (r->precision) {
+    case GTMOE_FLOAT64: return ((const double *)r->values)[(size_t)row * r->width + i];
+    case GTMOE_FLOAT32: return (double)((const float *)r->values)[(size_t)row * r->width + i];
+    case GTMOE_INT8:
+        return (double)((const int8_t *)r->values)[(size_t)row * r->width + i] *
+               (double)r->scales[row * blocks + i / 16];
+    default: {
+        const uint8_t byte = ((const uint8_t *)r->values)[(size_t)row * ((r->width + 1) / 2) + i / 2];
+        const uint8_t code = (i % 2) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 15);
+        const double v = kFp4[code & 7] * (double)r->scales[row * blocks + i / 16];
+        return (code & 8) ? -v : v;
+    }
+    }
+}
+
+int32_t ensure_workspace(gtmoe_layer *L, int T)
+{
+    gtmoe_context *ctx = L->ctx;
+    if (T <= L->ws.cap) return GTMOE_OK;
+    int cap = T < 64 ? 64 : T;
+    if (L->ws.base) {
+        HIP_TRY(ctx, hipDeviceSynchronize());
+        (void)hipFree(L->ws.base);
+        L->ws = Workspace{};
+    }
+    const size_t P = (size_t)cap * (L->S + L->k);
+    const size_t TK = (size_t)cap * L->k;
+    struct Part {
+        void **ptr;
+        size_t bytes;
+    };
+    Workspace &w = L->ws;
+    Part parts[] = {
+        {(void **)&w.x64, (size_t)cap * L->d * 8},      {(void **)&w.y64, (size_t)cap * L->d * 8},
+        {(void **)&w.xf, (size_t)cap * L->dp * 4},      {(void **)&w.xb, (size_t)cap * L->dp * 2},
+        {(void **)&w.xs, (size_t)cap * L->d * 4},       {(void **)&w.logits, (size_t)cap * L->E * 8},
+        {(void **)&w.chosen, TK * 4},                   {(void **)&w.gates, TK * 8},
+        {(void **)&w.gates32, TK * 4},                  {(void **)&w.ids, (size_t)cap * 8},
+        {(void **)&w.load, (size_t)L->E * 4},           {(void **)&w.offsets, (size_t)(L->E + 1) * 4},
+        {(void **)&w.rows, TK * 4},                     {(void **)&w.pos, TK * 4},
+        {(void **)&w.goff, (size_t)(L->G + 1) * 4},     {(void **)&w.tile_off, (size_t)(L->G + 1) * 4},
+        {(void **)&w.tok, P * 4},                       {(void **)&w.hidden32, P * L->hp * 4},
+        {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
+    };
+    size_t total = 0;
+    for (const Part &p : parts) total += align_up(p.bytes, 256);
+    void *base = nullptr;
+    HIP_TRY(ctx, hipMalloc(&base, total));
+    // zero once: padding columns of the activation buffers are never written
+    HIP_TRY(ctx, hipMemset(base, 0, total));
+    size_t off = 0;
+    for (const Part &p : parts) {
+        *p.ptr = (char *)base + off;
+        off += align_up(p.bytes, 256);
+    }
+    w.base = base;
+    w.cap = cap;
+    return GTMOE_OK;
+}
+
+bool layer_ready(const gtmoe_layer *L, std::string &missing)
+{
+    for (int role = GTMOE_ROLE_ROUTER; role <= GTMOE_ROLE_ROUTED_DOWN; ++role) {
+        if (role == GTMOE_ROLE_ROUTER && L->desc.use_hash_routing) continue;
+        const int n = role == GTMOE_ROLE_ROUTER ? 1 : role <= GTMOE_ROLE_SHARED_DOWN ? L->S : L->E;
+        for (int i = 0; i < n; ++i)
+            if (!L->uploaded[role_slot(L, role, i)]) {
+                char buf[96];
+                snprintf(buf, sizeof buf, "role %d index %d", role, i);
+                missing = buf;
+                return false;
+            }
+    }
+    return true;
+}
+
+int choose_path(const gtmoe_layer *L, int T, uint32_t flags)
+{
+    if (flags == GTMOE_PATH_FP32 || flags == GTMOE_PATH_BF16) return (int)flags;
+    const long long routed = (long long)T * L->k;
+    const bool few = routed <= (long long)kGemvTokensPerExpert * L->E;
+    const bool fits = L->dp <= kMaxGemvK && L->hp <= kMaxGemvK;
+    return (few && fits) ? GTMOE_PATH_FP32 : GTMOE_PATH_BF16;
+}
+
+// Routing, dispatch and the expert kernels, reading the prepared inputs in
+// ws.xf (fp32 path) or ws.xb (bf16 path); leaves the slot outputs in
+// ws.slot_out.  token_ids: device pointer (hash routing).
+int32_t route_and_experts(gtmoe_layer *L, int T, const int64_t *token_ids, int path, hipStream_t s)
+{
+    gtmoe_context *ctx = L->ctx;
+    Workspace &w = L->ws;
+    if (L->desc.use_hash_routing) {
+        RUN(ctx, s, "hash_route", launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
+    } else {
+        RUN(ctx, s, "router", launch_router(w.xf, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s));
+        RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
+    }
+    const int bm = mfma_tile_m();
+    RUN(ctx, s, "dispatch",
+        launch_dispatch(w.chosen, T, L->k, L->E, L->S, bm, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
+                        w.tile_off, s));
+    if (path == GTMOE_PATH_FP32) {
+        GemvArgs a{};
+        a.w0 = L->gate.values;
+        a.s0 = L->gate.scales;
+        a.b0 = L->gate.biases;
+        a.w1 = L->up.values;
+        a.s1 = L->up.scales;
+        a.b1 = L->up.biases;
+        a.w_group_stride = (long long)L->gate.group_value_bytes();
+        a.s_group_stride = (long long)L->gate.group_scales();
+        a.rows = L->h;
+        a.nblocks = L->gate.nblocks;
+        a.row_bytes = L->gate.row_bytes;
+        a.in = w.xf;
+        a.ld_in = L->dp;
+        a.tok = w.tok;
+        a.goff = w.goff;
+        a.out = w.hidden32;
+        a.ld_out = L->hp;
+        a.clamp = (float)L->desc.clamp_limit;
+        RUN(ctx, s, "gemv_gateup", launch_gemv_gateup(a, L->gate.precision, L->G, s));
+        GemvArgs b{};
+        b.w0 = L->down.values;
+        b.s0 = L->down.scales;
+        b.b0 = L->down.biases;
+        b.w_group_stride = (long long)L->down.group_value_bytes();
+        b.s_group_stride = (long long)L->down.group_scales();
+        b.rows = L->d;
+        b.nblocks = L->down.nblocks;
+        b.row_bytes = L->down.row_bytes;
+        b.in = w.hidden32;
+        b.ld_in = L->hp;
+        b.tok = nullptr;
+        b.goff = w.goff;
+        b.out = w.slot_out;
+        b.ld_out = L->d;
+        RUN(ctx, s, "gemv_down", launch_gemv_down(b, L->down.precision, L->G, s));
+    } else {
+        const int max_tiles = L->S * ((T + bm - 1) / bm) + (T * L->k + bm - 1) / bm + L->E;
+        MfmaArgs a{};
+        a.w0 = L->gate.values;
+        a.s0 = L->gate.scales;
+        a.b0 = L->gate.biases;
+        a.w1 = L->up.values;
+        a.s1 = L->up.scales;
+        a.b1 = L->up.biases;
+        a.w_group_stride = (long long)L->gate.group_value_bytes();
+        a.s_group_stride = (long long)L->gate.group_scales();
+        a.n = L->h;
+        a.kp = L->dp;
+        a.row_bytes = L->gate.row_bytes;
+        a.nblocks = L->gate.nblocks;
+        a.a = w.xb;
+        a.lda = L->dp;
+        a.tok = w.tok;
+        a.goff = w.goff;
+        a.tile_off = w.tile_off;
+        a.groups = L->G;
+        a.out = w.hidden16;
+        a.ldo = L->hp;
+        a.clamp = (float)L->desc.clamp_limit;
+        RUN(ctx, s, "mfma_gateup", launch_mfma_gateup(a, L->gate.precision, max_tiles, s));
+        MfmaArgs b{};
+        b.w0 = L->down.values;
+        b.s0 = L->down.scales;
+        b.b0 = L->down.biases;
+        b.w_group_stride = (long long)L->down.group_value_bytes();
+        b.s_group_stride = (long long)L->down.group_scales();
+        b.n = L->d;
+        b.kp = L->hp;
+        b.row_bytes = L->down.row_bytes;
+        b.nblocks = L->down.nblocks;
+        b.a = w.hidden16;
+        b.lda = L->hp;
+        b.tok = nullptr;
+        b.goff = w.goff;
+        b.tile_off = w.tile_off;
+        b.groups = L->G;
+        b.out = w.slot_out;
+        b.ldo = L->d;
+        RUN(ctx, s, "mfma_down", launch_mfma_down(b, L->down.precision, max_tiles, s));
+    }
+    return GTMOE_OK;
+}
+
+void mark_forward(gtmoe_layer *L, int T, int path, hipStream_t s)
+{
+    L->last_T = T;
+    L->last_path = path;
+    L->last_stream = s;
+    L->load_on_host = false;
+}
+
+int32_t fetch_load(gtmoe_layer *L)
+{
+    gtmoe_context *ctx = L->ctx;
+    if (L->last_T < 0) return fail(ctx, GTMOE_ERR_NOT_READY, "call Forward before reading the expert load");
+    if (L->load_on_host) return GTMOE_OK;
+    L->last_load.assign(L->E, 0);
+    if (L->last_T > 0) {
+        HIP_TRY(ctx, hipStreamSynchronize(L->last_stream));
+        HIP_TRY(ctx, hipMemcpy(L->last_load.data(), L->ws.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost));
+    }
+    L->load_on_host = true;
+    return GTMOE_OK;
+}
+
+int32_t check_layer_call(gtmoe_layer *L)
+{
+    if (!L || !L->ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::string missing;
+    if (!layer_ready(L, missing))
+        return fail(L->ctx, GTMOE_ERR_NOT_READY, "mixture of experts: weights not uploaded (%s)", missing.c_str());
+    return GTMOE_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int32_t gtmoe_abi_version(void) { return GTMOE_ABI_VERSION; }
+
+int32_t gtmoe_device_count(int32_t *count)
+{
+    if (!count) return GTMOE_ERR_INVALID_ARGUMENT;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_open(int32_t device, gtmoe_context **out)
+{
+    if (!out) return fail(nullptr, GTMOE_ERR_INVALID_ARGUMENT, "out is null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, GTMOE_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    if (device < 0 || device >= n) return fail(nullptr, GTMOE_ERR_INVALID_ARGUMENT, "device %d of %d", device, n);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail(nullptr, GTMOE_ERR_DEVICE, "cannot read properties of device %d", device);
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, GTMOE_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950", device,
+                    prop.gcnArchName);
+    if (hipSetDevice(device) != hipSuccess) return fail(nullptr, GTMOE_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+    gtmoe_context *ctx = new gtmoe_context;
+    ctx->device = device;
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return fail(nullptr, GTMOE_ERR_DEVICE, "cannot create a stream");
+    }
+    *out = ctx;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_close(gtmoe_context *ctx)
+{
+    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    {
+        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        for (auto &r : ctx->pending) {
+            (void)hipEventDestroy(r.start);
+            (void)hipEventDestroy(r.stop);
+        }
+        for (auto e : ctx->spare_events) (void)hipEventDestroy(e);
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+    return GTMOE_OK;
+}
+
+const char *gtmoe_last_error(const gtmoe_context *ctx)
+{
+    return ctx ? ctx->error.c_str() : g_open_error.c_str();
+}
+
+int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtmoe_layer **out)
+{
+    if (!ctx || !desc || !out) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    *out = nullptr;
+    const gtmoe_layer_desc &D = *desc;
+    // buildMixtureOfExperts checks (mixtureofexperts.go:47-56) and NewLayer's
+    if (D.shared_experts < 0)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "number of shared experts can't be negative, got %d",
+                    D.shared_experts);
+    if (D.routed_experts < 1)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "needs at least 1 routed expert, got %d", D.routed_experts);
+    if (D.experts_per_token < 1 || D.experts_per_token > D.routed_experts)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "experts per token must be between 1 and %d, got %d",
+                    D.routed_experts, D.experts_per_token);
+    if (D.vector_size < 1 || D.expert_hidden_size < 1)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "vector size and hidden size must be at least 1");
+    if (D.clamp_limit < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "clamp limit must be above 0");
+    if (D.routed_experts > kMaxExperts)
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "at most %d routed experts on the GPU, got %d", kMaxExperts,
+                    D.routed_experts);
+    if (D.experts_per_token > kMaxK)
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "at most %d experts per token on the GPU, got %d", kMaxK,
+                    D.experts_per_token);
+    if (D.precision != GTMOE_FLOAT32 && D.precision != GTMOE_INT8 && D.precision != GTMOE_FP4)
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "expert weights at precision %d are not offered on the GPU",
+                    D.precision);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    gtmoe_layer *L = new gtmoe_layer;
+    L->ctx = ctx;
+    L->desc = D;
+    L->d = D.vector_size;
+    L->h = D.expert_hidden_size;
+    L->S = D.shared_experts;
+    L->E = D.routed_experts;
+    L->k = D.experts_per_token;
+    L->G = L->S + L->E;
+    L->dp = pad_k(L->d);
+    L->hp = pad_k(L->h);
+    L->balance_host.assign(L->E, 0.0);
+    L->uploaded.assign(1 + 3 * L->G, 0);
+    int32_t rc = GTMOE_OK;
+    if (rc == GTMOE_OK) rc = alloc_matrix(ctx, L->gate, D.precision, L->h, L->d, L->G);
+    if (rc == GTMOE_OK) rc = alloc_matrix(ctx, L->up, D.precision, L->h, L->d, L->G);
+    if (rc == GTMOE_OK) rc = alloc_matrix(ctx, L->down, D.precision, L->d, L->h, L->G);
+    if (rc == GTMOE_OK) {
+        const size_t rw = (size_t)L->E * L->dp * sizeof(float);
+        if (hipMalloc(&L->router_w, rw) != hipSuccess || hipMemset(L->router_w, 0, rw) != hipSuccess ||
+            hipMalloc(&L->router_b, sizeof(double) * L->E) != hipSuccess ||
+            hipMemset(L->router_b, 0, sizeof(double) * L->E) != hipSuccess ||
+            hipMalloc(&L->balance, sizeof(double) * L->E) != hipSuccess ||
+            hipMemset(L->balance, 0, sizeof(double) * L->E) != hipSuccess ||
+            hipMalloc(&L->norm_w, sizeof(float) * L->d) != hipSuccess)
+            rc = fail(ctx, GTMOE_ERR_OUT_OF_MEMORY, "cannot allocate the router");
+    }
+    if (rc != GTMOE_OK) {
+        gtmoe_layer_destroy(L);
+        return rc;
+    }
+    *out = L;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_destroy(gtmoe_layer *L)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    free_matrix(L->gate);
+    free_matrix(L->up);
+    free_matrix(L->down);
+    if (L->router_w) (void)hipFree(L->router_w);
+    if (L->router_b) (void)hipFree(L->router_b);
+    if (L->balance) (void)hipFree(L->balance);
+    if (L->norm_w) (void)hipFree(L->norm_w);
+    if (L->ws.base) (void)hipFree(L->ws.base);
+    delete L;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_upload_rows(gtmoe_layer *L, int32_t role, int32_t index, const gtmoe_rows *rows, const double *biases)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (!biases) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "biases are null");
+    if (role < GTMOE_ROLE_ROUTER || role > GTMOE_ROLE_ROUTED_DOWN)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown role %d", role);
+
+    if (role == GTMOE_ROLE_ROUTER) {
+        int32_t rc = check_rows(ctx, rows, L->E, L->d);
+        if (rc != GTMOE_OK) return rc;
+        // the router runs in fp32: decode the rows and round to float
+        std::vector<float> w((size_t)L->E * L->dp, 0.f);
+        for (int r = 0; r < L->E; ++r)
+            for (int i = 0; i < L->d; ++i) w[(size_t)r * L->dp + i] = (float)decoded_value(rows, r, i);
+        HIP_TRY(ctx, hipMemcpy(L->router_w, w.data(), w.size() * sizeof(float), hipMemcpyHostToDevice));
+        HIP_TRY(ctx, hipMemcpy(L->router_b, biases, sizeof(double) * L->E, hipMemcpyHostToDevice));
+        L->uploaded[role_slot(L, role, 0)] = 1;
+        return GTMOE_OK;
+    }
+
+    const bool shared = role <= GTMOE_ROLE_SHARED_DOWN;
+    const int n = shared ? L->S : L->E;
+    if (index < 0 || index >= n)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "%s expert %d of %d", shared ? "shared" : "routed", index, n);
+    const int which = shared ? role - GTMOE_ROLE_SHARED_GATE : role - GTMOE_ROLE_ROUTED_GATE;
+    DeviceMatrix &m = which == 0 ? L->gate : which == 1 ? L->up : L->down;
+    int32_t rc = check_rows(ctx, rows, m.rows, m.width);
+    if (rc != GTMOE_OK) return rc;
+    if (rows->precision != m.precision)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "expert weights at precision %d, the layer holds %d",
+                    rows->precision, m.precision);
+    const int group = shared ? index : L->S + index;
+    // repack into padded device rows
+    std::vector<uint8_t> vals(m.group_value_bytes(), 0);
+    const int src_row_bytes = m.precision == kInt8 ? m.width : m.precision == kFP4 ? (m.width + 1) / 2 : m.width * 4;
+    for (int r = 0; r < m.rows; ++r)
+        memcpy(vals.data() + (size_t)r * m.row_bytes, (const uint8_t *)rows->values + (size_t)r * src_row_bytes,
+               (size_t)src_row_bytes);
+    HIP_TRY(ctx, hipMemcpy((char *)m.values + (size_t)group * m.group_value_bytes(), vals.data(), vals.size(),
+                           hipMemcpyHostToDevice));
+    if (m.precision != kFloat32) {
+        const int src_blocks = (m.width + 15) / 16;
+        std::vector<float> sc(m.group_scales(), 0.f);
+        for (int r = 0; r < m.rows; ++r)
+            memcpy(sc.data() + (size_t)r * m.nblocks, rows->scales + (size_t)r * src_blocks,
+                   sizeof(float) * src_blocks);
+        HIP_TRY(ctx, hipMemcpy(m.scales + (size_t)group * m.group_scales(), sc.data(), sc.size() * sizeof(float),
+                               hipMemcpyHostToDevice));
+    }
+    std::vector<float> b(m.rows);
+    for (int r = 0; r < m.rows; ++r) b[r] = (float)biases[r];
+    HIP_TRY(ctx, hipMemcpy(m.biases + (size_t)group * m.rows, b.data(), sizeof(float) * m.rows, hipMemcpyHostToDevice));
+    L->uploaded[role_slot(L, role, index)] = 1;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_set_balance_biases(gtmoe_layer *L, const double *biases)
+{
+    if (!L || !biases) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    L->balance_host.assign(biases, biases + L->E);
+    HIP_TRY(ctx, hipMemcpy(L->balance, biases, sizeof(double) * L->E, hipMemcpyHostToDevice));
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_get_balance_biases(const gtmoe_layer *L, double *biases)
+{
+    if (!L || !biases) return GTMOE_ERR_INVALID_ARGUMENT;
+    memcpy(biases, L->balance_host.data(), sizeof(double) * L->E);
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_set_norm_weights(gtmoe_layer *L, const double *weights)
+{
+    if (!L || !weights) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    std::vector<float> w(weights, weights + L->d);
+    HIP_TRY(ctx, hipMemcpy(L->norm_w, w.data(), sizeof(float) * L->d, hipMemcpyHostToDevice));
+    L->has_norm = true;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, const int64_t *token_ids,
+                      double *outputs, uint32_t flags)
+{
+    int32_t rc = check_layer_call(L);
+    if (rc != GTMOE_OK) return rc;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int T = tokens;
+    if (T < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "negative number of tokens");
+    if (T > 0 && (!inputs || !outputs)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "inputs or outputs are null");
+    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
+    if (L->desc.use_hash_routing) {
+        if (T > 0 && !token_ids)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: hash routing needs one token ID per row");
+        for (int t = 0; t < T; ++t)
+            if (token_ids[t] < 0)
+                return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: token ID %lld at row %d is negative",
+                            (long long)token_ids[t], t);
+    }
+    const int path = choose_path(L, T, flags);
+    if (path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
+    rc = ensure_workspace(L, T);
+    if (rc != GTMOE_OK) return rc;
+    hipStream_t s = ctx->stream;
+    if (T == 0) {
+        mark_forward(L, 0, path, s);
+        L->last_load.assign(L->E, 0);
+        L->load_on_host = true;
+        return GTMOE_OK;
+    }
+    Workspace &w = L->ws;
+    HIP_TRY(ctx, hipMemcpyAsync(w.x64, inputs, sizeof(double) * T * L->d, hipMemcpyHostToDevice, s));
+    if (L->desc.use_hash_routing)
+        HIP_TRY(ctx, hipMemcpyAsync(w.ids, token_ids, sizeof(int64_t) * T, hipMemcpyHostToDevice, s));
+    const bool need_f32 = path == GTMOE_PATH_FP32 || !L->desc.use_hash_routing;
+    RUN(ctx, s, "convert_inputs",
+        launch_convert_inputs_f64(w.x64, T, L->d, need_f32 ? w.xf : nullptr, L->dp,
+                                  path == GTMOE_PATH_BF16 ? w.xb : nullptr, L->dp, s));
+    rc = route_and_experts(L, T, w.ids, path, s);
+    if (rc != GTMOE_OK) return rc;
+    RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, nullptr, nullptr, w.y64, s));
+    HIP_TRY(ctx, hipMemcpyAsync(outputs, w.y64, sizeof(double) * T * L->d, hipMemcpyDeviceToHost, s));
+    L->last_load.assign(L->E, 0);
+    HIP_TRY(ctx, hipMemcpyAsync(L->last_load.data(), w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    mark_forward(L, T, path, s);
+    L->load_on_host = true;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs, const int64_t *token_ids,
+                             float *outputs, uint32_t flags, void *stream)
+{
+    int32_t rc = check_layer_call(L);
+    if (rc != GTMOE_OK) return rc;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int T = tokens;
+    if (T < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "negative number of tokens");
+    if (T > 0 && (!inputs || !outputs)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "inputs or outputs are null");
+    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
+    if (L->desc.use_hash_routing && T > 0 && !token_ids)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: hash routing needs one token ID per row");
+    const int path = choose_path(L, T, flags);
+    if (path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
+    rc = ensure_workspace(L, T);
+    if (rc != GTMOE_OK) return rc;
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    if (T == 0) {
+        mark_forward(L, 0, path, s);
+        return GTMOE_OK;
+    }
+    Workspace &w = L->ws;
+    const bool need_f32 = path == GTMOE_PATH_FP32 || !L->desc.use_hash_routing;
+    RUN(ctx, s, "convert_inputs",
+        launch_convert_inputs_f32(inputs, T, L->d, need_f32 ? w.xf : nullptr, L->dp,
+                                  path == GTMOE_PATH_BF16 ? w.xb : nullptr, L->dp, s));
+    rc = route_and_experts(L, T, token_ids, path, s);
+    if (rc != GTMOE_OK) return rc;
+    RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, nullptr, outputs, nullptr, s));
+    mark_forward(L, T, path, s);
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen, double *gates, int32_t *load,
+                           int32_t *rows_for_expert, int32_t *expert_offsets)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (L->last_T < 0) return fail(ctx, GTMOE_ERR_NOT_READY, "call Forward before reading its routing");
+    const int T = L->last_T;
+    if (tokens_out) *tokens_out = T;
+    if (T == 0) {
+        if (load) memset(load, 0, sizeof(int32_t) * L->E);
+        if (expert_offsets) memset(expert_offsets, 0, sizeof(int32_t) * (L->E + 1));
+        return GTMOE_OK;
+    }
+    HIP_TRY(ctx, hipStreamSynchronize(L->last_stream));
+    const size_t tk = (size_t)T * L->k;
+    Workspace &w = L->ws;
+    if (chosen) HIP_TRY(ctx, hipMemcpy(chosen, w.chosen, tk * 4, hipMemcpyDeviceToHost));
+    if (gates) HIP_TRY(ctx, hipMemcpy(gates, w.gates, tk * 8, hipMemcpyDeviceToHost));
+    if (load) HIP_TRY(ctx, hipMemcpy(load, w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost));
+    if (rows_for_expert) HIP_TRY(ctx, hipMemcpy(rows_for_expert, w.rows, tk * 4, hipMemcpyDeviceToHost));
+    if (expert_offsets)
+        HIP_TRY(ctx, hipMemcpy(expert_offsets, w.offsets, sizeof(int32_t) * (L->E + 1), hipMemcpyDeviceToHost));
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_last_expert_load(gtmoe_layer *L, int32_t *load)
+{
+    if (!L || !load) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(L->ctx->mu);
+    HIP_TRY(L->ctx, hipSetDevice(L->ctx->device));
+    int32_t rc = fetch_load(L);
+    if (rc != GTMOE_OK) return rc;
+    memcpy(load, L->last_load.data(), sizeof(int32_t) * L->E);
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_update_balance(gtmoe_layer *L, double rate)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    // mixtureofexperts.go:293-310
+    if (L->last_T < 0 || L->desc.use_hash_routing) return GTMOE_OK;
+    int32_t rc = fetch_load(L);
+    if (rc != GTMOE_OK) return rc;
+    long long total = 0;
+    for (int e = 0; e < L->E; ++e) total += L->last_load[e];
+    const double average = (double)total / (double)L->E;
+    for (int e = 0; e < L->E; ++e) {
+        if ((double)L->last_load[e] < average) L->balance_host[e] += rate;
+        if ((double)L->last_load[e] > average) L->balance_host[e] -= rate;
+    }
+    HIP_TRY(ctx, hipMemcpy(L->balance, L->balance_host.data(), sizeof(double) * L->E, hipMemcpyHostToDevice));
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_route_from_logits(gtmoe_layer *L, int32_t tokens, const double *logits, int32_t *chosen, double *gates,
+                                int32_t *load, int32_t *rows_for_expert, int32_t *expert_offsets)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int T = tokens;
+    if (T < 0 || (T > 0 && !logits)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "bad logits");
+    int32_t rc = ensure_workspace(L, T);
+    if (rc != GTMOE_OK) return rc;
+    hipStream_t s = ctx->stream;
+    Workspace &w = L->ws;
+    if (T > 0) {
+        HIP_TRY(ctx, hipMemcpyAsync(w.logits, logits, sizeof(double) * T * L->E, hipMemcpyHostToDevice, s));
+        RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
+    }
+    RUN(ctx, s, "dispatch",
+        launch_dispatch(w.chosen, T, L->k, L->E, L->S, mfma_tile_m(), w.load, w.offsets, w.rows, w.pos, w.goff,
+                        w.tok, w.tile_off, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    mark_forward(L, T, L->last_path, s);
+    return gtmoe_last_routing(L, nullptr, chosen, gates, load, rows_for_expert, expert_offsets);
+}
+
+static int32_t stack_common(gtmoe_layer *const *layers, int32_t n_layers, int32_t T, gtmoe_context **ctx_out)
+{
+    if (!layers || n_layers < 1 || T < 0) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = layers[0] ? layers[0]->ctx : nullptr;
+    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    for (int l = 0; l < n_layers; ++l) {
+        if (!layers[l] || layers[l]->ctx != ctx || layers[l]->d != layers[0]->d)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "stack layer %d differs in context or vector size", l);
+        int32_t rc = check_layer_call(layers[l]);
+        if (rc != GTMOE_OK) return rc;
+        if (!layers[l]->has_norm) return fail(ctx, GTMOE_ERR_NOT_READY, "stack layer %d has no norm weights", l);
+    }
+    *ctx_out = ctx;
+    return GTMOE_OK;
+}
+
+// x <- x + MoE_l(RMSNorm_l(x)) over device fp32 x (T x d) on stream s.
+static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T, float *x, const int64_t *ids,
+                         uint32_t flags, hipStream_t s)
+{
+    gtmoe_context *ctx = layers[0]->ctx;
+    for (int l = 0; l < n_layers; ++l) {
+        gtmoe_layer *L = layers[l];
+        const int path = choose_path(L, T, flags);
+        if (path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
+            return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
+        int32_t rc = ensure_workspace(L, T);
+        if (rc != GTMOE_OK) return rc;
+        if (T == 0) {
+            mark_forward(L, 0, path, s);
+            continue;
+        }
+        Workspace &w = L->ws;
+        const bool need_f32 = path == GTMOE_PATH_FP32 || !L->desc.use_hash_routing;
+        RUN(ctx, s, "rmsnorm",
+            launch_rmsnorm(x, T, L->d, L->norm_w, need_f32 ? w.xf : nullptr, L->dp,
+                           path == GTMOE_PATH_BF16 ? w.xb : nullptr, L->dp, s));
+        rc = route_and_experts(L, T, ids, path, s);
+        if (rc != GTMOE_OK) return rc;
+        RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, x, x, nullptr, s));
+        mark_forward(L, T, path, s);
+    }
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, double *x,
+                            const int64_t *token_ids, uint32_t flags, int32_t *chosen, double *gates)
+{
+    gtmoe_context *ctx = nullptr;
+    int32_t rc = stack_common(layers, n_layers, tokens, &ctx);
+    if (rc != GTMOE_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int T = tokens;
+    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
+    if (T > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
+    const bool hashed = [&] {
+        for (int l = 0; l < n_layers; ++l)
+            if (layers[l]->desc.use_hash_routing) return true;
+        return false;
+    }();
+    if (hashed && T > 0) {
+        if (!token_ids) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "hash routing needs one token ID per row");
+        for (int t = 0; t < T; ++t)
+            if (token_ids[t] < 0)
+                return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "token ID %lld at row %d is negative",
+                            (long long)token_ids[t], t);
+    }
+    gtmoe_layer *L0 = layers[0];
+    rc = ensure_workspace(L0, T);
+    if (rc != GTMOE_OK) return rc;
+    hipStream_t s = ctx->stream;
+    Workspace &w0 = L0->ws;
+    if (T > 0) {
+        HIP_TRY(ctx, hipMemcpyAsync(w0.x64, x, sizeof(double) * T * L0->d, hipMemcpyHostToDevice, s));
+        if (hashed) HIP_TRY(ctx, hipMemcpyAsync(w0.ids, token_ids, sizeof(int64_t) * T, hipMemcpyHostToDevice, s));
+        RUN(ctx, s, "convert_inputs", launch_convert_inputs_f64(w0.x64, T, L0->d, w0.xs, L0->d, nullptr, 0, s));
+    }
+    rc = stack_run(layers, n_layers, T, w0.xs, w0.ids, flags, s);
+    if (rc != GTMOE_OK) return rc;
+    if (T > 0) {
+        RUN(ctx, s, "to_f64", launch_f32_to_f64(w0.xs, w0.y64, (long long)T * L0->d, s));
+        HIP_TRY(ctx, hipMemcpyAsync(x, w0.y64, sizeof(double) * T * L0->d, hipMemcpyDeviceToHost, s));
+        const size_t tk = (size_t)T * L0->k;
+        for (int l = 0; l < n_layers; ++l) {
+            Workspace &w = layers[l]->ws;
+            if (chosen)
+                HIP_TRY(ctx, hipMemcpyAsync(chosen + (size_t)l * tk, w.chosen, tk * 4, hipMemcpyDeviceToHost, s));
+            if (gates)
+                HIP_TRY(ctx, hipMemcpyAsync(gates + (size_t)l * tk, w.gates, tk * 8, hipMemcpyDeviceToHost, s));
+        }
+    }
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, float *x,
+                                   const int64_t *token_ids, uint32_t flags, void *stream)
+{
+    gtmoe_context *ctx = nullptr;
+    int32_t rc = stack_common(layers, n_layers, tokens, &ctx);
+    if (rc != GTMOE_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
+    if (tokens > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
+    for (int l = 0; l < n_layers; ++l)
+        if (layers[l]->desc.use_hash_routing && tokens > 0 && !token_ids)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "hash routing needs one token ID per row");
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return stack_run(layers, n_layers, tokens, x, token_ids, flags, s);
+}
+
+int32_t gtmoe_timing_enable(gtmoe_context *ctx, int32_t enabled)
+{
+    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    ctx->timing = enabled != 0;
+    return GTMOE_OK;
+}
+
+static int32_t collect_timing(gtmoe_context *ctx)
+{
+    if (ctx->pending.empty()) return GTMOE_OK;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    HIP_TRY(ctx, hipDeviceSynchronize());
+    for (auto &r : ctx->pending) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
+            auto &slot = ctx->totals[r.name];
+            slot.first += ms;
+            slot.second += 1;
+        }
+        ctx->spare_events.push_back(r.start);
+        ctx->spare_events.push_back(r.stop);
+    }
+    ctx->pending.clear();
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_timing_reset(gtmoe_context *ctx)
+{
+    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    int32_t rc = collect_timing(ctx);
+    ctx->totals.clear();
+    return rc;
+}
+
+int32_t gtmoe_timing_read(gtmoe_context *ctx, int32_t capacity, char *names, double *total_ms, int32_t *launches,
+                          int32_t *count)
+{
+    if (!ctx || !count) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    int32_t rc = collect_timing(ctx);
+    if (rc != GTMOE_OK) return rc;
+    int i = 0;
+    for (auto &kv : ctx->totals) {
+        if (i < capacity) {
+            if (names) {
+                strncpy(names + 64 * i, kv.first.c_str(), 63);
+                names[64 * i + 63] = 0;
+            }
+            if (total_ms) total_ms[i] = kv.second.first;
+            if (launches) launches[i] = kv.second.second;
+        }
+        ++i;
+    }
+    *count = i;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_last_path(const gtmoe_layer *L, int32_t *path)
+{
+    if (!L || !path) return GTMOE_ERR_INVALID_ARGUMENT;
+    *path = L->last_path;
+    return GTMOE_OK;
+}
+
+}  // extern "C"

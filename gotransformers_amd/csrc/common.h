@@ -1,0 +1,123 @@
+// Shared declarations of the gfx950 kernels and their host-side launchers.
+//
+// Device data layout (all of one layer resident in HBM):
+//   expert weights of one role (gate, up or down) for all G = S + E groups
+//   (shared experts first, then routed experts) in one allocation:
+//     values [G][rows][row_bytes]   rows padded to kp = ceil(width/64)*64
+//                                   values with zeros: int8 kp bytes, FP4
+//                                   kp/2 bytes (even index in the low
+//                                   nibble), float32 4*kp bytes
+//     scales [G][rows][kp/16]       float32 per 16 values (Int8, FP4)
+//     biases [G][rows]              float32
+//   activations are fp32 (or bf16 for the MFMA path) with a row stride of
+//   ceil(d/64)*64 resp. ceil(h/64)*64, padding columns zero.
+//
+// "Positions" number the rows the experts work on: P = T*(S+k).  Positions
+// [s*T, (s+1)*T) belong to shared expert s (token = position - s*T);
+// positions S*T + q for q in [0, T*k) hold the routed (token, slot) pairs in
+// dispatch order (experts ascending, tokens ascending inside an expert).
+// goff[G+1] holds the first position of every group.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gtmoe {
+
+enum Precision { kFloat64 = 0, kFloat32 = 1, kInt8 = 2, kFP4 = 3 };
+
+constexpr int kValuesPerScale = 16;
+constexpr int kPadK = 64;
+
+inline int pad_k(int width) { return (width + kPadK - 1) / kPadK * kPadK; }
+
+// One weight role of all groups on the device.
+struct DeviceMatrix {
+    int precision = 0;
+    int rows = 0;       // output neurons
+    int width = 0;      // inputs (unpadded)
+    int kp = 0;         // padded inputs
+    int row_bytes = 0;  // bytes per padded row
+    int nblocks = 0;    // kp / 16
+    int groups = 0;
+    void *values = nullptr;
+    float *scales = nullptr;
+    float *biases = nullptr;
+    size_t group_value_bytes() const { return (size_t)rows * row_bytes; }
+    size_t group_scales() const { return (size_t)rows * nblocks; }
+};
+
+// Arguments of the expert GEMV kernels (fp32 path).
+struct GemvArgs {
+    const void *w0;
+    const float *s0;
+    const float *b0;
+    const void *w1;  // up (gate/up kernel only)
+    const float *s1;
+    const float *b1;
+    long long w_group_stride;  // bytes
+    long long s_group_stride;  // floats
+    int rows;
+    int nblocks;
+    int row_bytes;
+    const float *in;
+    int ld_in;
+    const int32_t *tok;  // gate/up: token of every position; down: nullptr
+    const int32_t *goff;
+    float *out;
+    int ld_out;
+    float clamp;
+};
+
+// Arguments of the grouped MFMA GEMM kernels (bf16 path).
+struct MfmaArgs {
+    const void *w0;
+    const float *s0;
+    const float *b0;
+    const void *w1;
+    const float *s1;
+    const float *b1;
+    long long w_group_stride;
+    long long s_group_stride;
+    int n;          // output rows of the weight matrix
+    int kp;         // padded K
+    int row_bytes;
+    int nblocks;
+    const uint16_t *a;  // bf16 activations
+    int lda;
+    const int32_t *tok;  // gate/up: gather by token; down: nullptr
+    const int32_t *goff;
+    const int32_t *tile_off;  // [G+1] exclusive prefix of m-tiles per group
+    int groups;
+    void *out;  // gate/up: bf16 hidden; down: fp32 slot outputs
+    int ldo;
+    float clamp;
+};
+
+// Launchers (each returns the hipError_t of its launch).
+hipError_t launch_convert_inputs_f64(const double *x, int T, int d, float *xf, int ldf, uint16_t *xb, int ldb,
+                                     hipStream_t s);
+hipError_t launch_convert_inputs_f32(const float *x, int T, int d, float *xf, int ldf, uint16_t *xb, int ldb,
+                                     hipStream_t s);
+hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *xf, int ldf, uint16_t *xb, int ldb,
+                          hipStream_t s);
+hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
+                         double *logits, hipStream_t s);
+hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
+                       double *gates, float *gates32, hipStream_t s);
+hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,
+                             float *gates32, hipStream_t s);
+hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
+                           int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
+                           int32_t *tile_off, hipStream_t s);
+hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int groups, hipStream_t s);
+hipError_t launch_gemv_down(const GemvArgs &a, int precision, int groups, hipStream_t s);
+hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
+hipError_t launch_mfma_down(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
+int mfma_tile_m();
+hipError_t launch_combine(int T, int d, int S, int k, const float *slot_out, const int32_t *pos,
+                          const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s);
+hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s);
+hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);
+
+}  // namespace gtmoe

@@ -1,0 +1,308 @@
+// fp32 expert kernels for few tokens per expert (decode): a dequantizing
+// GEMV that streams each weight row from HBM once per group of tokens.
+//
+// Work split: grid (ceil(rows/16), groups); every wave owns 4 consecutive
+// output rows of one group (expert).  A row's K values are covered by the 64
+// lanes in 16-value blocks -- lane l takes blocks l, l+64, ... -- so each
+// load instruction of a wave reads one contiguous run of the row (1 KiB of
+// Int8, 512 B of FP4), coalesced, together with the matching fp32 scales.
+// Per block the lane forms the 16-term partial sum of every token it holds,
+// scales it once (the reference's DotRow order, lowprecision/rows.go:
+// 207-257), and accumulates.  The per-lane partials of all (row, matrix,
+// token) values are then summed across the wave by a transposing butterfly
+// that halves the live values at every exchange.
+//
+// Gate/up fuse the SwiGLU epilogue (feedforward/gatedfeedforward.go:49-57):
+// hidden = act_g(gate + b_g) * act_u(up + b_u).  Down adds its bias.
+#include "common.h"
+
+namespace gtmoe {
+
+namespace {
+
+template <int PREC>
+struct RawBlock;
+template <>
+struct RawBlock<kInt8> {
+    uint4 v;
+};
+template <>
+struct RawBlock<kFP4> {
+    uint2 v;
+};
+template <>
+struct RawBlock<kFloat32> {
+    float4 v[4];
+};
+
+template <int PREC>
+__device__ __forceinline__ void load_raw(RawBlock<PREC> &r, const char *row, int b);
+template <>
+__device__ __forceinline__ void load_raw<kInt8>(RawBlock<kInt8> &r, const char *row, int b)
+{
+    r.v = *reinterpret_cast<const uint4 *>(row + (size_t)b * 16);
+}
+template <>
+__device__ __forceinline__ void load_raw<kFP4>(RawBlock<kFP4> &r, const char *row, int b)
+{
+    r.v = *reinterpret_cast<const uint2 *>(row + (size_t)b * 8);
+}
+template <>
+__device__ __forceinline__ void load_raw<kFloat32>(RawBlock<kFloat32> &r, const char *row, int b)
+{
+    const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+}
+
+template <int PREC>
+__device__ __forceinline__ void zero_raw(RawBlock<PREC> &r)
+{
+    r = RawBlock<PREC>{};
+}
+
+// Codes of one block as floats (Int8 values, FP4 magnitudes with sign, or
+// the float32 weights themselves); the scale is applied by the caller.
+__device__ __forceinline__ void decode(const RawBlock<kInt8> &r, float (&w)[16])
+{
+    const uint32_t d[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[4 * i + j] = (float)(int)(int8_t)(d[i] >> (8 * j));
+}
+__device__ __forceinline__ void decode(const RawBlock<kFP4> &r, float (&w)[16])
+{
+    // e2m1 codes, even value in the low nibble; the hardware conversion
+    // with scale 1.0 yields exactly {0, .5, 1, 1.5, 2, 3, 4, 6} with sign.
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t d[2] = {r.v.x, r.v.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 0);
+        const f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 1);
+        const f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 2);
+        const f32x2 f3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 3);
+        w[8 * i + 0] = f0[0];
+        w[8 * i + 1] = f0[1];
+        w[8 * i + 2] = f1[0];
+        w[8 * i + 3] = f1[1];
+        w[8 * i + 4] = f2[0];
+        w[8 * i + 5] = f2[1];
+        w[8 * i + 6] = f3[0];
+        w[8 * i + 7] = f3[1];
+    }
+}
+__device__ __forceinline__ void decode(const RawBlock<kFloat32> &r, float (&w)[16])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w[4 * i + 0] = r.v[i].x;
+        w[4 * i + 1] = r.v[i].y;
+        w[4 * i + 2] = r.v[i].z;
+        w[4 * i + 3] = r.v[i].w;
+    }
+}
+
+// Sum N per-lane values over the 64 lanes of a wave.  Afterwards lane l
+// holds in v[0] the total of value index l / (64 / N).
+template <int N>
+__device__ __forceinline__ void wave_transpose_reduce(float (&v)[N], int lane)
+{
+    int off = 32;
+#pragma unroll
+    for (int half = N / 2; half >= 1; half /= 2) {
+        const bool upper = (lane & off) != 0;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = upper ? v[i] : v[i + half];
+            const float keep = upper ? v[i + half] : v[i];
+            v[i] = keep + __shfl_xor(send, off);
+        }
+        off >>= 1;
+    }
+    for (; off > 0; off >>= 1) v[0] += __shfl_xor(v[0], off);
+}
+
+template <int N>
+struct Log2 {
+    static constexpr int value = 1 + Log2<N / 2>::value;
+};
+template <>
+struct Log2<1> {
+    static constexpr int value = 0;
+};
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+}  // namespace
+
+// TC tokens of a group are held in registers at a time; RIF rows (of each
+// matrix) have their weight blocks in flight together.
+template <int PREC, int NB, int TC, int RIF, bool GATEUP>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
+{
+    constexpr int RPW = 4;
+    constexpr int MATS = GATEUP ? 2 : 1;
+    constexpr int NV = RIF * MATS * TC;  // values reduced per exchange round
+    constexpr int SHIFT = 6 - Log2<NV>::value;
+    static_assert(NV <= 64, "too many values per lane");
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = blockIdx.y;
+    const int p0 = a.goff[g];
+    const int M = a.goff[g + 1] - p0;
+    if (M <= 0) return;
+    const int r0 = (blockIdx.x * 4 + wave) * RPW;
+    if (r0 >= a.rows) return;
+
+    const char *wb0 = reinterpret_cast<const char *>(a.w0) + (size_t)g * a.w_group_stride;
+    const char *wb1 = GATEUP ? reinterpret_cast<const char *>(a.w1) + (size_t)g * a.w_group_stride : nullptr;
+    const float *sb0 = a.s0 + (size_t)g * a.s_group_stride;
+    const float *sb1 = GATEUP ? a.s1 + (size_t)g * a.s_group_stride : nullptr;
+    const float *bb0 = a.b0 + (size_t)g * a.rows;
+    const float *bb1 = GATEUP ? a.b1 + (size_t)g * a.rows : nullptr;
+
+    for (int c0 = 0; c0 < M; c0 += TC) {
+        float xr[TC][NB][16];
+#pragma unroll
+        for (int c = 0; c < TC; ++c) {
+            const int m = c0 + c;
+            const int src = (m < M) ? (GATEUP ? a.tok[p0 + m] : p0 + m) : 0;
+            const float *xrow = a.in + (size_t)src * a.ld_in;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int b = lane + 64 * j;
+                if (m < M && b < a.nblocks) {
+                    const float4 *p = reinterpret_cast<const float4 *>(xrow + (size_t)b * 16);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v = p[q];
+                        xr[c][j][4 * q + 0] = v.x;
+                        xr[c][j][4 * q + 1] = v.y;
+                        xr[c][j][4 * q + 2] = v.z;
+                        xr[c][j][4 * q + 3] = v.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) xr[c][j][q] = 0.f;
+                }
+            }
+        }
+
+#pragma unroll 1
+        for (int rr0 = 0; rr0 < RPW; rr0 += RIF) {
+            RawBlock<PREC> raw[RIF][MATS][NB];
+            float sc[RIF][MATS][NB];
+#pragma unroll
+            for (int rr = 0; rr < RIF; ++rr) {
+                const int r = r0 + rr0 + rr;
+#pragma unroll
+                for (int mt = 0; mt < MATS; ++mt) {
+                    const char *row = (mt == 0 ? wb0 : wb1) + (size_t)r * a.row_bytes;
+                    const float *srow = (mt == 0 ? sb0 : sb1) + (size_t)r * a.nblocks;
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        const int b = lane + 64 * j;
+                        if (r < a.rows && b < a.nblocks) {
+                            load_raw<PREC>(raw[rr][mt][j], row, b);
+                            sc[rr][mt][j] = (PREC == kFloat32) ? 1.0f : srow[b];
+                        } else {
+                            zero_raw<PREC>(raw[rr][mt][j]);
+                            sc[rr][mt][j] = 0.f;
+                        }
+                    }
+                }
+            }
+            float part[NV];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) part[i] = 0.f;
+#pragma unroll
+            for (int rr = 0; rr < RIF; ++rr)
+#pragma unroll
+                for (int mt = 0; mt < MATS; ++mt)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        float w[16];
+                        decode(raw[rr][mt][j], w);
+#pragma unroll
+                        for (int c = 0; c < TC; ++c) {
+                            float bs = 0.f;
+#pragma unroll
+                            for (int q = 0; q < 16; ++q) bs = fmaf(xr[c][j][q], w[q], bs);
+                            float &acc = part[(rr * MATS + mt) * TC + c];
+                            acc = fmaf(bs, sc[rr][mt][j], acc);
+                        }
+                    }
+            wave_transpose_reduce<NV>(part, lane);
+            const int v = lane >> SHIFT;
+            const bool writer = (lane & ((1 << SHIFT) - 1)) == 0;
+            const int c = v % TC;
+            const int m = c0 + c;
+            if (GATEUP) {
+                const float other = __shfl_xor(part[0], TC << SHIFT);
+                const int mt = (v / TC) % 2;
+                const int rr = v / (2 * TC);
+                const int r = r0 + rr0 + rr;
+                if (writer && mt == 0 && m < M && r < a.rows) {
+                    float gv = part[0] + bb0[r];
+                    float uv = other + bb1[r];
+                    if (a.clamp > 0.f) {
+                        gv = fminf(gv, a.clamp);                 // ClampedSiLU: x > L -> silu(L)
+                        uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
+                    }
+                    a.out[(size_t)(p0 + m) * a.ld_out + r] = silu(gv) * uv;
+                }
+            } else {
+                const int rr = v / TC;
+                const int r = r0 + rr0 + rr;
+                if (writer && m < M && r < a.rows) a.out[(size_t)(p0 + m) * a.ld_out + r] = part[0] + bb0[r];
+            }
+        }
+    }
+}
+
+namespace {
+
+template <bool GATEUP, int PREC>
+hipError_t launch_prec(const GemvArgs &a, int groups, hipStream_t s)
+{
+    const int nb = (a.nblocks + 63) / 64;
+    dim3 grid((a.rows + 15) / 16, groups);
+    constexpr int R = (PREC == kFloat32) ? 1 : 0;  // float32 rows are 4x wider: one row in flight
+    if (nb <= 1)
+        hipLaunchKernelGGL((gemv_kernel<PREC, 1, 4, R ? 1 : 4, GATEUP>), grid, dim3(256), 0, s, a);
+    else if (nb <= 2)
+        hipLaunchKernelGGL((gemv_kernel<PREC, 2, 2, R ? 1 : 2, GATEUP>), grid, dim3(256), 0, s, a);
+    else if (nb <= 4)
+        hipLaunchKernelGGL((gemv_kernel<PREC, 4, 1, 1, GATEUP>), grid, dim3(256), 0, s, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+template <bool GATEUP>
+hipError_t launch_any(const GemvArgs &a, int precision, int groups, hipStream_t s)
+{
+    if (groups <= 0) return hipSuccess;
+    switch (precision) {
+    case kInt8: return launch_prec<GATEUP, kInt8>(a, groups, s);
+    case kFP4: return launch_prec<GATEUP, kFP4>(a, groups, s);
+    case kFloat32: return launch_prec<GATEUP, kFloat32>(a, groups, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int groups, hipStream_t s)
+{
+    return launch_any<true>(a, precision, groups, s);
+}
+
+hipError_t launch_gemv_down(const GemvArgs &a, int precision, int groups, hipStream_t s)
+{
+    return launch_any<false>(a, precision, groups, s);
+}
+
+}  // namespace gtmoe

@@ -1,0 +1,481 @@
+// Routing kernels: fp32 router logits, float64 affinity / top-k / gates with
+// the reference's tie-break, hash routing, and the stable dispatch.
+//
+// Built with -ffp-contract=off: the affinity and gate arithmetic must round
+// exactly like the float64 CPU restatement (mixtureofexperts.go:153-173), so
+// nothing here may be fused unless written as an explicit fmaf.
+#include "common.h"
+
+#include <math.h>
+
+namespace gtmoe {
+
+// ---------------------------------------------------------------------------
+// float64 exp / log1p, the fdlibm methods that Go's portable math.Exp and
+// math.Log1p follow (activationfunction.Softplus calls them,
+// moreactivationfunctions.go:8-16).  Same operation sequence as the CPU
+// restatement, so results agree to the bit.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double bits_f64(unsigned long long u) { return __longlong_as_double((long long)u); }
+
+__device__ double go_exp(double x)
+{
+    const double ln2_hi = bits_f64(0x3fe62e42fee00000ULL);
+    const double ln2_lo = bits_f64(0x3dea39ef35793c76ULL);
+    const double log2e = bits_f64(0x3ff71547652b82feULL);
+    const double overflow = 7.09782712893383973096e+02;
+    const double underflow = -7.45133219101941108420e+02;
+    const double near_zero = 1.0 / (double)(1 << 28);
+    const double p1 = bits_f64(0x3fc5555555555555ULL);
+    const double p2 = bits_f64(0xbf66c16c16bebd93ULL);
+    const double p3 = bits_f64(0x3f11566aaf25de2cULL);
+    const double p4 = bits_f64(0xbebbbd41c5d26bf1ULL);
+    const double p5 = bits_f64(0x3e66376972bea4d0ULL);
+
+    if (isnan(x) || (isinf(x) && x > 0)) return x;
+    if (isinf(x)) return 0;
+    if (x > overflow) return INFINITY;
+    if (x < underflow) return 0;
+    if (-near_zero < x && x < near_zero) return 1 + x;
+
+    int k = 0;
+    if (x < 0) k = (int)(log2e * x - 0.5);
+    else if (x > 0) k = (int)(log2e * x + 0.5);
+    double hi = x - (double)k * ln2_hi;
+    double lo = (double)k * ln2_lo;
+    double r = hi - lo;
+    double t = r * r;
+    double c = r - t * (p1 + t * (p2 + t * (p3 + t * (p4 + t * p5))));
+    double y = 1 - ((lo - (r * c) / (2 - c)) - hi);
+    return ldexp(y, k);
+}
+
+__device__ double go_log1p(double x)
+{
+    const double sqrt2m1 = bits_f64(0x3fda827999fcef34ULL);
+    const double sqrt2halfm1 = bits_f64(0xbfd2bec333018866ULL);
+    const double small = 1.0 / (double)(1 << 29);
+    const double tiny = 1.0 / (double)(1ULL << 54);
+    const double two53 = (double)(1ULL << 53);
+    const double ln2_hi = bits_f64(0x3fe62e42fee00000ULL);
+    const double ln2_lo = bits_f64(0x3dea39ef35793c76ULL);
+    const double lp1 = bits_f64(0x3fe5555555555593ULL);
+    const double lp2 = bits_f64(0x3fd999999997fa04ULL);
+    const double lp3 = bits_f64(0x3fd2492494229359ULL);
+    const double lp4 = bits_f64(0x3fcc71c51d8e78afULL);
+    const double lp5 = bits_f64(0x3fc7466496cb03deULL);
+    const double lp6 = bits_f64(0x3fc39a09d078c69fULL);
+    const double lp7 = bits_f64(0x3fc2f112df3e5244ULL);
+
+    if (x < -1 || isnan(x)) return NAN;
+    if (x == -1) return -INFINITY;
+    if (isinf(x)) return INFINITY;
+
+    double absx = fabs(x);
+    double f = 0;
+    unsigned long long iu = 0;
+    int k = 1;
+    if (absx < sqrt2m1) {
+        if (absx < small) {
+            if (absx < tiny) return x;
+            return x - x * x * 0.5;
+        }
+        if (x > sqrt2halfm1) {
+            k = 0;
+            f = x;
+            iu = 1;
+        }
+    }
+    double c = 0;
+    if (k != 0) {
+        double u;
+        if (absx < two53) {
+            u = 1.0 + x;
+            iu = (unsigned long long)__double_as_longlong(u);
+            k = (int)((iu >> 52) - 1023);
+            if (k > 0) c = 1.0 - (u - x);
+            else c = x - (u - 1.0);
+            c /= u;
+        } else {
+            u = x;
+            iu = (unsigned long long)__double_as_longlong(u);
+            k = (int)((iu >> 52) - 1023);
+            c = 0;
+        }
+        iu &= 0x000fffffffffffffULL;
+        if (iu < 0x0006a09e667f3bcdULL) {
+            u = bits_f64(iu | 0x3ff0000000000000ULL);
+        } else {
+            k++;
+            u = bits_f64(iu | 0x3fe0000000000000ULL);
+            iu = (0x0010000000000000ULL - iu) >> 2;
+        }
+        f = u - 1.0;
+    }
+    double hfsq = 0.5 * f * f;
+    double s, r, z;
+    if (iu == 0) {
+        if (f == 0) {
+            if (k == 0) return 0;
+            c += (double)k * ln2_lo;
+            return (double)k * ln2_hi + c;
+        }
+        r = hfsq * (1.0 - 0.66666666666666666 * f);
+        if (k == 0) return f - r;
+        return (double)k * ln2_hi - ((r - ((double)k * ln2_lo + c)) - f);
+    }
+    s = f / (2.0 + f);
+    z = s * s;
+    r = z * (lp1 + z * (lp2 + z * (lp3 + z * (lp4 + z * (lp5 + z * (lp6 + z * lp7))))));
+    if (k == 0) return f - (hfsq - s * (hfsq + r));
+    return (double)k * ln2_hi - ((hfsq - (s * (hfsq + r) + ((double)k * ln2_lo + c))) - f);
+}
+
+// affinity = sqrt(softplus(logit)) (mixtureofexperts.go:80-82)
+__device__ double affinity(double logit)
+{
+    double sp;
+    if (logit > 20) sp = logit;
+    else if (logit < -20) sp = go_exp(logit);
+    else sp = go_log1p(go_exp(logit));
+    return sqrt(sp);
+}
+
+// ---------------------------------------------------------------------------
+// Router logits: logits[t][e] = double(sum_i x[t][i] * w[e][i]) + bias[e].
+// ---------------------------------------------------------------------------
+
+// Few tokens: one workgroup per expert and 16 tokens; each wave owns four
+// tokens and reduces a full-width dot product across its 64 lanes.
+__global__ __launch_bounds__(256) void router_small_kernel(const float *__restrict__ x, int ldx, int T, int d,
+                                                           const float *__restrict__ w, int ldw,
+                                                           const double *__restrict__ bias, int E,
+                                                           double *__restrict__ logits)
+{
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float *wr = w + (size_t)e * ldw;
+    for (int tt = 0; tt < 4; ++tt) {
+        const int t = blockIdx.y * 16 + wave * 4 + tt;
+        if (t >= T) break;
+        const float *xr = x + (size_t)t * ldx;
+        float acc = 0.f;
+        for (int i = lane; i < d; i += 64) acc = fmaf(xr[i], wr[i], acc);
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (lane == 0) logits[(size_t)t * E + e] = (double)acc + bias[e];
+    }
+}
+
+// Many tokens: 64 tokens x 64 experts per workgroup, K staged through LDS in
+// steps of 32, 4x4 outputs per thread.
+__global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ x, int ldx, int T, int d,
+                                                           const float *__restrict__ w, int ldw,
+                                                           const double *__restrict__ bias, int E,
+                                                           double *__restrict__ logits)
+{
+    __shared__ float xs[32][65];
+    __shared__ float ws[32][65];
+    const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;  // 16 x 16 threads
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < d; k0 += 32) {
+        // 64 rows x 32 values of x and w: 2048 each, 8 per thread
+        for (int i = 0; i < 8; ++i) {
+            int idx = tid + i * 256;
+            int r = idx >> 5, c = idx & 31;
+            int t = t0 + r, e = e0 + r, kk = k0 + c;
+            xs[c][r] = (t < T && kk < d) ? x[(size_t)t * ldx + kk] : 0.f;
+            ws[c][r] = (e < E && kk < d) ? w[(size_t)e * ldw + kk] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < 32; ++kk) {
+            float xv[4], wv[4];
+            for (int i = 0; i < 4; ++i) xv[i] = xs[kk][ty + 16 * i];
+            for (int j = 0; j < 4; ++j) wv[j] = ws[kk][tx + 16 * j];
+            for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+    for (int i = 0; i < 4; ++i) {
+        int t = t0 + ty + 16 * i;
+        if (t >= T) continue;
+        for (int j = 0; j < 4; ++j) {
+            int e = e0 + tx + 16 * j;
+            if (e < E) logits[(size_t)t * E + e] = (double)acc[i][j] + bias[e];
+        }
+    }
+}
+
+hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
+                         double *logits, hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    if (T <= 256) {
+        dim3 grid(E, (T + 15) / 16);
+        hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, d, w, ldw, bias, E, logits);
+    } else {
+        dim3 grid((E + 63) / 64, (T + 63) / 64);
+        hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, x, ldx, T, d, w, ldw, bias, E, logits);
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Top-k: one wave per token.  Score = affinity + balance bias; the k best in
+// the order (score descending, expert ascending) -- exactly the first k of
+// the reference's sort.SliceStable (mixtureofexperts.go:98-112) -- then
+// listed in ascending expert order, gates = affinity / sum of the chosen
+// affinities summed in that order (:162-169).
+// ---------------------------------------------------------------------------
+constexpr int kMaxExperts = 256;
+constexpr int kMaxK = 8;
+
+__device__ __forceinline__ bool better(double s1, int e1, double s2, int e2)
+{
+    return s1 > s2 || (s1 == s2 && e1 < e2);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ logits, int T, int E, int k,
+                                                   const double *__restrict__ balance, int32_t *__restrict__ chosen,
+                                                   double *__restrict__ gates, float *__restrict__ gates32)
+{
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // wave-uniform
+    double a[EPL], sc[EPL];
+    bool taken[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        taken[j] = false;
+        if (e < E) {
+            a[j] = affinity(logits[(size_t)t * E + e]);
+            sc[j] = a[j] + balance[e];
+        } else {
+            a[j] = 0.0;
+            sc[j] = -INFINITY;
+        }
+    }
+    for (int r = 0; r < k; ++r) {
+        double bs = -INFINITY;
+        int be = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            if (e < E && !taken[j] && better(sc[j], e, bs, be)) {
+                bs = sc[j];
+                be = e;
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const double os = __shfl_xor(bs, off);
+            const int oe = __shfl_xor(be, off);
+            if (better(os, oe, bs, be)) {
+                bs = os;
+                be = oe;
+            }
+        }
+        if (be == 0x7fffffff) {
+            // Only NaN scores remain (NaN never compares better): take the
+            // lowest unchosen expert so the outputs stay in range.
+            int lowest = 0x7fffffff;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const int e = lane + 64 * j;
+                if (e < E && !taken[j] && e < lowest) lowest = e;
+            }
+            for (int off = 32; off > 0; off >>= 1) lowest = min(lowest, __shfl_xor(lowest, off));
+            be = lowest;
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; ++j)
+            if (lane + 64 * j == be) taken[j] = true;
+    }
+    // chosen experts in ascending order, with their affinities
+    int list_e[kMaxK];
+    double list_a[kMaxK];
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        unsigned long long m = __ballot(taken[j]);
+        while (m) {
+            const int b = __builtin_ctzll(m);
+            m &= m - 1;
+            const double av = __shfl(a[j], b);
+#pragma unroll
+            for (int i = 0; i < kMaxK; ++i)
+                if (i == n) {
+                    list_e[i] = 64 * j + b;
+                    list_a[i] = av;
+                }
+            ++n;
+        }
+    }
+    double total = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i)
+        if (i < k) total += list_a[i];
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i) {
+        if (i < k && lane == i) {
+            const double g = list_a[i] / total;
+            chosen[(size_t)t * k + i] = list_e[i];
+            gates[(size_t)t * k + i] = g;
+            gates32[(size_t)t * k + i] = (float)g;
+        }
+    }
+}
+
+hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
+                       double *gates, float *gates32, hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    dim3 grid((T + 3) / 4);
+    if (E <= 64)
+        hipLaunchKernelGGL(topk_kernel<1>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32);
+    else if (E <= 128)
+        hipLaunchKernelGGL(topk_kernel<2>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32);
+    else
+        hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32);
+    return hipGetLastError();
+}
+
+// hashedExperts (mixtureofexperts.go:88-96): first = (id*2654435761 + 12345)
+// mod E in unsigned 64-bit arithmetic, then k consecutive experts; gates 1/k.
+// Ids are checked non-negative by the host before launch.
+__global__ void hash_route_kernel(const int64_t *__restrict__ ids, int T, int E, int k, int32_t *__restrict__ chosen,
+                                  double *__restrict__ gates, float *__restrict__ gates32)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const unsigned long long first =
+        ((unsigned long long)ids[t] * 2654435761ULL + 12345ULL) % (unsigned long long)E;
+    const double g = 1 / (double)k;
+    for (int i = 0; i < k; ++i) {
+        chosen[(size_t)t * k + i] = (int32_t)((first + (unsigned long long)i) % (unsigned long long)E);
+        gates[(size_t)t * k + i] = g;
+        gates32[(size_t)t * k + i] = (float)g;
+    }
+}
+
+hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates, float *gates32,
+                             hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(hash_route_kernel, dim3((T + 255) / 256), dim3(256), 0, s, ids, T, E, k, chosen, gates,
+                       gates32);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch (mixtureofexperts.go:175-190): per-expert load, exclusive offsets,
+// and a stable permutation -- experts ascending, tokens ascending inside an
+// expert -- built by one workgroup.  Tokens go through in chunks of 1024 (one
+// per thread); the rank of a token inside its expert comes from wave ballots
+// and a per-expert prefix over the 16 waves, so no atomic decides an order.
+// Also fills the position tables the expert kernels use (goff, tok) and the
+// per-group MFMA tile prefix (tile_off).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ chosen, int T, int k, int E, int S,
+                                                        int bm, int32_t *__restrict__ load, int32_t *__restrict__ offsets,
+                                                        int32_t *__restrict__ rows, int32_t *__restrict__ pos,
+                                                        int32_t *__restrict__ goff, int32_t *__restrict__ tok,
+                                                        int32_t *__restrict__ tile_off)
+{
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int running[kMaxExperts];
+    __shared__ int wave_cnt[16][kMaxExperts];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = S + E;
+
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    for (long long i = tid; i < (long long)T * k; i += 1024) atomicAdd(&cnt[chosen[i]], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) {
+            running[e] = acc;
+            offsets[e] = acc;
+            load[e] = cnt[e];
+            acc += cnt[e];
+        }
+        offsets[E] = acc;
+        // groups: shared experts own T positions each, then the routed experts
+        int tiles = 0;
+        for (int g = 0; g < G; ++g) {
+            const int start = g < S ? g * T : S * T + running[g - S];
+            const int m = g < S ? T : cnt[g - S];
+            goff[g] = start;
+            tile_off[g] = tiles;
+            tiles += (m + bm - 1) / bm;
+        }
+        goff[G] = S * T + T * k;
+        tile_off[G] = tiles;
+    }
+    // shared-expert positions: token = position mod T
+    for (long long p = tid; p < (long long)S * T; p += 1024) tok[p] = (int32_t)(p % T);
+    __syncthreads();
+
+    for (int c0 = 0; c0 < T; c0 += 1024) {
+        const int t = c0 + tid;
+        const bool valid = t < T;
+        int ce[kMaxK];
+        int rk[kMaxK];
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i) {
+            ce[i] = (valid && i < k) ? chosen[(size_t)t * k + i] : -1;
+            rk[i] = 0;
+        }
+        for (int e = 0; e < E; ++e) {
+            int match = -1;
+#pragma unroll
+            for (int i = 0; i < kMaxK; ++i)
+                if (ce[i] == e) match = i;
+            const unsigned long long b = __ballot(match >= 0);
+            if (lane == 0) wave_cnt[wave][e] = __popcll(b);
+            const int r = __popcll(b & ((1ULL << lane) - 1ULL));
+#pragma unroll
+            for (int i = 0; i < kMaxK; ++i)
+                if (i == match) rk[i] = r;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += 1024) {
+            int acc = running[e];
+            for (int w = 0; w < 16; ++w) {
+                const int c = wave_cnt[w][e];
+                wave_cnt[w][e] = acc;
+                acc += c;
+            }
+            running[e] = acc;
+        }
+        __syncthreads();
+        if (valid) {
+#pragma unroll
+            for (int i = 0; i < kMaxK; ++i) {
+                if (i < k) {
+                    const int p = wave_cnt[wave][ce[i]] + rk[i];
+                    rows[p] = t;
+                    pos[(size_t)t * k + i] = p;
+                    tok[(size_t)S * T + p] = t;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load, int32_t *offsets,
+                           int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok, int32_t *tile_off,
+                           hipStream_t s)
+{
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows, pos,
+                       goff, tok, tile_off);
+    return hipGetLastError();
+}
+
+}  // namespace gtmoe

@@ -1,0 +1,226 @@
+/*
+ * gtmoe.h -- C ABI of libgtmoe, the MI355X (gfx950) implementation of
+ * GoTransformers' mixture-of-experts forward pass over lowprecision expert
+ * weights.
+ *
+ * The ABI is plain C: opaque handles, plain pointers and sizes, int32 status
+ * codes.  A CGO_ENABLED=0 Go host binds it with purego Dlopen/Dlsym/
+ * RegisterFunc, the way gpu/library_unix.go:19-33 and gpu/vulkan.go:443-519
+ * bind Vulkan.  Every call that takes host buffers copies what it needs and
+ * blocks until its results are back in host memory (the contract of
+ * gpu/device.go:636-654).  Calls on one context are serialised by a mutex
+ * (gpu/device.go:40); a layer must not be used from two threads at once,
+ * just as mixtureofexperts.MixtureOfExperts has no lock.
+ *
+ * Status codes: 0 is success.  On failure the call returns a non-zero code
+ * and gtmoe_last_error() describes it; the Go side then answers on the CPU
+ * and records the error, as gpu/device.go:723-739 does for Vulkan.
+ */
+#ifndef GTMOE_H
+#define GTMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GTMOE_ABI_VERSION 1
+
+enum gtmoe_status {
+    GTMOE_OK = 0,
+    GTMOE_ERR_INVALID_ARGUMENT = 1, /* the reference would panic */
+    GTMOE_ERR_UNSUPPORTED = 2,      /* valid for the reference, not offered on the GPU */
+    GTMOE_ERR_DEVICE = 3,           /* a HIP call failed */
+    GTMOE_ERR_NOT_READY = 4,        /* weights missing, or no Forward yet */
+    GTMOE_ERR_OUT_OF_MEMORY = 5
+};
+
+/* lowprecision.Precision (lowprecision/lowprecision.go:9-16) */
+enum gtmoe_precision { GTMOE_FLOAT64 = 0, GTMOE_FLOAT32 = 1, GTMOE_INT8 = 2, GTMOE_FP4 = 3 };
+
+/* Which weight matrix an upload fills.  Gate, Up and Down are the three
+ * perceptron.Layers of feedforward.GatedFeedForward
+ * (feedforward/gatedfeedforward.go:11-19); ROUTER is
+ * MixtureOfExperts.RouterLayer (mixtureofexperts/mixtureofexperts.go:19). */
+enum gtmoe_role {
+    GTMOE_ROLE_ROUTER = 0,
+    GTMOE_ROLE_SHARED_GATE = 1,
+    GTMOE_ROLE_SHARED_UP = 2,
+    GTMOE_ROLE_SHARED_DOWN = 3,
+    GTMOE_ROLE_ROUTED_GATE = 4,
+    GTMOE_ROLE_ROUTED_UP = 5,
+    GTMOE_ROLE_ROUTED_DOWN = 6
+};
+
+/* Forward flags: which expert kernels run.  AUTO takes the fp32 dequant-GEMV
+ * path while tokens per expert are few (decode) and the bf16 MFMA grouped GEMM
+ * otherwise (prefill).  FP32 and BF16 force one path. */
+enum gtmoe_path { GTMOE_PATH_AUTO = 0, GTMOE_PATH_FP32 = 1, GTMOE_PATH_BF16 = 2 };
+
+typedef struct gtmoe_context gtmoe_context;
+typedef struct gtmoe_layer gtmoe_layer;
+
+/* The shape of one MixtureOfExperts.  Mirrors the arguments of
+ * NewMixtureOfExperts / NewClampedMixtureOfExperts
+ * (mixtureofexperts/mixtureofexperts.go:33-45) plus the fields
+ * UseHashRouting (:16) and the expert weight precision
+ * (transformer.Settings.WeightPrecision, transformer/settings.go:23). */
+typedef struct gtmoe_layer_desc {
+    int32_t vector_size;        /* d: RouterLayer.NumberOfInputs() */
+    int32_t expert_hidden_size; /* h */
+    int32_t shared_experts;     /* S >= 0 */
+    int32_t routed_experts;     /* E in [1, 256] */
+    int32_t experts_per_token;  /* k in [1, min(E, 8)] */
+    int32_t precision;          /* expert weights: GTMOE_FLOAT32, GTMOE_INT8 or GTMOE_FP4 */
+    int32_t use_hash_routing;   /* MixtureOfExperts.UseHashRouting */
+    int32_t reserved;
+    double clamp_limit;         /* > 0: clamped SwiGLU (feedforward.NewClampedSwiGLU); 0: SwiGLU */
+} gtmoe_layer_desc;
+
+/* One weight matrix in the reference's Rows storage (lowprecision/rows.go:8-18,
+ * RowsSnapshot at :148-170): `rows` output neurons of `width` inputs.
+ *   FLOAT64  values = double[rows*width]
+ *   FLOAT32  values = float[rows*width]
+ *   INT8     values = int8_t[rows*width], scales = float[rows*ceil(width/16)]
+ *   FP4      values = uint8_t[rows*ceil(width/2)] (even index in the low
+ *            nibble), scales = float[rows*ceil(width/16)]
+ * values_bytes and scale_count are the lengths of the two arrays and are
+ * checked like RowsFromSnapshot (rows.go:172-203). */
+typedef struct gtmoe_rows {
+    int32_t precision;
+    int32_t rows;
+    int32_t width;
+    int32_t reserved;
+    const void *values;
+    size_t values_bytes;
+    const float *scales;
+    size_t scale_count;
+} gtmoe_rows;
+
+/* ---- library and context -------------------------------------------------
+ * gtmoe_open replaces the device bring-up of gpu.Open/openDevice
+ * (gpu/device.go:90-130); gtmoe_close replaces Device.Close. */
+int32_t gtmoe_abi_version(void);
+int32_t gtmoe_device_count(int32_t *count);
+int32_t gtmoe_open(int32_t device, gtmoe_context **out);
+int32_t gtmoe_close(gtmoe_context *ctx);
+/* Text of the last failure on this context (Device.LastError,
+ * gpu/device.go:749-753).  With ctx NULL: the last failure of gtmoe_open. */
+const char *gtmoe_last_error(const gtmoe_context *ctx);
+
+/* ---- quantization ---------------------------------------------------------
+ * Rows.Append over `rows` rows of float64 values (lowprecision/rows.go:38-79,
+ * encoders lowprecision/lowprecision.go:56-104), bit-exact.  values_out is
+ * float/int8/packed-FP4 storage as in gtmoe_rows; scales_out is written for
+ * INT8 and FP4.  Host only; no context needed. */
+int32_t gtmoe_encode_rows(int32_t precision, int32_t rows, int32_t width, const double *values,
+                          void *values_out, float *scales_out);
+
+/* ---- layers ------------------------------------------------------------------
+ * A layer is one MixtureOfExperts with its weights resident in HBM.  It
+ * replaces buildMixtureOfExperts (mixtureofexperts.go:47-70) on the device. */
+int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtmoe_layer **out);
+int32_t gtmoe_layer_destroy(gtmoe_layer *layer);
+
+/* Upload one weight matrix and its float64 biases (perceptron.Layer.Weights /
+ * CompressedWeights and Biases, perceptron/layer.go:12-25).  index is the
+ * expert within its role (ignored for ROUTER).  Expert matrices must use the
+ * layer's precision; the router may be FLOAT64 or FLOAT32 (logits are
+ * computed in fp32 on the device).  Shapes: gate/up h x d, down d x h,
+ * router E x d.  Re-uploading replaces the matrix, as Layer.SetWeights does
+ * (layer.go:234-246). */
+int32_t gtmoe_upload_rows(gtmoe_layer *layer, int32_t role, int32_t index, const gtmoe_rows *rows,
+                          const double *biases);
+
+/* MixtureOfExperts.BalanceBiases (mixtureofexperts.go:20), E values. */
+int32_t gtmoe_set_balance_biases(gtmoe_layer *layer, const double *biases);
+int32_t gtmoe_get_balance_biases(const gtmoe_layer *layer, double *biases);
+
+/* RMSNorm weights applied before this layer by gtmoe_stack_forward
+ * (Block.FeedForwardNorm, transformer/block.go:59-60; epsilon 1e-6 as
+ * normalization.NewRMSNorm, normalization/rmsnorm.go:20-31). */
+int32_t gtmoe_set_norm_weights(gtmoe_layer *layer, const double *weights);
+
+/* ---- forward ---------------------------------------------------------------
+ * MixtureOfExperts.Forward (mixtureofexperts.go:122-216): inputs T x d
+ * float64 row-major, token_ids T values (required with hash routing, may be
+ * NULL otherwise), outputs T x d float64.  tokens may be 0.  flags is a
+ * gtmoe_path.  The routing, gates, dispatch and per-expert load of the call
+ * stay cached on the layer (the lastChosenExperts/lastGates/lastRowsForExpert/
+ * lastExpertLoad state, :207-214) and are read back with gtmoe_last_routing.
+ * A negative token id with hash routing returns GTMOE_ERR_INVALID_ARGUMENT
+ * (the reference panics, :144-146). */
+int32_t gtmoe_forward(gtmoe_layer *layer, int32_t tokens, const double *inputs, const int64_t *token_ids,
+                      double *outputs, uint32_t flags);
+
+/* Forward over device-resident fp32 activations (inputs and outputs T x d in
+ * HBM, token_ids T int64 in HBM or NULL), enqueued on `stream` (a
+ * hipStream_t; NULL = the context's stream) without synchronising.  Hash
+ * routing ids must be non-negative: the device cannot panic.  For callers
+ * that keep activations on the GPU between layers; no reference counterpart
+ * beyond Forward itself. */
+int32_t gtmoe_forward_device(gtmoe_layer *layer, int32_t tokens, const float *inputs,
+                             const int64_t *token_ids, float *outputs, uint32_t flags, void *stream);
+
+/* The routing state of the last forward on this layer, any pointer may be
+ * NULL: chosen T x k expert indices and gates T x k (lastChosenExperts,
+ * lastGates), load E (lastExpertLoad), rows_for_expert T*k token indices with
+ * expert_offsets E+1 (lastRowsForExpert flattened: experts ascending, tokens
+ * ascending inside an expert).  tokens_out receives T.  Synchronises. */
+int32_t gtmoe_last_routing(gtmoe_layer *layer, int32_t *tokens_out, int32_t *chosen, double *gates,
+                           int32_t *load, int32_t *rows_for_expert, int32_t *expert_offsets);
+
+/* MixtureOfExperts.LastExpertLoad (mixtureofexperts.go:287-291): E counts. */
+int32_t gtmoe_last_expert_load(gtmoe_layer *layer, int32_t *load);
+
+/* MixtureOfExperts.UpdateBalance (mixtureofexperts.go:293-310): moves every
+ * balance bias by +-rate against the last forward's mean load.  Does
+ * nothing before the first forward or with hash routing. */
+int32_t gtmoe_update_balance(gtmoe_layer *layer, double rate);
+
+/* Routing alone from given float64 router logits (pre-activation plus bias,
+ * T x E): affinity sqrt(softplus), top-k with the balance biases and the
+ * reference's tie-break, gates, then dispatch (mixtureofexperts.go:153-180).
+ * Runs the same device kernels as the forward; outputs as in
+ * gtmoe_last_routing (any may be NULL).  Bit-exact against the CPU
+ * restatement for any logits. */
+int32_t gtmoe_route_from_logits(gtmoe_layer *layer, int32_t tokens, const double *logits, int32_t *chosen,
+                                double *gates, int32_t *load, int32_t *rows_for_expert,
+                                int32_t *expert_offsets);
+
+/* A stack of blocks without attention, x <- x + MoE_l(RMSNorm_l(x)) for
+ * l = 0..n_layers-1 (the residual of transformer.Block.Forward,
+ * transformer/block.go:71-77).  x is T x d float64, updated in place; every
+ * layer needs gtmoe_set_norm_weights and the same d.  When chosen/gates are
+ * given they receive [n_layers][T][k] of each layer's routing. */
+int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, double *x,
+                            const int64_t *token_ids, uint32_t flags, int32_t *chosen, double *gates);
+
+/* The same stack over a device-resident fp32 x (T x d in HBM, updated in
+ * place), enqueued on `stream` without synchronising. */
+int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, float *x,
+                                   const int64_t *token_ids, uint32_t flags, void *stream);
+
+/* ---- measurement -----------------------------------------------------------
+ * Per-kernel timing with HIP events, the counterpart of the Vulkan
+ * timestamps behind Recorder.MeasureTime / DispatchTimes
+ * (gpu/compute.go:54-57,670-694).  While enabled, every kernel the context
+ * launches is bracketed by events on its stream; gtmoe_timing_read sums the
+ * elapsed milliseconds per kernel name since the last reset.  Reading
+ * synchronises.  names is a buffer of `capacity` entries of 64 bytes. */
+int32_t gtmoe_timing_enable(gtmoe_context *ctx, int32_t enabled);
+int32_t gtmoe_timing_reset(gtmoe_context *ctx);
+int32_t gtmoe_timing_read(gtmoe_context *ctx, int32_t capacity, char *names, double *total_ms,
+                          int32_t *launches, int32_t *count);
+
+/* The expert path the last forward on this layer took (a gtmoe_path other
+ * than AUTO). */
+int32_t gtmoe_last_path(const gtmoe_layer *layer, int32_t *path);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GTMOE_H */
