@@ -16,6 +16,8 @@
 // hidden = act_g(gate + b_g) * act_u(up + b_u).  Down adds its bias.
 #include "common.h"
 
+#include <utility>
+
 namespace gtmoe {
 
 namespace {
@@ -106,22 +108,42 @@ __device__ __forceinline__ void decode(const RawBlock<kFloat32> &r, float (&w)[1
 
 // Sum N per-lane values over the 64 lanes of a wave.  Afterwards lane l
 // holds in v[0] the total of value index l / (64 / N).
+//
+// Every exchange halves the live values: the lower lanes of a pair keep
+// values [0, half) and send [half, 2*half), the upper lanes the reverse.
+// The pair loop is expanded at compile time (index sequences) so the array
+// elements stay in registers; a runtime-indexed form lets the compiler fold
+// the per-lane choice into a register-file index, which costs a compare and
+// select per element.
+template <int I, int HALF>
+__device__ __forceinline__ void exchange_pair(float *v, bool upper, int off)
+{
+    const float lo = v[I], hi = v[I + HALF];
+    const float send = upper ? lo : hi;
+    const float keep = upper ? hi : lo;
+    v[I] = keep + __shfl_xor(send, off);
+}
+
+template <int HALF, int... I>
+__device__ __forceinline__ void exchange_all(float *v, bool upper, int off, std::integer_sequence<int, I...>)
+{
+    (exchange_pair<I, HALF>(v, upper, off), ...);
+}
+
+template <int HALF>
+__device__ __forceinline__ void halve(float *v, int lane, int off)
+{
+    if constexpr (HALF >= 1) {
+        exchange_all<HALF>(v, (lane & off) != 0, off, std::make_integer_sequence<int, HALF>{});
+        halve<HALF / 2>(v, lane, off >> 1);
+    }
+}
+
 template <int N>
 __device__ __forceinline__ void wave_transpose_reduce(float (&v)[N], int lane)
 {
-    int off = 32;
-#pragma unroll
-    for (int half = N / 2; half >= 1; half /= 2) {
-        const bool upper = (lane & off) != 0;
-#pragma unroll
-        for (int i = 0; i < half; ++i) {
-            const float send = upper ? v[i] : v[i + half];
-            const float keep = upper ? v[i + half] : v[i];
-            v[i] = keep + __shfl_xor(send, off);
-        }
-        off >>= 1;
-    }
-    for (; off > 0; off >>= 1) v[0] += __shfl_xor(v[0], off);
+    halve<N / 2>(v, lane, 32);
+    for (int off = 32 / N; off > 0; off >>= 1) v[0] += __shfl_xor(v[0], off);
 }
 
 template <int N>
@@ -137,10 +159,14 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x));
 
 }  // namespace
 
-// TC tokens of a group are held in registers at a time; RIF rows (of each
-// matrix) have their weight blocks in flight together.
+// One chunk of TC tokens (positions p0+c0 .. p0+c0+TC-1, those >= M masked)
+// of a group against the RPW rows of this wave: TC tokens are held in
+// registers, RIF rows (of each matrix) have their weight blocks in flight
+// together.
 template <int PREC, int NB, int TC, int RIF, bool GATEUP>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
+__device__ __forceinline__ void gemv_chunk(const GemvArgs &a, int p0, int M, int c0, int r0, int lane,
+                                           const char *wb0, const char *wb1, const float *sb0, const float *sb1,
+                                           const float *bb0, const float *bb1)
 {
     constexpr int RPW = 4;
     constexpr int MATS = GATEUP ? 2 : 1;
@@ -148,6 +174,110 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     constexpr int SHIFT = 6 - Log2<NV>::value;
     static_assert(NV <= 64, "too many values per lane");
 
+    float xr[TC][NB][16];
+#pragma unroll
+    for (int c = 0; c < TC; ++c) {
+        const int m = c0 + c;
+        const int src = (m < M) ? (GATEUP ? a.tok[p0 + m] : p0 + m) : 0;
+        const float *xrow = a.in + (size_t)src * a.ld_in;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int b = lane + 64 * j;
+            if (m < M && b < a.nblocks) {
+                const float4 *p = reinterpret_cast<const float4 *>(xrow + (size_t)b * 16);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v = p[q];
+                    xr[c][j][4 * q + 0] = v.x;
+                    xr[c][j][4 * q + 1] = v.y;
+                    xr[c][j][4 * q + 2] = v.z;
+                    xr[c][j][4 * q + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) xr[c][j][q] = 0.f;
+            }
+        }
+    }
+
+#pragma unroll 1
+    for (int rr0 = 0; rr0 < RPW; rr0 += RIF) {
+        RawBlock<PREC> raw[RIF][MATS][NB];
+        float sc[RIF][MATS][NB];
+#pragma unroll
+        for (int rr = 0; rr < RIF; ++rr) {
+            const int r = r0 + rr0 + rr;
+#pragma unroll
+            for (int mt = 0; mt < MATS; ++mt) {
+                const char *row = (mt == 0 ? wb0 : wb1) + (size_t)r * a.row_bytes;
+                const float *srow = (mt == 0 ? sb0 : sb1) + (size_t)r * a.nblocks;
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int b = lane + 64 * j;
+                    if (r < a.rows && b < a.nblocks) {
+                        load_raw<PREC>(raw[rr][mt][j], row, b);
+                        sc[rr][mt][j] = (PREC == kFloat32) ? 1.0f : srow[b];
+                    } else {
+                        zero_raw<PREC>(raw[rr][mt][j]);
+                        sc[rr][mt][j] = 0.f;
+                    }
+                }
+            }
+        }
+        float part[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) part[i] = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < RIF; ++rr)
+#pragma unroll
+            for (int mt = 0; mt < MATS; ++mt)
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    float w[16];
+                    decode(raw[rr][mt][j], w);
+#pragma unroll
+                    for (int c = 0; c < TC; ++c) {
+                        float bs = 0.f;
+#pragma unroll
+                        for (int q = 0; q < 16; ++q) bs = fmaf(xr[c][j][q], w[q], bs);
+                        float &acc = part[(rr * MATS + mt) * TC + c];
+                        acc = fmaf(bs, sc[rr][mt][j], acc);
+                    }
+                }
+        wave_transpose_reduce<NV>(part, lane);
+        const int v = lane >> SHIFT;
+        const bool writer = (lane & ((1 << SHIFT) - 1)) == 0;
+        const int c = v % TC;
+        const int m = c0 + c;
+        if (GATEUP) {
+            const float other = __shfl_xor(part[0], TC << SHIFT);
+            const int mt = (v / TC) % 2;
+            const int rr = v / (2 * TC);
+            const int r = r0 + rr0 + rr;
+            if (writer && mt == 0 && m < M && r < a.rows) {
+                float gv = part[0] + bb0[r];
+                float uv = other + bb1[r];
+                if (a.clamp > 0.f) {
+                    gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
+                    uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
+                }
+                a.out[(size_t)(p0 + m) * a.ld_out + r] = silu(gv) * uv;
+            }
+        } else {
+            const int rr = v / TC;
+            const int r = r0 + rr0 + rr;
+            if (writer && m < M && r < a.rows) a.out[(size_t)(p0 + m) * a.ld_out + r] = part[0] + bb0[r];
+        }
+    }
+}
+
+// One wave = 4 output rows of one group; the group's tokens go through in
+// chunks whose width follows the group's token count (TCMAX, then 2, then 1),
+// so a group with one or two tokens does no work for absent ones.
+template <int PREC, int NB, int TCMAX, int RIF, bool GATEUP>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
+{
+    constexpr int RPW = 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = blockIdx.y;
     const int p0 = a.goff[g];
@@ -163,103 +293,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     const float *bb0 = a.b0 + (size_t)g * a.rows;
     const float *bb1 = GATEUP ? a.b1 + (size_t)g * a.rows : nullptr;
 
-    for (int c0 = 0; c0 < M; c0 += TC) {
-        float xr[TC][NB][16];
-#pragma unroll
-        for (int c = 0; c < TC; ++c) {
-            const int m = c0 + c;
-            const int src = (m < M) ? (GATEUP ? a.tok[p0 + m] : p0 + m) : 0;
-            const float *xrow = a.in + (size_t)src * a.ld_in;
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int b = lane + 64 * j;
-                if (m < M && b < a.nblocks) {
-                    const float4 *p = reinterpret_cast<const float4 *>(xrow + (size_t)b * 16);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float4 v = p[q];
-                        xr[c][j][4 * q + 0] = v.x;
-                        xr[c][j][4 * q + 1] = v.y;
-                        xr[c][j][4 * q + 2] = v.z;
-                        xr[c][j][4 * q + 3] = v.w;
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 16; ++q) xr[c][j][q] = 0.f;
-                }
-            }
-        }
-
-#pragma unroll 1
-        for (int rr0 = 0; rr0 < RPW; rr0 += RIF) {
-            RawBlock<PREC> raw[RIF][MATS][NB];
-            float sc[RIF][MATS][NB];
-#pragma unroll
-            for (int rr = 0; rr < RIF; ++rr) {
-                const int r = r0 + rr0 + rr;
-#pragma unroll
-                for (int mt = 0; mt < MATS; ++mt) {
-                    const char *row = (mt == 0 ? wb0 : wb1) + (size_t)r * a.row_bytes;
-                    const float *srow = (mt == 0 ? sb0 : sb1) + (size_t)r * a.nblocks;
-#pragma unroll
-                    for (int j = 0; j < NB; ++j) {
-                        const int b = lane + 64 * j;
-                        if (r < a.rows && b < a.nblocks) {
-                            load_raw<PREC>(raw[rr][mt][j], row, b);
-                            sc[rr][mt][j] = (PREC == kFloat32) ? 1.0f : srow[b];
-                        } else {
-                            zero_raw<PREC>(raw[rr][mt][j]);
-                            sc[rr][mt][j] = 0.f;
-                        }
-                    }
-                }
-            }
-            float part[NV];
-#pragma unroll
-            for (int i = 0; i < NV; ++i) part[i] = 0.f;
-#pragma unroll
-            for (int rr = 0; rr < RIF; ++rr)
-#pragma unroll
-                for (int mt = 0; mt < MATS; ++mt)
-#pragma unroll
-                    for (int j = 0; j < NB; ++j) {
-                        float w[16];
-                        decode(raw[rr][mt][j], w);
-#pragma unroll
-                        for (int c = 0; c < TC; ++c) {
-                            float bs = 0.f;
-#pragma unroll
-                            for (int q = 0; q < 16; ++q) bs = fmaf(xr[c][j][q], w[q], bs);
-                            float &acc = part[(rr * MATS + mt) * TC + c];
-                            acc = fmaf(bs, sc[rr][mt][j], acc);
-                        }
-                    }
-            wave_transpose_reduce<NV>(part, lane);
-            const int v = lane >> SHIFT;
-            const bool writer = (lane & ((1 << SHIFT) - 1)) == 0;
-            const int c = v % TC;
-            const int m = c0 + c;
-            if (GATEUP) {
-                const float other = __shfl_xor(part[0], TC << SHIFT);
-                const int mt = (v / TC) % 2;
-                const int rr = v / (2 * TC);
-                const int r = r0 + rr0 + rr;
-                if (writer && mt == 0 && m < M && r < a.rows) {
-                    float gv = part[0] + bb0[r];
-                    float uv = other + bb1[r];
-                    if (a.clamp > 0.f) {
-                        gv = fminf(gv, a.clamp);                 // ClampedSiLU: x > L -> silu(L)
-                        uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
-                    }
-                    a.out[(size_t)(p0 + m) * a.ld_out + r] = silu(gv) * uv;
-                }
-            } else {
-                const int rr = v / TC;
-                const int r = r0 + rr0 + rr;
-                if (writer && m < M && r < a.rows) a.out[(size_t)(p0 + m) * a.ld_out + r] = part[0] + bb0[r];
-            }
-        }
+    int c0 = 0;
+    if constexpr (TCMAX >= 4) {
+        for (; M - c0 >= 3; c0 += 4)
+            gemv_chunk<PREC, NB, 4, RIF, GATEUP>(a, p0, M, c0, r0, lane, wb0, wb1, sb0, sb1, bb0, bb1);
     }
+    if constexpr (TCMAX >= 2) {
+        for (; M - c0 >= 2; c0 += 2)
+            gemv_chunk<PREC, NB, 2, RIF, GATEUP>(a, p0, M, c0, r0, lane, wb0, wb1, sb0, sb1, bb0, bb1);
+    }
+    for (; c0 < M; ++c0)
+        gemv_chunk<PREC, NB, 1, RIF, GATEUP>(a, p0, M, c0, r0, lane, wb0, wb1, sb0, sb1, bb0, bb1);
 }
 
 namespace {

@@ -145,25 +145,30 @@ __device__ double affinity(double logit)
 // Router logits: logits[t][e] = double(sum_i x[t][i] * w[e][i]) + bias[e].
 // ---------------------------------------------------------------------------
 
-// Few tokens: one workgroup per expert and 16 tokens; each wave owns four
-// tokens and reduces a full-width dot product across its 64 lanes.
-__global__ __launch_bounds__(256) void router_small_kernel(const float *__restrict__ x, int ldx, int T, int d,
+// Few tokens: one wave per (token, expert) dot product; lanes read float4
+// runs of the zero-padded rows (x row stride ldx, router row stride ldw, both
+// multiples of 64 floats) and reduce across the wave.
+__global__ __launch_bounds__(256) void router_small_kernel(const float *__restrict__ x, int ldx, int T, int kp,
                                                            const float *__restrict__ w, int ldw,
                                                            const double *__restrict__ bias, int E,
                                                            double *__restrict__ logits)
 {
-    const int e = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float *wr = w + (size_t)e * ldw;
-    for (int tt = 0; tt < 4; ++tt) {
-        const int t = blockIdx.y * 16 + wave * 4 + tt;
-        if (t >= T) break;
-        const float *xr = x + (size_t)t * ldx;
-        float acc = 0.f;
-        for (int i = lane; i < d; i += 64) acc = fmaf(xr[i], wr[i], acc);
-        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-        if (lane == 0) logits[(size_t)t * E + e] = (double)acc + bias[e];
+    const int lane = threadIdx.x & 63;
+    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pair >= T * E) return;  // wave-uniform
+    const int t = pair / E, e = pair - t * E;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)t * ldx);
+    const float4 *wr = reinterpret_cast<const float4 *>(w + (size_t)e * ldw);
+    float acc = 0.f;
+    for (int i = lane; i < kp / 4; i += 64) {
+        const float4 a = xr[i], b = wr[i];
+        acc = fmaf(a.x, b.x, acc);
+        acc = fmaf(a.y, b.y, acc);
+        acc = fmaf(a.z, b.z, acc);
+        acc = fmaf(a.w, b.w, acc);
     }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) logits[(size_t)t * E + e] = (double)acc + bias[e];
 }
 
 // Many tokens: 64 tokens x 64 experts per workgroup, K staged through LDS in
@@ -214,8 +219,10 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
 {
     if (T <= 0) return hipSuccess;
     if (T <= 256) {
-        dim3 grid(E, (T + 15) / 16);
-        hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, d, w, ldw, bias, E, logits);
+        // rows are zero-padded to a multiple of 64 values
+        const int kp = (d + 63) / 64 * 64;
+        dim3 grid((T * E + 3) / 4);
+        hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits);
     } else {
         dim3 grid((E + 63) / 64, (T + 63) / 64);
         hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, x, ldx, T, d, w, ldw, bias, E, logits);

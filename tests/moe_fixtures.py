@@ -13,8 +13,7 @@ LINEAR, SILU, CLAMPED_SILU, CLAMPED_LINEAR = 0, 1, 2, 3
 def make_layer(encode, precision, rows, width, rng, std=0.02, bias_std=0.0, activation=LINEAR, clamp=0.0):
     w = rng.normal(0.0, std, size=(rows, width))
     b = rng.normal(0.0, bias_std, size=rows) if bias_std else np.zeros(rows)
-    return SimpleNamespace(weights=encode(precision, w), biases=b, activation=activation,
-                           clamp_limit=clamp, dense=w)
+    return SimpleNamespace(weights=encode(precision, w), biases=b, activation=activation, clamp_limit=clamp)
 
 
 def make_expert(encode, precision, d, h, rng, std=0.02, bias_std=0.0, clamp=0.0):

@@ -1,0 +1,152 @@
+"""GPU parity of the bf16 MFMA path (prefill) against the CPU oracle.
+
+Bars: routing equal to the oracle's except at near-ties (reported); the
+dispatch permutation and load bit-exact for the device's routing; outputs
+under the device's routing within max |y - r| / max |r| <= 2e-2.  At the
+full configuration sizes the oracle evaluates a seeded sample of tokens:
+a token's output depends only on its own row and routing."""
+import sys
+
+import numpy as np
+import pytest
+
+import gotransformers_amd as gt
+import oracle
+from tests.moe_fixtures import FLOAT32, FP4, INT8, make_moe, zipf_router_bias
+from tests.test_gpu_parity import SMALL, rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+FP32_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = gt.Context(0)
+    yield c
+    c.close()
+
+
+def oracle_routing(spec, x):
+    logits = oracle.layer_forward(spec.router, x, threads=16)
+    return oracle.route_from_logits(logits, spec.experts_per_token, spec.balance_biases)
+
+
+def check_flips(gpu_chosen, ref, spec, label):
+    k = spec.experts_per_token
+    diff = np.nonzero(np.any(gpu_chosen != ref.chosen, axis=1))[0]
+    for t in diff:
+        s = np.sort(ref.affinities[t] + spec.balance_biases)[::-1]
+        assert s[k - 1] - s[k] <= 1e-5 * max(1.0, abs(s[k - 1])), (label, t)
+    say(f"[{label}] routing flips at near-ties: {len(diff)} of {len(gpu_chosen)} tokens")
+
+
+def check_dispatch(r, E):
+    d = oracle.dispatch(r.chosen, E)
+    assert np.array_equal(r.load, d.load)
+    assert np.array_equal(r.offsets, d.offsets)
+    assert np.array_equal(r.rows, d.rows)
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+@pytest.mark.parametrize("prec", [FLOAT32, INT8, FP4])
+def test_small_layers_bf16_path(ctx, name, prec):
+    say(f"bf16 small layer {name} precision {prec}")
+    cfg = SMALL[name]
+    spec = make_moe(gt.encode_rows, precision=prec, seed=7, std=0.3, bias_std=0.05, **cfg)
+    rng = np.random.default_rng(8)
+    T = 300
+    x = rng.uniform(-1, 1, size=(T, cfg["d"]))
+    ids = rng.integers(0, 1000, size=T) if cfg.get("use_hash") else None
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        y = m.forward(x, ids, path=gt.PATH_BF16)
+        r = m.last_routing()
+        assert m.last_path == gt.PATH_BF16
+    finally:
+        m.destroy()
+    check_dispatch(r, cfg["E"])
+    ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates)
+    e = rel_err(y, ref.outputs)
+    assert e <= BF16_TOL, e
+
+
+def test_bf16_one_row_matches_many_rows(ctx):
+    say("bf16 one row vs many rows")
+    spec = make_moe(gt.encode_rows, d=128, h=192, E=4, k=2, S=1, seed=9, precision=INT8)
+    x = np.random.default_rng(10).uniform(-1, 1, (200, 128))
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        allrows = m.forward(x, path=gt.PATH_BF16)
+        for t in (0, 77, 199):
+            one = m.forward(x[t:t + 1], path=gt.PATH_BF16)
+            assert np.array_equal(one[0], allrows[t])
+    finally:
+        m.destroy()
+
+
+def run_full(ctx, spec, x, sample, label, path=gt.PATH_AUTO, tol=BF16_TOL):
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        y = m.forward(x, path=path)
+        r = m.last_routing()
+        used = m.last_path
+    finally:
+        m.destroy()
+    E = len(spec.routed)
+    check_dispatch(r, E)
+    check_flips(r.chosen, oracle_routing(spec, x), spec, label)
+    ref = oracle.moe_forward_routed(spec, x[sample], r.chosen[sample], r.gates[sample], threads=16)
+    e = rel_err(y[sample], ref.outputs)
+    say(f"[{label}] path {used}, max rel err on {len(sample)} sampled tokens {e:.3e}")
+    assert e <= tol
+    return r, used
+
+
+def test_c3_fp4_prefill(ctx):
+    # d=1024, 64 routed + 1 shared expert, top-6, hidden 512, FP4, 4096 tokens
+    say("C3 fp4 prefill T=4096")
+    spec = make_moe(gt.encode_rows, d=1024, h=512, E=64, S=1, k=6, precision=FP4, seed=3)
+    x = np.random.default_rng(3).normal(size=(4096, 1024))
+    sample = np.sort(np.random.default_rng(33).choice(4096, 48, replace=False))
+    _, used = run_full(ctx, spec, x, sample, "C3")
+    assert used == gt.PATH_BF16
+
+
+def test_c4_int8_skewed_prefill(ctx):
+    # d=2048, 128 experts, top-8, hidden 768, Int8, 16384 tokens, Zipf(1.2) router-bias skew
+    say("C4 int8 skewed prefill T=16384")
+    bias = zipf_router_bias(128, 1.2, seed=4, scale=0.6)
+    spec = make_moe(gt.encode_rows, d=2048, h=768, E=128, S=0, k=8, precision=INT8, seed=4, router_bias=bias)
+    x = np.random.default_rng(4).normal(size=(16384, 2048))
+    sample = np.sort(np.random.default_rng(44).choice(16384, 24, replace=False))
+    r, used = run_full(ctx, spec, x, sample, "C4")
+    assert used == gt.PATH_BF16
+    load = np.sort(r.load)[::-1]
+    say(f"[C4] realized loads (desc), first 8: {load[:8].tolist()}, median {int(np.median(load))}, "
+        f"min {int(load[-1])}")
+
+
+@pytest.mark.parametrize("T,path,tol", [(64, gt.PATH_AUTO, FP32_TOL), (1024, gt.PATH_AUTO, BF16_TOL)])
+def test_c5_shaped_stack(ctx, T, path, tol):
+    # per layer d=2048, 64 experts + 1 shared, top-4, hidden 1024, FP4; 3 layers
+    say(f"C5-shaped stack, 3 layers, T={T}")
+    layers = [make_moe(gt.encode_rows, d=2048, h=1024, E=64, S=1, k=4, precision=FP4, seed=50 + i)
+              for i in range(3)]
+    norms = [np.ones(2048)] * 3
+    x0 = np.random.default_rng(5).normal(size=(T, 2048))
+    ms = [gt.MixtureOfExperts.from_spec(ctx, s) for s in layers]
+    try:
+        for m, w in zip(ms, norms):
+            m.set_norm_weights(w)
+        x, chosen, gates = gt.stack_forward(ms, x0, path=path, with_routing=True)
+        used = ms[0].last_path
+    finally:
+        for m in ms:
+            m.destroy()
+    sample = np.sort(np.random.default_rng(55).choice(T, min(T, 24), replace=False))
+    ref = oracle.stack_forward_routed(layers, norms, x0[sample], chosen[:, sample], gates[:, sample], threads=16)
+    e = rel_err(x[sample], ref)
+    say(f"[C5 stack T={T}] path {used}, max rel err {e:.3e}")
+    assert e <= tol
