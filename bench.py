@@ -1,17 +1,23 @@
 """Benchmark of the MoE layer forward on one MI355X.
 
-Workload (the decode configuration the metric is quoted on): one MoE layer,
-d=1024, 16 routed experts, top-2, SwiGLU hidden 2048, Int8 expert weights
-(per-16 absmax/127 block scales), fp32 router, a batch of 32 tokens with
-N(0,1) activations resident in HBM; weights N(0, 0.02), seed 0.  A step is
-one layer forward (router, top-k, dispatch, gate/up, down, combine).
-
+Default workload (the decode configuration the metric is quoted on): one MoE
+layer, d=1024, 16 routed experts, top-2, SwiGLU hidden 2048, Int8 expert
+weights (per-16 absmax/127 block scales), fp32 router, a batch of 32 tokens
+with N(0,1) activations resident in HBM; weights N(0, 0.02), seed 0.  A step
+is one layer forward (router, top-k, dispatch, gate/up, down, combine).
 Four copies of the layer's weights (4 x 126 MB) are used round-robin so the
-256 MB Infinity Cache cannot hold the weight set: the gate/up and down
-kernels read their weights from HBM.
+256 MB Infinity Cache cannot hold the weight set.
 
-Prints one JSON line.  `roofline` is for the dominant kernel (gemv_gateup):
-achieved = algorithmic bytes per launch / mean launch time from HIP events
+Other workloads (--workload): c2 with --tokens 1/8/32; c3 (FP4 prefill,
+d=1024, 64+1 experts, top-6, h=512, T=4096); c4 (Int8 prefill, d=2048, 128
+experts, top-8, h=768, T=16384, Zipf(1.2) router-bias skew); c5d / c5p (24
+blocks RMSNorm + MoE + residual, d=2048, 64+1 experts, top-4, h=1024, FP4,
+T=64 / T=8192; four distinct seeded weight sets cycled over the 24 layers,
+every layer with its own resident copy).
+
+Prints one JSON line.  `roofline` is for the dominant kernel: HBM-bound
+gemv_gateup (decode) or MFMA-bound mfma_gateup (prefill); achieved =
+algorithmic bytes or FLOPs per launch / mean launch time from HIP events
 recorded around every kernel of the timed region.  `cpu_baseline` times the
 CPU restatement of the reference algorithm (oracle/, float64, the
 reference's SplitAcrossThreads policy) on a bounded sample of the same
@@ -31,70 +37,109 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer tokens/s @1 GPU; achieved HBM GB/s & MFMA util vs peak"
 HBM_PEAK_GBS = 8000.0
-D, E, K, H = 1024, 16, 2, 2048
-COPIES = 4
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+WORKLOADS = {
+    "c2": dict(d=1024, E=16, k=2, h=2048, S=0, prec="int8", T=32, layers=1, copies=4, seed=0),
+    "c3": dict(d=1024, E=64, k=6, h=512, S=1, prec="fp4", T=4096, layers=1, copies=1, seed=3),
+    "c4": dict(d=2048, E=128, k=8, h=768, S=0, prec="int8", T=16384, layers=1, copies=1, seed=4, zipf=0.6),
+    "c5d": dict(d=2048, E=64, k=4, h=1024, S=1, prec="fp4", T=64, layers=24, copies=1, seed=5, sets=4),
+    "c5p": dict(d=2048, E=64, k=4, h=1024, S=1, prec="fp4", T=8192, layers=24, copies=1, seed=5, sets=4),
+}
 
 
-def expert_specs(gt, seed):
-    """Encoded weights of one layer (same arrays for every copy)."""
-    from tests.moe_fixtures import FLOAT32, INT8, make_moe
-    return make_moe(gt.encode_rows, d=D, h=H, E=E, k=K, S=0, precision=INT8, router_precision=FLOAT32, seed=seed)
+def weight_bytes_per_value(prec):
+    return {"int8": 1.0, "fp4": 0.5, "fp32": 4.0}[prec]
 
 
-def gateup_bytes(load, tokens):
-    """Algorithmic HBM bytes of one gemv_gateup launch: gate and up rows
-    (Int8 codes + fp32 scale per 16) of every expert with load > 0, the
-    token rows it reads (fp32) and the hidden rows it writes (fp32)."""
-    active = int(np.count_nonzero(load))
-    weights = active * 2 * H * (D + D // 16 * 4)
-    return weights + tokens * D * 4 + int(load.sum()) * H * 4
+def expert_bytes(c, rows, width):
+    """Reference-format bytes of one rows x width matrix (codes + scales)."""
+    b = weight_bytes_per_value(c["prec"])
+    scales = 0 if c["prec"] == "fp32" else rows * ((width + 15) // 16) * 4
+    return int(rows * width * b) + scales
 
 
-def step_bytes(load, tokens):
-    """Algorithmic HBM bytes of a whole layer forward (for the extra
-    whole-step fraction): router, all weights of active experts, inputs,
-    outputs."""
-    active = int(np.count_nonzero(load))
-    per_expert = 3 * D * H + 3 * D * H // 16 * 4
-    return active * per_expert + E * D * 4 + E * 8 + 2 * tokens * D * 4
+def gateup_bytes(c, load, T):
+    """Algorithmic HBM bytes of one gate/up launch: gate and up matrices of
+    every expert with load > 0 (plus shared experts), the token rows read
+    (fp32) and hidden rows written (fp32)."""
+    active = int(np.count_nonzero(load)) + c["S"]
+    return active * 2 * expert_bytes(c, c["h"], c["d"]) + T * c["d"] * 4 + (int(load.sum()) + c["S"] * T) * c["h"] * 4
 
 
-def cpu_baseline(spec, tokens, budget_s):
-    import oracle
-    cores = os.cpu_count() or 1
+def step_bytes(c, load, T):
+    active = int(np.count_nonzero(load)) + c["S"]
+    per_expert = 2 * expert_bytes(c, c["h"], c["d"]) + expert_bytes(c, c["d"], c["h"])
+    return active * per_expert + c["E"] * c["d"] * 4 + c["E"] * 8 + 2 * T * c["d"] * 4
+
+
+def gateup_flops(c, load, T):
+    """Useful FLOPs of one gate/up launch: 2 * rows * (2h) * d."""
+    rows = int(load.sum()) + c["S"] * T
+    return 2.0 * rows * 2 * c["h"] * c["d"]
+
+
+def layer_flops(c, T):
+    return 2.0 * T * (c["E"] * c["d"] + (c["k"] + c["S"]) * 3 * c["d"] * c["h"])
+
+
+def make_specs(gt, c):
+    from tests.moe_fixtures import FLOAT32, FP4, INT8, make_moe, zipf_router_bias
+    prec = {"int8": INT8, "fp4": FP4, "fp32": FLOAT32}[c["prec"]]
+    bias = zipf_router_bias(c["E"], 1.2, seed=c["seed"], scale=c["zipf"]) if "zipf" in c else None
+    sets = c.get("sets", 1)
+    return [make_moe(gt.encode_rows, d=c["d"], h=c["h"], E=c["E"], k=c["k"], S=c["S"], precision=prec,
+                     router_precision=FLOAT32, seed=c["seed"] + 101 * i, router_bias=bias) for i in range(sets)]
+
+
+def host_cores():
     try:
-        cores = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        pass
-    x = np.random.default_rng(0).normal(size=(tokens, D))
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(c, specs, budget_s):
+    """The CPU restatement of the reference forward on the host cores, timed
+    on a bounded sample of the workload's tokens."""
+    import oracle
+    cores = host_cores()
+    tokens = min(c["T"], 32)
+    x = np.random.default_rng(0).normal(size=(tokens, c["d"]))
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.moe_forward(spec, x, threads=cores)
+        if c["layers"] > 1:
+            norms = [np.ones(c["d"])] * c["layers"]
+            layers = [specs[i % len(specs)] for i in range(c["layers"])]
+            oracle.stack_forward(layers, norms, x, threads=cores)
+        else:
+            oracle.moe_forward(specs[0], x, threads=cores)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
+    what = f"{c['layers']}-layer stack" if c["layers"] > 1 else "layer"
     return {"value": tokens * reps / el, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{reps} forwards of the same layer at T={tokens} (float64 restatement, "
-                      f"SplitAcrossThreads over {cores} threads), {el:.1f} s"}
+            "sample": f"{reps} forwards of the {what} over {tokens} of the workload's tokens "
+                      f"(float64 restatement, SplitAcrossThreads over {cores} threads), {el:.1f} s"}
 
 
-def traffic_from_profiles(workload_key):
+def traffic_from_profiles(key):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        data = json.load(f)
-    entry = data.get(workload_key)
+        entry = json.load(f).get(key)
     return None if entry is None else entry.get("bytes_per_launch")
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--tokens", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -102,50 +147,67 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
-              f"(the path is measured at one GPU's share; see DESIGN.md for sharding)", file=sys.stderr)
+              f"(the path is measured at one GPU's share; DESIGN.md describes how it would shard)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
     import gotransformers_amd as gt
 
-    T = args.tokens
-    spec = expert_specs(gt, seed=0)
+    c = dict(WORKLOADS[args.workload])
+    if args.tokens:
+        c["T"] = args.tokens
+    T, d = c["T"], c["d"]
+    prefill_like = T * c["k"] > 8 * c["E"]
+    steps = args.steps or (400 if not prefill_like and c["layers"] == 1 else 30 if c["layers"] == 1 else 10)
+    warmup = args.warmup if args.warmup is not None else max(3, steps // 10)
+
+    specs = make_specs(gt, c)
     ctx = gt.Context(0)
-    layers = [gt.MixtureOfExperts.from_spec(ctx, spec) for _ in range(COPIES)]
+    n_obj = c["copies"] * c["layers"]
+    layers = [gt.MixtureOfExperts.from_spec(ctx, specs[i % len(specs)]) for i in range(n_obj)]
+    if c["layers"] > 1:
+        for m in layers:
+            m.set_norm_weights(np.ones(d))
     g = torch.Generator(device="cpu").manual_seed(0)
-    x = torch.randn(T, D, generator=g, dtype=torch.float32).cuda()
-    y = torch.empty(T, D, dtype=torch.float32, device="cuda")
+    x0 = torch.randn(T, d, generator=g, dtype=torch.float32).cuda()
+    x = x0.clone()
+    y = torch.empty(T, d, dtype=torch.float32, device="cuda")
 
     def step(i):
-        layers[i % COPIES].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO)
+        if c["layers"] > 1:
+            x.copy_(x0)
+            gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO)
+        else:
+            layers[i % c["copies"]].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     path = layers[0].last_path
     load = layers[0].last_expert_load()
 
-    # timed region: K steps, per-kernel HIP events on the layer's stream
+    # timed region with a HIP event pair around every kernel on the layer stream
     ctx.timing(True)
     ctx.timing_reset()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     times = ctx.timing_read()
     ctx.timing(False)
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    ms_events = (t1 - t0) * 1e3 / steps
 
-    # the same K steps without per-kernel events (launch overhead of events excluded)
+    # the same steps without the per-kernel events: the step time reported
     torch.cuda.synchronize()
     t2 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     torch.cuda.synchronize()
     t3 = time.perf_counter()
-    ms_plain = (t3 - t2) * 1e3 / args.steps
+    ms_plain = (t3 - t2) * 1e3 / steps
 
     if args.copy_calibration:
         a = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
@@ -153,48 +215,63 @@ def main():
         b.copy_(a)
         torch.cuda.synchronize()
 
-    dominant = "gemv_gateup" if path == gt.PATH_FP32 else "mfma_gateup"
+    decode = path == gt.PATH_FP32
+    dominant = "gemv_gateup" if decode else "mfma_gateup"
     kms, klaunch = times.get(dominant, (float("nan"), 1))
     kmean_s = kms / klaunch / 1e3
-    gbytes = gateup_bytes(load, T)
-    achieved = gbytes / kmean_s / 1e9
-    workload = f"C2 decode: MoE layer d={D} E={E} k={K} h={H} Int8 experts, T={T}"
-    traffic = traffic_from_profiles(f"{dominant}/c2_int8_t{T}")
-    step_total_ms = sum(v[0] for v in times.values()) / args.steps
+    key = f"{dominant}/{args.workload}_t{T}"
+    if decode:
+        per_launch = gateup_bytes(c, load, T)
+        achieved = per_launch / kmean_s / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profiles(key)}
+    else:
+        per_launch = gateup_flops(c, load, T)
+        achieved = per_launch / kmean_s / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic_from_profiles(key)}
+    roof.update({"kernel": dominant, "algorithmic_per_launch": per_launch, "mean_launch_us": kmean_s * 1e6,
+                 "launches": klaunch})
 
     for m in layers:
         m.destroy()
     ctx.close()
 
-    cpu = None if args.no_cpu else cpu_baseline(spec, T, args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline(c, specs, args.cpu_seconds)
 
+    names = {"c2": "C2 decode: MoE layer", "c3": "C3 prefill: MoE layer", "c4": "C4 skewed prefill: MoE layer",
+             "c5d": "C5 decode: 24-block stack", "c5p": "C5 prefill: 24-block stack"}
+    workload = (f"{names[args.workload]} d={d} E={c['E']}+{c['S']} shared k={c['k']} h={c['h']} "
+                f"{c['prec']} experts, T={T}")
+    step_layers = c["layers"]
     line = {
         "metric": METRIC,
         "value": T / (ms_plain / 1e3),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_plain,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if decode else "bf16",
         "data": "synthetic",
-        "config": {"workload": workload, "tokens": T, "d_model": D, "routed_experts": E, "top_k": K,
-                   "expert_hidden": H, "expert_weights": "Int8 per-16 fp32 scales", "weight_copies": COPIES,
-                   "path": "fp32 dequant-GEMV" if path == gt.PATH_FP32 else "bf16 MFMA"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": dominant,
-                     "algorithmic_bytes_per_launch": gbytes, "mean_launch_us": kmean_s * 1e6},
+        "config": {"workload": workload, "tokens": T, "d_model": d, "routed_experts": c["E"],
+                   "shared_experts": c["S"], "top_k": c["k"], "expert_hidden": c["h"],
+                   "expert_weights": f"{c['prec']} per-16 fp32 scales", "layers_per_step": step_layers,
+                   "weight_copies": c["copies"],
+                   "path": "fp32 dequant-GEMV" if decode else "bf16 MFMA grouped GEMM"},
+        "roofline": roof,
         "cpu_baseline": cpu,
         "detail": {
-            "ms_per_step_with_kernel_events": ms_per_step,
-            "kernel_ms_per_step": {k: v[0] / args.steps for k, v in sorted(times.items())},
-            "sum_of_kernel_ms_per_step": step_total_ms,
-            "active_experts": int(np.count_nonzero(load)),
-            "step_algorithmic_bytes": step_bytes(load, T),
-            "step_hbm_frac": step_bytes(load, T) / (ms_plain / 1e3) / 1e9 / HBM_PEAK_GBS,
+            "ms_per_step_with_kernel_events": ms_events,
+            "kernel_ms_per_step": {k: v[0] / steps for k, v in sorted(times.items())},
+            "active_experts_layer0": int(np.count_nonzero(load)),
+            "step_algorithmic_bytes": step_bytes(c, load, T) * step_layers,
+            "step_hbm_frac": step_bytes(c, load, T) * step_layers / (ms_plain / 1e3) / 1e9 / HBM_PEAK_GBS,
+            "step_flops": layer_flops(c, T) * step_layers,
+            "step_mfma_frac": layer_flops(c, T) * step_layers / (ms_plain / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         },
     }
     print(json.dumps(line), flush=True)
