@@ -15,10 +15,15 @@ blocks RMSNorm + MoE + residual, d=2048, 64+1 experts, top-4, h=1024, FP4,
 T=64 / T=8192; four distinct seeded weight sets cycled over the 24 layers,
 every layer with its own resident copy).
 
-Prints one JSON line.  `roofline` is for the dominant kernel: HBM-bound
-gemv_gateup (decode) or MFMA-bound mfma_gateup (prefill); achieved =
-algorithmic bytes or FLOPs per launch / mean launch time from HIP events
-recorded around every kernel of the timed region.  `cpu_baseline` times the
+Prints one JSON line.  `value` comes from the timed steps (synchronised on
+both sides, no per-kernel events).  `roofline` is for the dominant kernel:
+HBM-bound gemv_gateup (decode) or MFMA-bound mfma_gateup (prefill); achieved
+= algorithmic bytes or FLOPs per launch / mean launch time, the mean taken by
+one HIP event pair (torch.cuda.Event on the stream the kernels run on) around
+a burst of back-to-back relaunches of that kernel over every resident layer
+copy, which keeps per-launch event skew out of the figure.  A further pass
+with an event pair around every kernel gives the per-kernel breakdown in
+`detail`.  `cpu_baseline` times the
 CPU restatement of the reference algorithm (oracle/, float64, the
 reference's SplitAcrossThreads policy) on a bounded sample of the same
 workload on the host cores."""
@@ -174,12 +179,18 @@ def main():
     x = x0.clone()
     y = torch.empty(T, d, dtype=torch.float32, device="cuda")
 
+    # a stream of our own (default priority): its handle is non-null, so the
+    # library launches on it and torch events recorded on it bracket our kernels
+    stream = torch.cuda.Stream()
+    sptr = stream.cuda_stream
+    torch.cuda.set_stream(stream)
+
     def step(i):
         if c["layers"] > 1:
             x.copy_(x0)
-            gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO)
+            gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
         else:
-            layers[i % c["copies"]].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO)
+            layers[i % c["copies"]].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
 
     for i in range(warmup):
         step(i)
@@ -187,27 +198,44 @@ def main():
     path = layers[0].last_path
     load = layers[0].last_expert_load()
 
-    # timed region with a HIP event pair around every kernel on the layer stream
-    ctx.timing(True)
-    ctx.timing_reset()
+    # timed region: K steps bracketed by synchronisation (no per-kernel events)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         step(i)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    times = ctx.timing_read()
-    ctx.timing(False)
-    ms_events = (t1 - t0) * 1e3 / steps
+    ms_plain = (t1 - t0) * 1e3 / steps
 
-    # the same steps without the per-kernel events: the step time reported
+    # the dominant kernel: a burst of relaunches of the last forward's
+    # gate/up kernel on the same stream, rotating through every resident
+    # layer (so weight reads keep missing the Infinity Cache), bracketed by
+    # one HIP event pair
+    n_burst = max(len(layers), (200 if path == gt.PATH_FP32 else 20) // len(layers) * len(layers))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for m in layers:
+        m.relaunch(gt.KERNEL_GATEUP, stream=sptr)
+    ev0.record(stream)
+    for i in range(n_burst):
+        layers[i % len(layers)].relaunch(gt.KERNEL_GATEUP, stream=sptr)
+    ev1.record(stream)
+    ev1.synchronize()
+    kmean_s = ev0.elapsed_time(ev1) / n_burst / 1e3
+    klaunch = n_burst
+
+    # per-kernel breakdown: event pairs around every kernel over a few steps
+    ctx.timing(True)
+    ctx.timing_reset()
+    n_detail = min(steps, 50)
     torch.cuda.synchronize()
     t2 = time.perf_counter()
-    for i in range(steps):
+    for i in range(n_detail):
         step(i)
     torch.cuda.synchronize()
     t3 = time.perf_counter()
-    ms_plain = (t3 - t2) * 1e3 / steps
+    times = ctx.timing_read()
+    ctx.timing(False)
+    ms_events = (t3 - t2) * 1e3 / n_detail
 
     if args.copy_calibration:
         a = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
@@ -217,8 +245,6 @@ def main():
 
     decode = path == gt.PATH_FP32
     dominant = "gemv_gateup" if decode else "mfma_gateup"
-    kms, klaunch = times.get(dominant, (float("nan"), 1))
-    kmean_s = kms / klaunch / 1e3
     key = f"{dominant}/{args.workload}_t{T}"
     if decode:
         per_launch = gateup_bytes(c, load, T)
@@ -266,7 +292,7 @@ def main():
         "cpu_baseline": cpu,
         "detail": {
             "ms_per_step_with_kernel_events": ms_events,
-            "kernel_ms_per_step": {k: v[0] / steps for k, v in sorted(times.items())},
+            "kernel_ms_per_step_events": {k: v[0] / n_detail for k, v in sorted(times.items())},
             "active_experts_layer0": int(np.count_nonzero(load)),
             "step_algorithmic_bytes": step_bytes(c, load, T) * step_layers,
             "step_hbm_frac": step_bytes(c, load, T) * step_layers / (ms_plain / 1e3) / 1e9 / HBM_PEAK_GBS,

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libgtmoe.so")
 
 FLOAT64, FLOAT32, INT8, FP4 = 0, 1, 2, 3
 PATH_AUTO, PATH_FP32, PATH_BF16 = 0, 1, 2
+KERNEL_GATEUP, KERNEL_DOWN = 0, 1
 
 ROLE_ROUTER = 0
 ROLES = {("shared", "gate"): 1, ("shared", "up"): 2, ("shared", "down"): 3,
@@ -32,7 +33,7 @@ EXPORTED = [
     "gtmoe_set_balance_biases", "gtmoe_get_balance_biases", "gtmoe_set_norm_weights", "gtmoe_forward",
     "gtmoe_forward_device", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
     "gtmoe_route_from_logits", "gtmoe_stack_forward", "gtmoe_stack_forward_device", "gtmoe_timing_enable",
-    "gtmoe_timing_reset", "gtmoe_timing_read", "gtmoe_last_path",
+    "gtmoe_timing_reset", "gtmoe_timing_read", "gtmoe_last_path", "gtmoe_relaunch",
 ]
 
 
@@ -95,6 +96,7 @@ def library():
         "gtmoe_timing_reset": ([P], i32),
         "gtmoe_timing_read": ([P, i32, P, P, P, P], i32),
         "gtmoe_last_path": ([P, P], i32),
+        "gtmoe_relaunch": ([P, i32, P], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -340,6 +342,10 @@ class MixtureOfExperts:
                                                           gates.ctypes.data, load.ctypes.data, rows.ctypes.data,
                                                           offsets.ctypes.data))
         return SimpleNamespace(chosen=chosen, gates=gates, load=load, rows=rows, offsets=offsets)
+
+    def relaunch(self, kernel=KERNEL_GATEUP, stream=None):
+        """Launch one expert kernel of the last forward again (for timing)."""
+        self.ctx.check(library().gtmoe_relaunch(self.handle, kernel, stream))
 
     @property
     def last_path(self):

@@ -139,6 +139,7 @@ struct Workspace {
     float *hidden32 = nullptr;    // [P][hp]
     uint16_t *hidden16 = nullptr;  // [P][hp] bf16
     float *slot_out = nullptr;    // [P][d]
+    int32_t *chunk_cnt = nullptr;  // [chunks][E] scratch of the many-token dispatch
 };
 
 struct gtmoe_layer {
@@ -152,6 +153,14 @@ struct gtmoe_layer {
     std::vector<double> balance_host;
     float *norm_w = nullptr;  // [d]
     bool has_norm = false;
+    float *router_wn = nullptr;        // [E][dp] router rows times the norm weights
+    std::vector<float> router_host;    // [E][dp] fp32 router rows
+    std::vector<float> norm_host;      // [d]
+    // launch arguments of the expert kernels of the last forward
+    GemvArgs last_gemv[2]{};
+    MfmaArgs last_mfma[2]{};
+    int last_max_tiles = 0;
+    bool relaunch_ready = false;  // the expert kernels of the last forward can be launched again
     std::vector<char> uploaded;  // per (role, index)
     Workspace ws;
     // state of the last forward
@@ -287,6 +296,7 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
         {(void **)&w.goff, (size_t)(L->G + 1) * 4},     {(void **)&w.tile_off, (size_t)(L->G + 1) * 4},
         {(void **)&w.tok, P * 4},                       {(void **)&w.hidden32, P * L->hp * 4},
         {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
+        {(void **)&w.chunk_cnt, (size_t)dispatch_chunks(cap) * L->E * 4},
     };
     size_t total = 0;
     for (const Part &p : parts) total += align_up(p.bytes, 256);
@@ -329,23 +339,89 @@ int choose_path(const gtmoe_layer *L, int T, uint32_t flags)
     return (few && fits) ? GTMOE_PATH_FP32 : GTMOE_PATH_BF16;
 }
 
-// Routing, dispatch and the expert kernels, reading the prepared inputs in
-// ws.xf (fp32 path) or ws.xb (bf16 path); leaves the slot outputs in
-// ws.slot_out.  token_ids: device pointer (hash routing).
-int32_t route_and_experts(gtmoe_layer *L, int T, const int64_t *token_ids, int path, hipStream_t s)
+// Where a forward's input rows come from: raw rows [T][d] as float or
+// double, optionally passed through the layer's RMSNorm first.
+struct Inputs {
+    const void *x;
+    bool f64;
+    bool norm;
+};
+
+// Input preparation, routing and dispatch.  Few tokens: one fused launch.
+// Otherwise: convert or RMSNorm into ws.xf / ws.xb, router and top-k (or hash
+// routing), then the dispatch.  token_ids: device pointer (hash routing).
+int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t *token_ids, int path, hipStream_t s)
 {
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
-    if (L->desc.use_hash_routing) {
+    const bool hash = L->desc.use_hash_routing != 0;
+    const bool need_f32 = path == GTMOE_PATH_FP32 || !hash;
+    float *xf = need_f32 ? w.xf : nullptr;
+    uint16_t *xb = path == GTMOE_PATH_BF16 ? w.xb : nullptr;
+    // the dispatch's per-group tile prefix counts MFMA m-tiles on the bf16
+    // path and token slices on the fp32 path
+    const int bm = path == GTMOE_PATH_BF16 ? mfma_tile_m() : kGemvSlice;
+    if (fused_route_fits(T, L->k)) {
+        FusedArgs f{};
+        f.x = in.x;
+        f.norm = in.norm ? L->norm_w : nullptr;
+        f.w = in.norm ? L->router_wn : L->router_w;
+        f.bias = L->router_b;
+        f.balance = L->balance;
+        f.ids = token_ids;
+        f.T = T;
+        f.d = L->d;
+        f.kp = L->dp;
+        f.E = L->E;
+        f.k = L->k;
+        f.S = L->S;
+        f.bm = bm;
+        f.xf = xf;
+        f.xb = xb;
+        f.logits = w.logits;
+        f.chosen = w.chosen;
+        f.gates = w.gates;
+        f.gates32 = w.gates32;
+        f.load = w.load;
+        f.offsets = w.offsets;
+        f.rows = w.rows;
+        f.pos = w.pos;
+        f.goff = w.goff;
+        f.tok = w.tok;
+        f.tile_off = w.tile_off;
+        RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, s));
+        return GTMOE_OK;
+    }
+    if (in.norm) {
+        RUN(ctx, s, "rmsnorm", launch_rmsnorm((const float *)in.x, T, L->d, L->norm_w, xf, L->dp, xb, L->dp, s));
+    } else if (in.f64) {
+        RUN(ctx, s, "convert_inputs",
+            launch_convert_inputs_f64((const double *)in.x, T, L->d, xf, L->dp, xb, L->dp, s));
+    } else {
+        RUN(ctx, s, "convert_inputs",
+            launch_convert_inputs_f32((const float *)in.x, T, L->d, xf, L->dp, xb, L->dp, s));
+    }
+    if (hash) {
         RUN(ctx, s, "hash_route", launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
     } else {
         RUN(ctx, s, "router", launch_router(w.xf, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s));
         RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
     }
-    const int bm = mfma_tile_m();
     RUN(ctx, s, "dispatch",
         launch_dispatch(w.chosen, T, L->k, L->E, L->S, bm, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
-                        w.tile_off, s));
+                        w.tile_off, w.chunk_cnt, s));
+    return GTMOE_OK;
+}
+
+// The expert kernels over the dispatched positions, reading ws.xf (fp32
+// path) or ws.xb (bf16 path); leaves the slot outputs in ws.slot_out.
+int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
+{
+    gtmoe_context *ctx = L->ctx;
+    Workspace &w = L->ws;
+    const int bm = path == GTMOE_PATH_BF16 ? mfma_tile_m() : kGemvSlice;
+    // upper bound of the tiles / slices over all groups
+    const int max_tiles = L->S * ((T + bm - 1) / bm) + (T * L->k + bm - 1) / bm + L->E;
     if (path == GTMOE_PATH_FP32) {
         GemvArgs a{};
         a.w0 = L->gate.values;
@@ -363,10 +439,16 @@ int32_t route_and_experts(gtmoe_layer *L, int T, const int64_t *token_ids, int p
         a.ld_in = L->dp;
         a.tok = w.tok;
         a.goff = w.goff;
+        a.slice_off = w.tile_off;
+        a.groups = L->G;
+        a.tslice = kGemvSlice;
         a.out = w.hidden32;
         a.ld_out = L->hp;
         a.clamp = (float)L->desc.clamp_limit;
-        RUN(ctx, s, "gemv_gateup", launch_gemv_gateup(a, L->gate.precision, L->G, s));
+        L->last_gemv[0] = a;
+        L->last_max_tiles = max_tiles;
+        L->relaunch_ready = true;
+        RUN(ctx, s, "gemv_gateup", launch_gemv_gateup(a, L->gate.precision, max_tiles, s));
         GemvArgs b{};
         b.w0 = L->down.values;
         b.s0 = L->down.scales;
@@ -380,11 +462,14 @@ int32_t route_and_experts(gtmoe_layer *L, int T, const int64_t *token_ids, int p
         b.ld_in = L->hp;
         b.tok = nullptr;
         b.goff = w.goff;
+        b.slice_off = w.tile_off;
+        b.groups = L->G;
+        b.tslice = kGemvSlice;
         b.out = w.slot_out;
         b.ld_out = L->d;
-        RUN(ctx, s, "gemv_down", launch_gemv_down(b, L->down.precision, L->G, s));
+        L->last_gemv[1] = b;
+        RUN(ctx, s, "gemv_down", launch_gemv_down(b, L->down.precision, max_tiles, s));
     } else {
-        const int max_tiles = L->S * ((T + bm - 1) / bm) + (T * L->k + bm - 1) / bm + L->E;
         MfmaArgs a{};
         a.w0 = L->gate.values;
         a.s0 = L->gate.scales;
@@ -407,6 +492,9 @@ int32_t route_and_experts(gtmoe_layer *L, int T, const int64_t *token_ids, int p
         a.out = w.hidden16;
         a.ldo = L->hp;
         a.clamp = (float)L->desc.clamp_limit;
+        L->last_mfma[0] = a;
+        L->last_max_tiles = max_tiles;
+        L->relaunch_ready = true;
         RUN(ctx, s, "mfma_gateup", launch_mfma_gateup(a, L->gate.precision, max_tiles, s));
         MfmaArgs b{};
         b.w0 = L->down.values;
@@ -426,6 +514,7 @@ int32_t route_and_experts(gtmoe_layer *L, int T, const int64_t *token_ids, int p
         b.groups = L->G;
         b.out = w.slot_out;
         b.ldo = L->d;
+        L->last_mfma[1] = b;
         RUN(ctx, s, "mfma_down", launch_mfma_down(b, L->down.precision, max_tiles, s));
     }
     return GTMOE_OK;
@@ -450,6 +539,19 @@ int32_t fetch_load(gtmoe_layer *L)
         HIP_TRY(ctx, hipMemcpy(L->last_load.data(), L->ws.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost));
     }
     L->load_on_host = true;
+    return GTMOE_OK;
+}
+
+// Router rows with the RMSNorm weights folded in, for the fused routing of
+// a normalised input: logit = inv_rms * sum_i x_i * (w_ei * norm_i) + b_e.
+int32_t refresh_folded_router(gtmoe_layer *L)
+{
+    if (L->router_host.empty() || L->norm_host.empty()) return GTMOE_OK;
+    std::vector<float> wn(L->router_host.size(), 0.f);
+    for (int e = 0; e < L->E; ++e)
+        for (int i = 0; i < L->d; ++i)
+            wn[(size_t)e * L->dp + i] = L->router_host[(size_t)e * L->dp + i] * L->norm_host[i];
+    HIP_TRY(L->ctx, hipMemcpy(L->router_wn, wn.data(), wn.size() * sizeof(float), hipMemcpyHostToDevice));
     return GTMOE_OK;
 }
 
@@ -549,6 +651,9 @@ int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtm
     if (D.routed_experts > kMaxExperts)
         return fail(ctx, GTMOE_ERR_UNSUPPORTED, "at most %d routed experts on the GPU, got %d", kMaxExperts,
                     D.routed_experts);
+    if (D.shared_experts + D.routed_experts > 1024)
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "at most 1024 experts in all on the GPU, got %d",
+                    D.shared_experts + D.routed_experts);
     if (D.experts_per_token > kMaxK)
         return fail(ctx, GTMOE_ERR_UNSUPPORTED, "at most %d experts per token on the GPU, got %d", kMaxK,
                     D.experts_per_token);
@@ -580,7 +685,8 @@ int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtm
             hipMemset(L->router_b, 0, sizeof(double) * L->E) != hipSuccess ||
             hipMalloc(&L->balance, sizeof(double) * L->E) != hipSuccess ||
             hipMemset(L->balance, 0, sizeof(double) * L->E) != hipSuccess ||
-            hipMalloc(&L->norm_w, sizeof(float) * L->d) != hipSuccess)
+            hipMalloc(&L->norm_w, sizeof(float) * L->d) != hipSuccess ||
+            hipMalloc(&L->router_wn, rw) != hipSuccess || hipMemset(L->router_wn, 0, rw) != hipSuccess)
             rc = fail(ctx, GTMOE_ERR_OUT_OF_MEMORY, "cannot allocate the router");
     }
     if (rc != GTMOE_OK) {
@@ -605,6 +711,7 @@ int32_t gtmoe_layer_destroy(gtmoe_layer *L)
     if (L->router_b) (void)hipFree(L->router_b);
     if (L->balance) (void)hipFree(L->balance);
     if (L->norm_w) (void)hipFree(L->norm_w);
+    if (L->router_wn) (void)hipFree(L->router_wn);
     if (L->ws.base) (void)hipFree(L->ws.base);
     delete L;
     return GTMOE_OK;
@@ -629,8 +736,9 @@ int32_t gtmoe_upload_rows(gtmoe_layer *L, int32_t role, int32_t index, const gtm
             for (int i = 0; i < L->d; ++i) w[(size_t)r * L->dp + i] = (float)decoded_value(rows, r, i);
         HIP_TRY(ctx, hipMemcpy(L->router_w, w.data(), w.size() * sizeof(float), hipMemcpyHostToDevice));
         HIP_TRY(ctx, hipMemcpy(L->router_b, biases, sizeof(double) * L->E, hipMemcpyHostToDevice));
+        L->router_host.swap(w);
         L->uploaded[role_slot(L, role, 0)] = 1;
-        return GTMOE_OK;
+        return refresh_folded_router(L);
     }
 
     const bool shared = role <= GTMOE_ROLE_SHARED_DOWN;
@@ -695,8 +803,9 @@ int32_t gtmoe_set_norm_weights(gtmoe_layer *L, const double *weights)
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     std::vector<float> w(weights, weights + L->d);
     HIP_TRY(ctx, hipMemcpy(L->norm_w, w.data(), sizeof(float) * L->d, hipMemcpyHostToDevice));
+    L->norm_host.swap(w);
     L->has_norm = true;
-    return GTMOE_OK;
+    return refresh_folded_router(L);
 }
 
 int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, const int64_t *token_ids,
@@ -735,11 +844,8 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     HIP_TRY(ctx, hipMemcpyAsync(w.x64, inputs, sizeof(double) * T * L->d, hipMemcpyHostToDevice, s));
     if (L->desc.use_hash_routing)
         HIP_TRY(ctx, hipMemcpyAsync(w.ids, token_ids, sizeof(int64_t) * T, hipMemcpyHostToDevice, s));
-    const bool need_f32 = path == GTMOE_PATH_FP32 || !L->desc.use_hash_routing;
-    RUN(ctx, s, "convert_inputs",
-        launch_convert_inputs_f64(w.x64, T, L->d, need_f32 ? w.xf : nullptr, L->dp,
-                                  path == GTMOE_PATH_BF16 ? w.xb : nullptr, L->dp, s));
-    rc = route_and_experts(L, T, w.ids, path, s);
+    rc = prepare_and_route(L, T, Inputs{w.x64, true, false}, w.ids, path, s);
+    if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
     RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, nullptr, nullptr, w.y64, s));
     HIP_TRY(ctx, hipMemcpyAsync(outputs, w.y64, sizeof(double) * T * L->d, hipMemcpyDeviceToHost, s));
@@ -776,11 +882,8 @@ int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs
         return GTMOE_OK;
     }
     Workspace &w = L->ws;
-    const bool need_f32 = path == GTMOE_PATH_FP32 || !L->desc.use_hash_routing;
-    RUN(ctx, s, "convert_inputs",
-        launch_convert_inputs_f32(inputs, T, L->d, need_f32 ? w.xf : nullptr, L->dp,
-                                  path == GTMOE_PATH_BF16 ? w.xb : nullptr, L->dp, s));
-    rc = route_and_experts(L, T, token_ids, path, s);
+    rc = prepare_and_route(L, T, Inputs{inputs, false, false}, token_ids, path, s);
+    if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
     RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, nullptr, outputs, nullptr, s));
     mark_forward(L, T, path, s);
@@ -865,9 +968,10 @@ int32_t gtmoe_route_from_logits(gtmoe_layer *L, int32_t tokens, const double *lo
     }
     RUN(ctx, s, "dispatch",
         launch_dispatch(w.chosen, T, L->k, L->E, L->S, mfma_tile_m(), w.load, w.offsets, w.rows, w.pos, w.goff,
-                        w.tok, w.tile_off, s));
+                        w.tok, w.tile_off, w.chunk_cnt, s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
     mark_forward(L, T, L->last_path, s);
+    L->relaunch_ready = false;
     return gtmoe_last_routing(L, nullptr, chosen, gates, load, rows_for_expert, expert_offsets);
 }
 
@@ -904,11 +1008,8 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
             continue;
         }
         Workspace &w = L->ws;
-        const bool need_f32 = path == GTMOE_PATH_FP32 || !L->desc.use_hash_routing;
-        RUN(ctx, s, "rmsnorm",
-            launch_rmsnorm(x, T, L->d, L->norm_w, need_f32 ? w.xf : nullptr, L->dp,
-                           path == GTMOE_PATH_BF16 ? w.xb : nullptr, L->dp, s));
-        rc = route_and_experts(L, T, ids, path, s);
+        rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s);
+        if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
         if (rc != GTMOE_OK) return rc;
         RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, x, x, nullptr, s));
         mark_forward(L, T, path, s);
@@ -1040,6 +1141,30 @@ int32_t gtmoe_timing_read(gtmoe_context *ctx, int32_t capacity, char *names, dou
         ++i;
     }
     *count = i;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_relaunch(gtmoe_layer *L, int32_t kernel, void *stream)
+{
+    if (!L || (kernel != GTMOE_KERNEL_GATEUP && kernel != GTMOE_KERNEL_DOWN)) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (L->last_T <= 0 || !L->relaunch_ready)
+        return fail(ctx, GTMOE_ERR_NOT_READY, "no forward with tokens to launch again");
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const bool gateup = kernel == GTMOE_KERNEL_GATEUP;
+    if (L->last_path == GTMOE_PATH_FP32) {
+        const GemvArgs &a = L->last_gemv[gateup ? 0 : 1];
+        RUN(ctx, s, gateup ? "gemv_gateup" : "gemv_down",
+            gateup ? launch_gemv_gateup(a, L->gate.precision, L->last_max_tiles, s)
+                   : launch_gemv_down(a, L->down.precision, L->last_max_tiles, s));
+    } else {
+        const MfmaArgs &a = L->last_mfma[gateup ? 0 : 1];
+        RUN(ctx, s, gateup ? "mfma_gateup" : "mfma_down",
+            gateup ? launch_mfma_gateup(a, L->gate.precision, L->last_max_tiles, s)
+                   : launch_mfma_down(a, L->down.precision, L->last_max_tiles, s));
+    }
     return GTMOE_OK;
 }
 

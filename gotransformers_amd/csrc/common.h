@@ -64,10 +64,16 @@ struct GemvArgs {
     int ld_in;
     const int32_t *tok;  // gate/up: token of every position; down: nullptr
     const int32_t *goff;
+    const int32_t *slice_off;  // [groups+1] prefix of token slices per group
+    int groups;
+    int tslice;  // tokens per slice
     float *out;
     int ld_out;
     float clamp;
 };
+
+// Tokens per work slice of the GEMV path (the dispatch's tile size there).
+constexpr int kGemvSlice = 8;
 
 // Arguments of the grouped MFMA GEMM kernels (bf16 path).
 struct MfmaArgs {
@@ -94,6 +100,25 @@ struct MfmaArgs {
     float clamp;
 };
 
+// Arguments of the few-token routing (input preparation and router logits in
+// one launch, top-k or hash routing and the dispatch in a second).
+struct FusedArgs {
+    const void *x;        // input rows [T][d]: float or double
+    const float *norm;    // RMSNorm weights or nullptr
+    const float *w;       // router rows [E][kp] (norm folded in when norm != nullptr)
+    const double *bias;   // [E]
+    const double *balance;
+    const int64_t *ids;   // hash routing
+    int T, d, kp, E, k, S, bm;
+    float *xf;            // prepared rows [T][kp] (fp32) or nullptr
+    uint16_t *xb;         // prepared rows [T][kp] (bf16) or nullptr
+    double *logits;       // [T][E]
+    int32_t *chosen;
+    double *gates;
+    float *gates32;
+    int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off;
+};
+
 // Launchers (each returns the hipError_t of its launch).
 hipError_t launch_convert_inputs_f64(const double *x, int T, int d, float *xf, int ldf, uint16_t *xb, int ldb,
                                      hipStream_t s);
@@ -107,11 +132,16 @@ hipError_t launch_topk(const double *logits, int T, int E, int k, const double *
                        double *gates, float *gates32, hipStream_t s);
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,
                              float *gates32, hipStream_t s);
+bool fused_route_fits(int T, int k);
+hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s);
+// Dispatch: one workgroup up to 1024 tokens, else count / scan / scatter over
+// chunks of 256 tokens using chunk_cnt [dispatch_chunks(T)][E] as scratch.
+int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
                            int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
-                           int32_t *tile_off, hipStream_t s);
-hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int groups, hipStream_t s);
-hipError_t launch_gemv_down(const GemvArgs &a, int precision, int groups, hipStream_t s);
+                           int32_t *tile_off, int32_t *chunk_cnt, hipStream_t s);
+hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
+hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
 hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 hipError_t launch_mfma_down(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 int mfma_tile_m();

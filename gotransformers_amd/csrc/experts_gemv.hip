@@ -1,8 +1,9 @@
 // fp32 expert kernels for few tokens per expert (decode): a dequantizing
 // GEMV that streams each weight row from HBM once per group of tokens.
 //
-// Work split: grid (ceil(rows/16), groups); every wave owns 4 consecutive
-// output rows of one group (expert).  A row's K values are covered by the 64
+// Work split: grid (ceil(rows/16), token slices of all groups); every wave
+// owns 4 consecutive output rows of one group (expert) for one slice of at
+// most 8 of its tokens.  A row's K values are covered by the 64
 // lanes in 16-value blocks -- lane l takes blocks l, l+64, ... -- so each
 // load instruction of a wave reads one contiguous run of the row (1 KiB of
 // Int8, 512 B of FP4), coalesced, together with the matching fp32 scales.
@@ -271,17 +272,28 @@ __device__ __forceinline__ void gemv_chunk(const GemvArgs &a, int p0, int M, int
     }
 }
 
-// One wave = 4 output rows of one group; the group's tokens go through in
-// chunks whose width follows the group's token count (TCMAX, then 2, then 1),
-// so a group with one or two tokens does no work for absent ones.
+// One wave = 4 output rows of one group over one slice of at most tslice of
+// the group's tokens (blockIdx.y enumerates the slices of all groups; the
+// dispatch wrote their prefix).  Inside the slice, tokens go through in
+// chunks whose width follows the count left (TCMAX, then 2, then 1), so a
+// group with one or two tokens does no work for absent ones.
 template <int PREC, int NB, int TCMAX, int RIF, bool GATEUP>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
     constexpr int RPW = 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = blockIdx.y;
-    const int p0 = a.goff[g];
-    const int M = a.goff[g + 1] - p0;
+    const int item = blockIdx.y;
+    if (item >= a.slice_off[a.groups]) return;
+    int lo = 0, hi = a.groups - 1;
+    while (lo < hi) {  // last group whose first slice is <= item
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.slice_off[mid] <= item) lo = mid;
+        else hi = mid - 1;
+    }
+    const int g = lo;
+    const int first = (item - a.slice_off[g]) * a.tslice;
+    const int p0 = a.goff[g] + first;
+    const int M = min(a.goff[g + 1] - a.goff[g] - first, a.tslice);
     if (M <= 0) return;
     const int r0 = (blockIdx.x * 4 + wave) * RPW;
     if (r0 >= a.rows) return;
@@ -309,10 +321,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 namespace {
 
 template <bool GATEUP, int PREC>
-hipError_t launch_prec(const GemvArgs &a, int groups, hipStream_t s)
+hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
 {
     const int nb = (a.nblocks + 63) / 64;
-    dim3 grid((a.rows + 15) / 16, groups);
+    dim3 grid((a.rows + 15) / 16, max_slices);
     constexpr int R = (PREC == kFloat32) ? 1 : 0;  // float32 rows are 4x wider: one row in flight
     if (nb <= 1)
         hipLaunchKernelGGL((gemv_kernel<PREC, 1, 4, R ? 1 : 4, GATEUP>), grid, dim3(256), 0, s, a);
@@ -326,27 +338,27 @@ hipError_t launch_prec(const GemvArgs &a, int groups, hipStream_t s)
 }
 
 template <bool GATEUP>
-hipError_t launch_any(const GemvArgs &a, int precision, int groups, hipStream_t s)
+hipError_t launch_any(const GemvArgs &a, int precision, int max_slices, hipStream_t s)
 {
-    if (groups <= 0) return hipSuccess;
+    if (max_slices <= 0) return hipSuccess;
     switch (precision) {
-    case kInt8: return launch_prec<GATEUP, kInt8>(a, groups, s);
-    case kFP4: return launch_prec<GATEUP, kFP4>(a, groups, s);
-    case kFloat32: return launch_prec<GATEUP, kFloat32>(a, groups, s);
+    case kInt8: return launch_prec<GATEUP, kInt8>(a, max_slices, s);
+    case kFP4: return launch_prec<GATEUP, kFP4>(a, max_slices, s);
+    case kFloat32: return launch_prec<GATEUP, kFloat32>(a, max_slices, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int groups, hipStream_t s)
+hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int max_slices, hipStream_t s)
 {
-    return launch_any<true>(a, precision, groups, s);
+    return launch_any<true>(a, precision, max_slices, s);
 }
 
-hipError_t launch_gemv_down(const GemvArgs &a, int precision, int groups, hipStream_t s)
+hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hipStream_t s)
 {
-    return launch_any<false>(a, precision, groups, s);
+    return launch_any<false>(a, precision, max_slices, s);
 }
 
 }  // namespace gtmoe

@@ -82,7 +82,8 @@ hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *x
 // Weighted combine (mixtureofexperts.go:182-205) in the reference's order:
 // out = 0, + each shared expert's row, then + gate_i * routed row for the
 // slots in chosen order.  With a residual: out = residual + that sum
-// (transformer/block.go:77).  Writes fp32 and/or float64 output.
+// (transformer/block.go:77).  Writes fp32 and/or float64 output.  Grid
+// (T, ceil(d / 1024)); each thread owns four consecutive columns.
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k, const float *__restrict__ slot_out,
                                                       const int32_t *__restrict__ pos,
                                                       const float *__restrict__ gates32,
@@ -90,6 +91,8 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
                                                       double *__restrict__ out64)
 {
     const int t = blockIdx.x;
+    const int j0 = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if (j0 >= d) return;
     int p[8];
     float g[8];
 #pragma unroll
@@ -97,15 +100,39 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
         p[i] = i < k ? S * T + pos[(size_t)t * k + i] : 0;
         g[i] = i < k ? gates32[(size_t)t * k + i] : 0.f;
     }
-    for (int j = threadIdx.x; j < d; j += 256) {
-        float acc = 0.f;
-        for (int s = 0; s < S; ++s) acc += slot_out[((size_t)s * T + t) * d + j];
+    const int n = min(4, d - j0);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (n == 4 && (d & 3) == 0) {
+        for (int s = 0; s < S; ++s) {
+            const float4 v = *reinterpret_cast<const float4 *>(slot_out + ((size_t)s * T + t) * d + j0);
+            acc[0] += v.x;
+            acc[1] += v.y;
+            acc[2] += v.z;
+            acc[3] += v.w;
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (i < k) acc = fmaf(g[i], slot_out[(size_t)p[i] * d + j], acc);
-        if (residual) acc = residual[(size_t)t * d + j] + acc;
-        if (out32) out32[(size_t)t * d + j] = acc;
-        if (out64) out64[(size_t)t * d + j] = (double)acc;
+            if (i < k) {
+                const float4 v = *reinterpret_cast<const float4 *>(slot_out + (size_t)p[i] * d + j0);
+                acc[0] = fmaf(g[i], v.x, acc[0]);
+                acc[1] = fmaf(g[i], v.y, acc[1]);
+                acc[2] = fmaf(g[i], v.z, acc[2]);
+                acc[3] = fmaf(g[i], v.w, acc[3]);
+            }
+    } else {
+        for (int q = 0; q < n; ++q) {
+            for (int s = 0; s < S; ++s) acc[q] += slot_out[((size_t)s * T + t) * d + j0 + q];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (i < k) acc[q] = fmaf(g[i], slot_out[(size_t)p[i] * d + j0 + q], acc[q]);
+        }
+    }
+    for (int q = 0; q < n; ++q) {
+        const size_t o = (size_t)t * d + j0 + q;
+        float v = acc[q];
+        if (residual) v = residual[o] + v;
+        if (out32) out32[o] = v;
+        if (out64) out64[o] = (double)v;
     }
 }
 
@@ -113,8 +140,8 @@ hipError_t launch_combine(int T, int d, int S, int k, const float *slot_out, con
                           const float *residual, float *out32, double *out64, hipStream_t s)
 {
     if (T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, s, T, d, S, k, slot_out, pos, gates32, residual, out32,
-                       out64);
+    hipLaunchKernelGGL(combine_kernel, dim3(T, (d + 1023) / 1024), dim3(256), 0, s, T, d, S, k, slot_out, pos, gates32,
+                       residual, out32, out64);
     return hipGetLastError();
 }
 

@@ -245,14 +245,15 @@ __device__ __forceinline__ bool better(double s1, int e1, double s2, int e2)
     return s1 > s2 || (s1 == s2 && e1 < e2);
 }
 
+// Top-k of one token by one wave (EPL experts per lane).  Writes chosen,
+// gates (float64 and fp32) for token t, and the chosen list to `chosen_copy`
+// when given.
 template <int EPL>
-__global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ logits, int T, int E, int k,
-                                                   const double *__restrict__ balance, int32_t *__restrict__ chosen,
-                                                   double *__restrict__ gates, float *__restrict__ gates32)
+__device__ __forceinline__ void topk_token(const double *__restrict__ logit_row, int t, int E, int k,
+                                           const double *__restrict__ balance, int lane, int32_t *__restrict__ chosen,
+                                           double *__restrict__ gates, float *__restrict__ gates32,
+                                           int32_t *chosen_copy)
 {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;  // wave-uniform
     double a[EPL], sc[EPL];
     bool taken[EPL];
 #pragma unroll
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ lo
         const int e = lane + 64 * j;
         taken[j] = false;
         if (e < E) {
-            a[j] = affinity(logits[(size_t)t * E + e]);
+            a[j] = affinity(logit_row[e]);
             sc[j] = a[j] + balance[e];
         } else {
             a[j] = 0.0;
@@ -333,8 +334,20 @@ __global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ lo
             chosen[(size_t)t * k + i] = list_e[i];
             gates[(size_t)t * k + i] = g;
             gates32[(size_t)t * k + i] = (float)g;
+            if (chosen_copy) chosen_copy[t * k + i] = list_e[i];
         }
     }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ logits, int T, int E, int k,
+                                                   const double *__restrict__ balance, int32_t *__restrict__ chosen,
+                                                   double *__restrict__ gates, float *__restrict__ gates32)
+{
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // wave-uniform
+    topk_token<EPL>(logits + (size_t)t * E, t, E, k, balance, lane, chosen, gates, gates32, nullptr);
 }
 
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
@@ -354,19 +367,28 @@ hipError_t launch_topk(const double *logits, int T, int E, int k, const double *
 // hashedExperts (mixtureofexperts.go:88-96): first = (id*2654435761 + 12345)
 // mod E in unsigned 64-bit arithmetic, then k consecutive experts; gates 1/k.
 // Ids are checked non-negative by the host before launch.
+__device__ __forceinline__ void hash_token(const int64_t *__restrict__ ids, int t, int E, int k,
+                                           int32_t *__restrict__ chosen, double *__restrict__ gates,
+                                           float *__restrict__ gates32, int32_t *chosen_copy)
+{
+    const unsigned long long first =
+        ((unsigned long long)ids[t] * 2654435761ULL + 12345ULL) % (unsigned long long)E;
+    const double g = 1 / (double)k;
+    for (int i = 0; i < k; ++i) {
+        const int32_t e = (int32_t)((first + (unsigned long long)i) % (unsigned long long)E);
+        chosen[(size_t)t * k + i] = e;
+        gates[(size_t)t * k + i] = g;
+        gates32[(size_t)t * k + i] = (float)g;
+        if (chosen_copy) chosen_copy[t * k + i] = e;
+    }
+}
+
 __global__ void hash_route_kernel(const int64_t *__restrict__ ids, int T, int E, int k, int32_t *__restrict__ chosen,
                                   double *__restrict__ gates, float *__restrict__ gates32)
 {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T) return;
-    const unsigned long long first =
-        ((unsigned long long)ids[t] * 2654435761ULL + 12345ULL) % (unsigned long long)E;
-    const double g = 1 / (double)k;
-    for (int i = 0; i < k; ++i) {
-        chosen[(size_t)t * k + i] = (int32_t)((first + (unsigned long long)i) % (unsigned long long)E);
-        gates[(size_t)t * k + i] = g;
-        gates32[(size_t)t * k + i] = (float)g;
-    }
+    hash_token(ids, t, E, k, chosen, gates, gates32, nullptr);
 }
 
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates, float *gates32,
@@ -381,91 +403,140 @@ hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *c
 // ---------------------------------------------------------------------------
 // Dispatch (mixtureofexperts.go:175-190): per-expert load, exclusive offsets,
 // and a stable permutation -- experts ascending, tokens ascending inside an
-// expert -- built by one workgroup.  Tokens go through in chunks of 1024 (one
-// per thread); the rank of a token inside its expert comes from wave ballots
-// and a per-expert prefix over the 16 waves, so no atomic decides an order.
-// Also fills the position tables the expert kernels use (goff, tok) and the
+// expert.  The rank of a token inside its expert comes from wave ballots and
+// prefix sums, never from an atomic, so the order is the reference's.  Also
+// fills the position tables the expert kernels use (goff, tok) and the
 // per-group MFMA tile prefix (tile_off).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ chosen, int T, int k, int E, int S,
-                                                        int bm, int32_t *__restrict__ load, int32_t *__restrict__ offsets,
-                                                        int32_t *__restrict__ rows, int32_t *__restrict__ pos,
-                                                        int32_t *__restrict__ goff, int32_t *__restrict__ tok,
-                                                        int32_t *__restrict__ tile_off)
-{
-    __shared__ int cnt[kMaxExperts];
-    __shared__ int running[kMaxExperts];
-    __shared__ int wave_cnt[16][kMaxExperts];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int G = S + E;
+constexpr int kScanMax = 1024;  // experts + shared experts handled by the scans
 
-    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
-    __syncthreads();
-    for (long long i = tid; i < (long long)T * k; i += 1024) atomicAdd(&cnt[chosen[i]], 1);
-    __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; ++e) {
-            running[e] = acc;
-            offsets[e] = acc;
-            load[e] = cnt[e];
-            acc += cnt[e];
-        }
-        offsets[E] = acc;
-        // groups: shared experts own T positions each, then the routed experts
-        int tiles = 0;
-        for (int g = 0; g < G; ++g) {
-            const int start = g < S ? g * T : S * T + running[g - S];
-            const int m = g < S ? T : cnt[g - S];
-            goff[g] = start;
-            tile_off[g] = tiles;
-            tiles += (m + bm - 1) / bm;
-        }
-        goff[G] = S * T + T * k;
-        tile_off[G] = tiles;
+// Exclusive scan of vals[0..n) (n <= 1024) by a 1024-thread workgroup into
+// out[0..n); returns the total.  vals and out may alias.
+__device__ int block_exclusive_scan(const int *vals, int *out, int n, int *wave_sums, int *total_slot)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int v = tid < n ? vals[tid] : 0;
+    int x = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
     }
-    // shared-expert positions: token = position mod T
-    for (long long p = tid; p < (long long)S * T; p += 1024) tok[p] = (int32_t)(p % T);
+    if (lane == 63) wave_sums[wave] = x;
+    __syncthreads();
+    if (wave == 0) {
+        int w = lane < 16 ? wave_sums[lane] : 0;
+        int inc = w;
+        for (int off = 1; off < 16; off <<= 1) {
+            const int y = __shfl_up(inc, off);
+            if (lane >= off) inc += y;
+        }
+        if (lane < 16) wave_sums[lane] = inc - w;
+        if (lane == 15) *total_slot = inc;
+    }
+    __syncthreads();
+    if (tid < n) out[tid] = x - v + wave_sums[wave];
+    __syncthreads();
+    return *total_slot;
+}
+
+// Ranks of a chunk of tokens inside their experts.  Each of the block's
+// threads holds one token's k chosen experts in ce[] (-1 when absent); on
+// return rk[i] is the number of lower tokens of the same wave with expert
+// ce[i], and wave_cnt[w][e] the count of expert e in wave w.
+__device__ __forceinline__ void wave_ranks(const int (&ce)[kMaxK], int (&rk)[kMaxK], int E, int lane, int wave,
+                                           int (*wave_cnt)[kMaxExperts])
+{
+    for (int e = 0; e < E; ++e) {
+        int match = -1;
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i)
+            if (ce[i] == e) match = i;
+        const unsigned long long b = __ballot(match >= 0);
+        if (lane == 0) wave_cnt[wave][e] = __popcll(b);
+        const int r = __popcll(b & ((1ULL << lane) - 1ULL));
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i)
+            if (i == match) rk[i] = r;
+    }
+}
+
+struct DispatchShared {
+    int cnt[kScanMax];
+    int base[kScanMax];
+    int tiles[kScanMax];
+    int wave_cnt[16][kMaxExperts];
+    int wave_sums[16];
+    int total;
+};
+
+// Group tables from per-expert counts (in sh.cnt) and their exclusive
+// offsets (in sh.base): load, offsets, goff, tile_off and the shared-expert
+// part of tok.
+__device__ void write_group_tables(int T, int k, int E, int S, int bm, DispatchShared &sh, int32_t *__restrict__ load,
+                                   int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
+                                   int32_t *__restrict__ tok, int32_t *__restrict__ tile_off)
+{
+    const int tid = threadIdx.x;
+    const int G = S + E;
+    for (int e = tid; e < E; e += blockDim.x) {
+        load[e] = sh.cnt[e];
+        offsets[e] = sh.base[e];
+    }
+    if (tid == 0) offsets[E] = T * k;
+    for (int g = tid; g < G; g += blockDim.x) {
+        const int m = g < S ? T : sh.cnt[g - S];
+        sh.tiles[g] = (m + bm - 1) / bm;
+        goff[g] = g < S ? g * T : S * T + sh.base[g - S];
+    }
+    if (tid == 0) goff[G] = S * T + T * k;
+    __syncthreads();
+    const int total_tiles = block_exclusive_scan(sh.tiles, sh.tiles, G, sh.wave_sums, &sh.total);
+    for (int g = tid; g < G; g += blockDim.x) tile_off[g] = sh.tiles[g];
+    if (tid == 0) tile_off[G] = total_tiles;
+    for (long long p = tid; p < (long long)S * T; p += blockDim.x) tok[p] = (int32_t)(p % T);
+}
+
+// Whole dispatch by one 1024-thread workgroup; `chosen` may be in LDS.
+__device__ void dispatch_block(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *__restrict__ load,
+                               int32_t *__restrict__ offsets, int32_t *__restrict__ rows, int32_t *__restrict__ pos,
+                               int32_t *__restrict__ goff, int32_t *__restrict__ tok,
+                               int32_t *__restrict__ tile_off, DispatchShared &sh)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += 1024) sh.cnt[e] = 0;
+    __syncthreads();
+    for (long long i = tid; i < (long long)T * k; i += 1024) atomicAdd(&sh.cnt[chosen[i]], 1);
+    __syncthreads();
+    block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
+    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off);
     __syncthreads();
 
     for (int c0 = 0; c0 < T; c0 += 1024) {
         const int t = c0 + tid;
         const bool valid = t < T;
-        int ce[kMaxK];
-        int rk[kMaxK];
+        int ce[kMaxK], rk[kMaxK];
 #pragma unroll
         for (int i = 0; i < kMaxK; ++i) {
             ce[i] = (valid && i < k) ? chosen[(size_t)t * k + i] : -1;
             rk[i] = 0;
         }
-        for (int e = 0; e < E; ++e) {
-            int match = -1;
-#pragma unroll
-            for (int i = 0; i < kMaxK; ++i)
-                if (ce[i] == e) match = i;
-            const unsigned long long b = __ballot(match >= 0);
-            if (lane == 0) wave_cnt[wave][e] = __popcll(b);
-            const int r = __popcll(b & ((1ULL << lane) - 1ULL));
-#pragma unroll
-            for (int i = 0; i < kMaxK; ++i)
-                if (i == match) rk[i] = r;
-        }
+        wave_ranks(ce, rk, E, lane, wave, sh.wave_cnt);
         __syncthreads();
         for (int e = tid; e < E; e += 1024) {
-            int acc = running[e];
+            int acc = sh.base[e];
             for (int w = 0; w < 16; ++w) {
-                const int c = wave_cnt[w][e];
-                wave_cnt[w][e] = acc;
+                const int c = sh.wave_cnt[w][e];
+                sh.wave_cnt[w][e] = acc;
                 acc += c;
             }
-            running[e] = acc;
+            sh.base[e] = acc;
         }
         __syncthreads();
         if (valid) {
 #pragma unroll
             for (int i = 0; i < kMaxK; ++i) {
                 if (i < k) {
-                    const int p = wave_cnt[wave][ce[i]] + rk[i];
+                    const int p = sh.wave_cnt[wave][ce[i]] + rk[i];
                     rows[p] = t;
                     pos[(size_t)t * k + i] = p;
                     tok[(size_t)S * T + p] = t;
@@ -476,12 +547,250 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
     }
 }
 
+__global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ chosen, int T, int k, int E, int S,
+                                                        int bm, int32_t *__restrict__ load, int32_t *__restrict__ offsets,
+                                                        int32_t *__restrict__ rows, int32_t *__restrict__ pos,
+                                                        int32_t *__restrict__ goff, int32_t *__restrict__ tok,
+                                                        int32_t *__restrict__ tile_off)
+{
+    __shared__ DispatchShared sh;
+    dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, sh);
+}
+
+// Many tokens: chunks of 256 tokens (4 waves) per workgroup.
+//   count:   per-chunk, per-expert counts            -> chunk_cnt[c][e]
+//   scan:    one workgroup: per-expert totals, offsets, the group tables, and
+//            every chunk's starting position per expert -> chunk_cnt[c][e]
+//   scatter: per chunk, wave ranks + the chunk's base  -> rows, pos, tok
+constexpr int kChunk = 256;
+
+__global__ __launch_bounds__(kChunk) void dispatch_count_kernel(const int32_t *__restrict__ chosen, int T, int k, int E,
+                                                                int32_t *__restrict__ chunk_cnt)
+{
+    __shared__ int cnt[kMaxExperts];
+    for (int e = threadIdx.x; e < E; e += kChunk) cnt[e] = 0;
+    __syncthreads();
+    const int t = blockIdx.x * kChunk + threadIdx.x;
+    if (t < T)
+        for (int i = 0; i < k; ++i) atomicAdd(&cnt[chosen[(size_t)t * k + i]], 1);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += kChunk) chunk_cnt[(size_t)blockIdx.x * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int T, int k, int E, int S, int bm, int chunks,
+                                                             int32_t *__restrict__ chunk_cnt, int32_t *__restrict__ load,
+                                                             int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
+                                                             int32_t *__restrict__ tok, int32_t *__restrict__ tile_off)
+{
+    __shared__ DispatchShared sh;
+    const int tid = threadIdx.x;
+    // per-expert totals
+    for (int e = tid; e < E; e += 1024) {
+        int acc = 0;
+        for (int c = 0; c < chunks; ++c) acc += chunk_cnt[(size_t)c * E + e];
+        sh.cnt[e] = acc;
+    }
+    __syncthreads();
+    block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
+    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off);
+    // each chunk's first position per expert
+    for (int e = tid; e < E; e += 1024) {
+        int acc = sh.base[e];
+        for (int c = 0; c < chunks; ++c) {
+            const int n = chunk_cnt[(size_t)c * E + e];
+            chunk_cnt[(size_t)c * E + e] = acc;
+            acc += n;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kChunk) void dispatch_scatter_kernel(const int32_t *__restrict__ chosen, int T, int k, int E,
+                                                                  int S, const int32_t *__restrict__ chunk_base,
+                                                                  int32_t *__restrict__ rows, int32_t *__restrict__ pos,
+                                                                  int32_t *__restrict__ tok)
+{
+    __shared__ int wave_cnt[kChunk / 64][kMaxExperts];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.x * kChunk + tid;
+    const bool valid = t < T;
+    int ce[kMaxK], rk[kMaxK];
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i) {
+        ce[i] = (valid && i < k) ? chosen[(size_t)t * k + i] : -1;
+        rk[i] = 0;
+    }
+    wave_ranks(ce, rk, E, lane, wave, wave_cnt);
+    __syncthreads();
+    for (int e = tid; e < E; e += kChunk) {
+        int acc = chunk_base[(size_t)blockIdx.x * E + e];
+        for (int w = 0; w < kChunk / 64; ++w) {
+            const int c = wave_cnt[w][e];
+            wave_cnt[w][e] = acc;
+            acc += c;
+        }
+    }
+    __syncthreads();
+    if (valid) {
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i) {
+            if (i < k) {
+                const int p = wave_cnt[wave][ce[i]] + rk[i];
+                rows[p] = t;
+                pos[(size_t)t * k + i] = p;
+                tok[(size_t)S * T + p] = t;
+            }
+        }
+    }
+}
+
+int dispatch_chunks(int T) { return (T + kChunk - 1) / kChunk; }
+
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load, int32_t *offsets,
                            int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok, int32_t *tile_off,
-                           hipStream_t s)
+                           int32_t *chunk_cnt, hipStream_t s)
 {
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows, pos,
-                       goff, tok, tile_off);
+    if (T <= 1024) {
+        hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows,
+                           pos, goff, tok, tile_off);
+        return hipGetLastError();
+    }
+    const int chunks = dispatch_chunks(T);
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, chunk_cnt);
+    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, T, k, E, S, bm, chunks, chunk_cnt, load,
+                       offsets, goff, tok, tile_off);
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, S, chunk_cnt, rows,
+                       pos, tok);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Routing for few tokens (decode) in two launches: route_token_kernel (one
+// workgroup per token: input preparation, router logits, top-k or hash
+// routing) and dispatch_kernel.  With RMSNorm in front
+// (normalization/rmsnorm.go:33-53) the norm weights are folded into the
+// router rows (wn = w * norm) and the inverse RMS comes from a pass over the
+// raw row, logit = inv_rms * dot(x, wn) + bias.
+// ---------------------------------------------------------------------------
+constexpr int kFusedMaxTK = 2048;  // T*k handled by the two-launch routing
+
+__device__ __forceinline__ uint16_t bf16_bits(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <typename InT>
+__device__ __forceinline__ float in_at(const InT *row, int i)
+{
+    return (float)row[i];
+}
+
+// four consecutive inputs starting at a 4-aligned index (16 B aligned for
+// float rows, 32 B for double rows when d is a multiple of 4)
+__device__ __forceinline__ float4 in4(const float *row, int i) { return *reinterpret_cast<const float4 *>(row + i); }
+__device__ __forceinline__ float4 in4(const double *row, int i)
+{
+    const double2 a = *reinterpret_cast<const double2 *>(row + i);
+    const double2 b = *reinterpret_cast<const double2 *>(row + i + 2);
+    return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+}
+
+// One workgroup per token: the token's E logits (four waves share the
+// experts), then top-k (or hash routing) by wave 0 from LDS, and the token's
+// prepared row (converted or normalised, zero-padded) written by all threads.
+template <typename InT, bool NORM, bool HASH, int EPL>
+__global__ __launch_bounds__(256) void route_token_kernel(FusedArgs a)
+{
+    __shared__ double lg[kMaxExperts];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x;
+    const InT *xr = reinterpret_cast<const InT *>(a.x) + (size_t)t * a.d;
+    const bool vec = (a.d & 3) == 0;
+
+    float ss = 0.f;
+    if (NORM) {
+        if (vec) {
+            for (int i = 4 * lane; i < a.d; i += 256) {
+                const float4 v = in4(xr, i);
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+        } else {
+            for (int i = lane; i < a.d; i += 64) {
+                const float v = in_at(xr, i);
+                ss = fmaf(v, v, ss);
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    }
+    const float inv = NORM ? 1.0f / sqrtf(ss / (float)a.d + 1e-6f) : 1.0f;
+
+    if (!HASH) {
+        for (int e = wave; e < a.E; e += 4) {
+            const float *wr = a.w + (size_t)e * a.kp;
+            float dot = 0.f;
+            if (vec) {
+#pragma unroll 4
+                for (int i = 4 * lane; i < a.d; i += 256) {
+                    const float4 v = in4(xr, i);
+                    const float4 w = *reinterpret_cast<const float4 *>(wr + i);
+                    dot = fmaf(v.x, w.x, dot);
+                    dot = fmaf(v.y, w.y, dot);
+                    dot = fmaf(v.z, w.z, dot);
+                    dot = fmaf(v.w, w.w, dot);
+                }
+            } else {
+                for (int i = lane; i < a.d; i += 64) dot = fmaf(in_at(xr, i), wr[i], dot);
+            }
+            for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+            if (lane == 0) lg[e] = (double)(dot * inv) + a.bias[e];
+        }
+    }
+    for (int i = threadIdx.x; i < a.kp; i += 256) {
+        float v = 0.f;
+        if (i < a.d) {
+            v = in_at(xr, i);
+            if (NORM) v = v * inv * a.norm[i];
+        }
+        if (a.xf) a.xf[(size_t)t * a.kp + i] = v;
+        if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        if (HASH) {
+            if (lane == 0) hash_token(a.ids, t, a.E, a.k, a.chosen, a.gates, a.gates32, nullptr);
+        } else {
+            topk_token<EPL>(lg, t, a.E, a.k, a.balance, lane, a.chosen, a.gates, a.gates32, nullptr);
+        }
+    }
+}
+
+bool fused_route_fits(int T, int k) { return T >= 1 && T * k <= kFusedMaxTK && T <= 1024; }
+
+template <typename InT, bool NORM>
+static hipError_t launch_token_typed(const FusedArgs &a, bool hash, hipStream_t s)
+{
+    dim3 grid(a.T);
+    if (hash) hipLaunchKernelGGL((route_token_kernel<InT, NORM, true, 1>), grid, dim3(256), 0, s, a);
+    else if (a.E <= 64) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 1>), grid, dim3(256), 0, s, a);
+    else if (a.E <= 128) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 2>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 4>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s)
+{
+    if (!fused_route_fits(a.T, a.k)) return hipErrorInvalidValue;
+    hipError_t e;
+    if (input_f64) e = a.norm ? launch_token_typed<double, true>(a, hash, s) : launch_token_typed<double, false>(a, hash, s);
+    else e = a.norm ? launch_token_typed<float, true>(a, hash, s) : launch_token_typed<float, false>(a, hash, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a.chosen, a.T, a.k, a.E, a.S, a.bm, a.load,
+                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off);
     return hipGetLastError();
 }
 

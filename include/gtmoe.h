@@ -219,6 +219,16 @@ int32_t gtmoe_timing_read(gtmoe_context *ctx, int32_t capacity, char *names, dou
  * than AUTO). */
 int32_t gtmoe_last_path(const gtmoe_layer *layer, int32_t *path);
 
+/* Launch one expert kernel of the last forward on this layer again, with the
+ * same arguments and workspace, on `stream` (a hipStream_t; NULL = the
+ * context's stream), without synchronising.  Bracketing a burst of these with
+ * events gives the kernel's duration free of per-launch event skew -- the
+ * per-dispatch timing of Recorder.MeasureTime (gpu/compute.go:670-694) for a
+ * single program.  kernel: GTMOE_KERNEL_GATEUP (gate/up + SwiGLU) or
+ * GTMOE_KERNEL_DOWN of the path the last forward took. */
+enum gtmoe_kernel { GTMOE_KERNEL_GATEUP = 0, GTMOE_KERNEL_DOWN = 1 };
+int32_t gtmoe_relaunch(gtmoe_layer *layer, int32_t kernel, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
