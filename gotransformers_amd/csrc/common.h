@@ -65,6 +65,7 @@ struct GemvArgs {
     const int32_t *tok;  // gate/up: token of every position; down: nullptr
     const int32_t *goff;
     const int32_t *slice_off;  // [groups+1] prefix of token slices per group
+    const int32_t *group_of;   // group of every slice
     int groups;
     int tslice;  // tokens per slice
     float *out;
@@ -94,6 +95,7 @@ struct MfmaArgs {
     const int32_t *tok;  // gate/up: gather by token; down: nullptr
     const int32_t *goff;
     const int32_t *tile_off;  // [G+1] exclusive prefix of m-tiles per group
+    const int32_t *group_of;  // group of every m-tile
     int groups;
     void *out;  // gate/up: bf16 hidden; down: fp32 slot outputs
     int ldo;
@@ -116,7 +118,7 @@ struct FusedArgs {
     int32_t *chosen;
     double *gates;
     float *gates32;
-    int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off;
+    int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off, *group_of;
 };
 
 // Launchers (each returns the hipError_t of its launch).
@@ -132,14 +134,14 @@ hipError_t launch_topk(const double *logits, int T, int E, int k, const double *
                        double *gates, float *gates32, hipStream_t s);
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,
                              float *gates32, hipStream_t s);
-bool fused_route_fits(int T, int k);
+bool fused_route_fits(int T, int k, int kp);
 hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s);
 // Dispatch: one workgroup up to 1024 tokens, else count / scan / scatter over
 // chunks of 256 tokens using chunk_cnt [dispatch_chunks(T)][E] as scratch.
 int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
                            int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
-                           int32_t *tile_off, int32_t *chunk_cnt, hipStream_t s);
+                           int32_t *tile_off, int32_t *group_of, int32_t *chunk_cnt, hipStream_t s);
 hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
 hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
 hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);

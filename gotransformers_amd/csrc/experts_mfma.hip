@@ -100,13 +100,7 @@ __global__ __launch_bounds__(256) void mfma_gemm_kernel(MfmaArgs a)
 
     const int tile = blockIdx.x;
     if (tile >= a.tile_off[a.groups]) return;
-    int lo = 0, hi = a.groups - 1;
-    while (lo < hi) {  // last group whose first tile is <= tile
-        const int mid = (lo + hi + 1) >> 1;
-        if (a.tile_off[mid] <= tile) lo = mid;
-        else hi = mid - 1;
-    }
-    const int g = lo;
+    const int g = a.group_of[tile];
     const int p0 = a.goff[g];
     const int M = a.goff[g + 1] - p0;
     const int m0 = (tile - a.tile_off[g]) * BM;

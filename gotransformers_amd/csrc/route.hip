@@ -474,7 +474,8 @@ struct DispatchShared {
 // part of tok.
 __device__ void write_group_tables(int T, int k, int E, int S, int bm, DispatchShared &sh, int32_t *__restrict__ load,
                                    int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
-                                   int32_t *__restrict__ tok, int32_t *__restrict__ tile_off)
+                                   int32_t *__restrict__ tok, int32_t *__restrict__ tile_off,
+                                   int32_t *__restrict__ group_of)
 {
     const int tid = threadIdx.x;
     const int G = S + E;
@@ -491,59 +492,82 @@ __device__ void write_group_tables(int T, int k, int E, int S, int bm, DispatchS
     if (tid == 0) goff[G] = S * T + T * k;
     __syncthreads();
     const int total_tiles = block_exclusive_scan(sh.tiles, sh.tiles, G, sh.wave_sums, &sh.total);
-    for (int g = tid; g < G; g += blockDim.x) tile_off[g] = sh.tiles[g];
+    for (int g = tid; g < G; g += blockDim.x) {
+        tile_off[g] = sh.tiles[g];
+        const int end = g + 1 < G ? sh.tiles[g + 1] : total_tiles;
+        for (int t = sh.tiles[g]; t < end; ++t) group_of[t] = g;  // tile -> group
+    }
     if (tid == 0) tile_off[G] = total_tiles;
     for (long long p = tid; p < (long long)S * T; p += blockDim.x) tok[p] = (int32_t)(p % T);
 }
 
-// Whole dispatch by one 1024-thread workgroup; `chosen` may be in LDS.
+// Whole dispatch by one 1024-thread workgroup for T <= 1024; `chosen` may be
+// in LDS.  Tokens form token-waves of 64 (lane = token); the (token-wave,
+// expert) pairs are spread over the 16 waves.  For each pair a ballot of
+// "has this expert" gives the pair's count (pass 1) and every token's rank
+// (pass 2); a per-expert prefix over token-waves in between turns counts into
+// starting positions.  No atomics, and every wave has a share of the work.
 __device__ void dispatch_block(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *__restrict__ load,
                                int32_t *__restrict__ offsets, int32_t *__restrict__ rows, int32_t *__restrict__ pos,
                                int32_t *__restrict__ goff, int32_t *__restrict__ tok,
-                               int32_t *__restrict__ tile_off, DispatchShared &sh)
+                               int32_t *__restrict__ tile_off, int32_t *__restrict__ group_of, DispatchShared &sh)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += 1024) sh.cnt[e] = 0;
+    const int ntw = (T + 63) / 64;  // token-waves, <= 16
+    int ntwp = 1;
+    while (ntwp < ntw) ntwp <<= 1;
+    const int wpt = 16 / ntwp;  // waves per token-wave
+    const int tw = wave / wpt, sub = wave % wpt;
+    const int t = tw * 64 + lane;
+    const bool active = tw < ntw;
+    int ce[kMaxK];
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i) ce[i] = (active && t < T && i < k) ? chosen[(size_t)t * k + i] : -1;
+
+    // pass 1: counts per (token-wave, expert)
+    if (active) {
+        for (int e = sub; e < E; e += wpt) {
+            bool has = false;
+#pragma unroll
+            for (int i = 0; i < kMaxK; ++i) has |= ce[i] == e;
+            const unsigned long long b = __ballot(has);
+            if (lane == 0) sh.wave_cnt[tw][e] = __popcll(b);
+        }
+    }
     __syncthreads();
-    for (long long i = tid; i < (long long)T * k; i += 1024) atomicAdd(&sh.cnt[chosen[i]], 1);
+    // per-expert totals and the prefix over token-waves
+    for (int e = tid; e < E; e += 1024) {
+        int acc = 0;
+        for (int w = 0; w < ntw; ++w) acc += sh.wave_cnt[w][e];
+        sh.cnt[e] = acc;
+    }
     __syncthreads();
     block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
-    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off);
+    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, group_of);
+    for (int e = tid; e < E; e += 1024) {
+        int acc = sh.base[e];
+        for (int w = 0; w < ntw; ++w) {
+            const int c = sh.wave_cnt[w][e];
+            sh.wave_cnt[w][e] = acc;
+            acc += c;
+        }
+    }
     __syncthreads();
-
-    for (int c0 = 0; c0 < T; c0 += 1024) {
-        const int t = c0 + tid;
-        const bool valid = t < T;
-        int ce[kMaxK], rk[kMaxK];
+    // pass 2: positions
+    if (active) {
+        for (int e = sub; e < E; e += wpt) {
+            int match = -1;
 #pragma unroll
-        for (int i = 0; i < kMaxK; ++i) {
-            ce[i] = (valid && i < k) ? chosen[(size_t)t * k + i] : -1;
-            rk[i] = 0;
-        }
-        wave_ranks(ce, rk, E, lane, wave, sh.wave_cnt);
-        __syncthreads();
-        for (int e = tid; e < E; e += 1024) {
-            int acc = sh.base[e];
-            for (int w = 0; w < 16; ++w) {
-                const int c = sh.wave_cnt[w][e];
-                sh.wave_cnt[w][e] = acc;
-                acc += c;
-            }
-            sh.base[e] = acc;
-        }
-        __syncthreads();
-        if (valid) {
-#pragma unroll
-            for (int i = 0; i < kMaxK; ++i) {
-                if (i < k) {
-                    const int p = sh.wave_cnt[wave][ce[i]] + rk[i];
-                    rows[p] = t;
-                    pos[(size_t)t * k + i] = p;
-                    tok[(size_t)S * T + p] = t;
-                }
+            for (int i = 0; i < kMaxK; ++i)
+                if (ce[i] == e) match = i;
+            const unsigned long long b = __ballot(match >= 0);
+            if (match >= 0) {
+                const int p = sh.wave_cnt[tw][e] + __popcll(b & ((1ULL << lane) - 1ULL));
+                rows[p] = t;
+                pos[(size_t)t * k + match] = p;
+                tok[(size_t)S * T + p] = t;
             }
         }
-        __syncthreads();
     }
 }
 
@@ -551,10 +575,10 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                                                         int bm, int32_t *__restrict__ load, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ rows, int32_t *__restrict__ pos,
                                                         int32_t *__restrict__ goff, int32_t *__restrict__ tok,
-                                                        int32_t *__restrict__ tile_off)
+                                                        int32_t *__restrict__ tile_off, int32_t *__restrict__ group_of)
 {
     __shared__ DispatchShared sh;
-    dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, sh);
+    dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, group_of, sh);
 }
 
 // Many tokens: chunks of 256 tokens (4 waves) per workgroup.
@@ -580,7 +604,8 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(const int32_t *_
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int T, int k, int E, int S, int bm, int chunks,
                                                              int32_t *__restrict__ chunk_cnt, int32_t *__restrict__ load,
                                                              int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
-                                                             int32_t *__restrict__ tok, int32_t *__restrict__ tile_off)
+                                                             int32_t *__restrict__ tok, int32_t *__restrict__ tile_off,
+                                                             int32_t *__restrict__ group_of)
 {
     __shared__ DispatchShared sh;
     const int tid = threadIdx.x;
@@ -592,7 +617,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int T, int k, int E
     }
     __syncthreads();
     block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
-    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off);
+    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, group_of);
     // each chunk's first position per expert
     for (int e = tid; e < E; e += 1024) {
         int acc = sh.base[e];
@@ -647,17 +672,17 @@ int dispatch_chunks(int T) { return (T + kChunk - 1) / kChunk; }
 
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load, int32_t *offsets,
                            int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok, int32_t *tile_off,
-                           int32_t *chunk_cnt, hipStream_t s)
+                           int32_t *group_of, int32_t *chunk_cnt, hipStream_t s)
 {
-    if (T <= 1024) {
+    if (T <= 1024) {  // one workgroup: token-waves x experts over its 16 waves
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows,
-                           pos, goff, tok, tile_off);
+                           pos, goff, tok, tile_off, group_of);
         return hipGetLastError();
     }
     const int chunks = dispatch_chunks(T);
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, chunk_cnt);
     hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, T, k, E, S, bm, chunks, chunk_cnt, load,
-                       offsets, goff, tok, tile_off);
+                       offsets, goff, tok, tile_off, group_of);
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, S, chunk_cnt, rows,
                        pos, tok);
     return hipGetLastError();
@@ -697,11 +722,13 @@ __device__ __forceinline__ float4 in4(const double *row, int i)
     return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
 }
 
-// One workgroup per token: the token's E logits (four waves share the
-// experts), then top-k (or hash routing) by wave 0 from LDS, and the token's
-// prepared row (converted or normalised, zero-padded) written by all threads.
-template <typename InT, bool NORM, bool HASH, int EPL>
-__global__ __launch_bounds__(256) void route_token_kernel(FusedArgs a)
+// One 1024-thread workgroup per token.  Each lane keeps its share of the
+// token's row in registers (NX float4 runs, d <= 256*NX); the 16 waves share
+// the experts, two router rows in flight at a time; logits go to LDS, then
+// wave 0 runs top-k (or hash routing) and all threads write the token's
+// prepared row (converted or normalised, zero-padded).
+template <typename InT, bool NORM, bool HASH, int EPL, int NX>
+__global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
     __shared__ double lg[kMaxExperts];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -709,48 +736,69 @@ __global__ __launch_bounds__(256) void route_token_kernel(FusedArgs a)
     const InT *xr = reinterpret_cast<const InT *>(a.x) + (size_t)t * a.d;
     const bool vec = (a.d & 3) == 0;
 
+    float4 xv[NX];
     float ss = 0.f;
-    if (NORM) {
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+        const int i = 4 * lane + 256 * j;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (vec) {
-            for (int i = 4 * lane; i < a.d; i += 256) {
-                const float4 v = in4(xr, i);
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-            }
+            if (i < a.d) v = in4(xr, i);
         } else {
-            for (int i = lane; i < a.d; i += 64) {
-                const float v = in_at(xr, i);
-                ss = fmaf(v, v, ss);
-            }
+            if (i < a.d) v.x = in_at(xr, i);
+            if (i + 1 < a.d) v.y = in_at(xr, i + 1);
+            if (i + 2 < a.d) v.z = in_at(xr, i + 2);
+            if (i + 3 < a.d) v.w = in_at(xr, i + 3);
         }
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        xv[j] = v;
+        if (NORM) {
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
     }
-    const float inv = NORM ? 1.0f / sqrtf(ss / (float)a.d + 1e-6f) : 1.0f;
+    float inv = 1.0f;
+    if (NORM) {
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        inv = 1.0f / sqrtf(ss / (float)a.d + 1e-6f);
+    }
 
     if (!HASH) {
-        for (int e = wave; e < a.E; e += 4) {
-            const float *wr = a.w + (size_t)e * a.kp;
-            float dot = 0.f;
-            if (vec) {
-#pragma unroll 4
-                for (int i = 4 * lane; i < a.d; i += 256) {
-                    const float4 v = in4(xr, i);
-                    const float4 w = *reinterpret_cast<const float4 *>(wr + i);
-                    dot = fmaf(v.x, w.x, dot);
-                    dot = fmaf(v.y, w.y, dot);
-                    dot = fmaf(v.z, w.z, dot);
-                    dot = fmaf(v.w, w.w, dot);
+        for (int e0 = wave; e0 < a.E; e0 += 32) {
+            const int e1 = e0 + 16;
+            const bool two = e1 < a.E;
+            const float *w0 = a.w + (size_t)e0 * a.kp;
+            const float *w1 = a.w + (size_t)(two ? e1 : e0) * a.kp;
+            float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < NX; ++j) {
+                const int i = 4 * lane + 256 * j;
+                if (i < a.kp) {
+                    const float4 p = *reinterpret_cast<const float4 *>(w0 + i);
+                    const float4 q = *reinterpret_cast<const float4 *>(w1 + i);
+                    d0 = fmaf(xv[j].x, p.x, d0);
+                    d0 = fmaf(xv[j].y, p.y, d0);
+                    d0 = fmaf(xv[j].z, p.z, d0);
+                    d0 = fmaf(xv[j].w, p.w, d0);
+                    d1 = fmaf(xv[j].x, q.x, d1);
+                    d1 = fmaf(xv[j].y, q.y, d1);
+                    d1 = fmaf(xv[j].z, q.z, d1);
+                    d1 = fmaf(xv[j].w, q.w, d1);
                 }
-            } else {
-                for (int i = lane; i < a.d; i += 64) dot = fmaf(in_at(xr, i), wr[i], dot);
             }
-            for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
-            if (lane == 0) lg[e] = (double)(dot * inv) + a.bias[e];
+            for (int off = 32; off > 0; off >>= 1) {
+                d0 += __shfl_xor(d0, off);
+                d1 += __shfl_xor(d1, off);
+            }
+            if (lane == 0) {
+                lg[e0] = (double)(d0 * inv) + a.bias[e0];
+                if (two) lg[e1] = (double)(d1 * inv) + a.bias[e1];
+            }
         }
     }
-    for (int i = threadIdx.x; i < a.kp; i += 256) {
+    // prepared row
+    for (int i = threadIdx.x; i < a.kp; i += 1024) {
         float v = 0.f;
         if (i < a.d) {
             v = in_at(xr, i);
@@ -769,28 +817,38 @@ __global__ __launch_bounds__(256) void route_token_kernel(FusedArgs a)
     }
 }
 
-bool fused_route_fits(int T, int k) { return T >= 1 && T * k <= kFusedMaxTK && T <= 1024; }
+bool fused_route_fits(int T, int k, int kp) { return T >= 1 && T * k <= kFusedMaxTK && T <= 1024 && kp <= 4096; }
+
+template <typename InT, bool NORM, int NX>
+static hipError_t launch_token_nx(const FusedArgs &a, bool hash, hipStream_t s)
+{
+    dim3 grid(a.T);
+    if (hash) hipLaunchKernelGGL((route_token_kernel<InT, NORM, true, 1, NX>), grid, dim3(1024), 0, s, a);
+    else if (a.E <= 64) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 1, NX>), grid, dim3(1024), 0, s, a);
+    else if (a.E <= 128) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 2, NX>), grid, dim3(1024), 0, s, a);
+    else hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 4, NX>), grid, dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
 
 template <typename InT, bool NORM>
 static hipError_t launch_token_typed(const FusedArgs &a, bool hash, hipStream_t s)
 {
-    dim3 grid(a.T);
-    if (hash) hipLaunchKernelGGL((route_token_kernel<InT, NORM, true, 1>), grid, dim3(256), 0, s, a);
-    else if (a.E <= 64) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 1>), grid, dim3(256), 0, s, a);
-    else if (a.E <= 128) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 2>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 4>), grid, dim3(256), 0, s, a);
-    return hipGetLastError();
+    if (a.kp <= 256) return launch_token_nx<InT, NORM, 1>(a, hash, s);
+    if (a.kp <= 1024) return launch_token_nx<InT, NORM, 4>(a, hash, s);
+    if (a.kp <= 2048) return launch_token_nx<InT, NORM, 8>(a, hash, s);
+    if (a.kp <= 4096) return launch_token_nx<InT, NORM, 16>(a, hash, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s)
 {
-    if (!fused_route_fits(a.T, a.k)) return hipErrorInvalidValue;
+    if (!fused_route_fits(a.T, a.k, a.kp)) return hipErrorInvalidValue;
     hipError_t e;
     if (input_f64) e = a.norm ? launch_token_typed<double, true>(a, hash, s) : launch_token_typed<double, false>(a, hash, s);
     else e = a.norm ? launch_token_typed<float, true>(a, hash, s) : launch_token_typed<float, false>(a, hash, s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a.chosen, a.T, a.k, a.E, a.S, a.bm, a.load,
-                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off);
+                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off, a.group_of);
     return hipGetLastError();
 }
 
