@@ -166,6 +166,7 @@ def main():
     prefill_like = T * c["k"] > 8 * c["E"]
     steps = args.steps or (400 if not prefill_like and c["layers"] == 1 else 30 if c["layers"] == 1 else 10)
     warmup = args.warmup if args.warmup is not None else max(3, steps // 10)
+    warmup = max(warmup, c["copies"])  # every weight copy has run a forward before the relaunch burst
 
     specs = make_specs(gt, c)
     ctx = gt.Context(0)

@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -189,6 +190,7 @@ int32_t alloc_matrix(gtmoe_context *ctx, DeviceMatrix &m, int precision, int row
 {
     m.precision = precision;
     m.rows = rows;
+    m.rows_p = pad_rows(rows);
     m.width = width;
     m.kp = pad_k(width);
     m.nblocks = m.kp / kValuesPerScale;
@@ -760,20 +762,23 @@ int32_t gtmoe_upload_rows(gtmoe_layer *L, int32_t role, int32_t index, const gtm
         return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "expert weights at precision %d, the layer holds %d",
                     rows->precision, m.precision);
     const int group = shared ? index : L->S + index;
-    // repack into padded device rows
+    // repack into the panel layout (16-byte units of 64 rows side by side)
     std::vector<uint8_t> vals(m.group_value_bytes(), 0);
     const int src_row_bytes = m.precision == kInt8 ? m.width : m.precision == kFP4 ? (m.width + 1) / 2 : m.width * 4;
-    for (int r = 0; r < m.rows; ++r)
-        memcpy(vals.data() + (size_t)r * m.row_bytes, (const uint8_t *)rows->values + (size_t)r * src_row_bytes,
-               (size_t)src_row_bytes);
+    for (int r = 0; r < m.rows; ++r) {
+        const uint8_t *src = (const uint8_t *)rows->values + (size_t)r * src_row_bytes;
+        for (int u = 0; u * 16 < src_row_bytes; ++u)
+            memcpy(vals.data() + panel_unit_offset(r, u, m.row_bytes), src + (size_t)u * 16,
+                   (size_t)std::min(16, src_row_bytes - u * 16));
+    }
     HIP_TRY(ctx, hipMemcpy((char *)m.values + (size_t)group * m.group_value_bytes(), vals.data(), vals.size(),
                            hipMemcpyHostToDevice));
     if (m.precision != kFloat32) {
         const int src_blocks = (m.width + 15) / 16;
         std::vector<float> sc(m.group_scales(), 0.f);
         for (int r = 0; r < m.rows; ++r)
-            memcpy(sc.data() + (size_t)r * m.nblocks, rows->scales + (size_t)r * src_blocks,
-                   sizeof(float) * src_blocks);
+            for (int b = 0; b < src_blocks; ++b)
+                sc[panel_scale_index(r, b, m.nblocks)] = rows->scales[(size_t)r * src_blocks + b];
         HIP_TRY(ctx, hipMemcpy(m.scales + (size_t)group * m.group_scales(), sc.data(), sc.size() * sizeof(float),
                                hipMemcpyHostToDevice));
     }

@@ -2,13 +2,18 @@
 //
 // Device data layout (all of one layer resident in HBM):
 //   expert weights of one role (gate, up or down) for all G = S + E groups
-//   (shared experts first, then routed experts) in one allocation:
-//     values [G][rows][row_bytes]   rows padded to kp = ceil(width/64)*64
-//                                   values with zeros: int8 kp bytes, FP4
-//                                   kp/2 bytes (even index in the low
-//                                   nibble), float32 4*kp bytes
-//     scales [G][rows][kp/16]       float32 per 16 values (Int8, FP4)
-//     biases [G][rows]              float32
+//   (shared experts first, then routed experts) in one allocation, rows
+//   padded to kp = ceil(width/64)*64 values (zeros) and grouped in panels of
+//   64 rows (rows padded to a multiple of 64 with zero rows):
+//     values [G][panel][unit][64 rows][16 B]   a unit is 16 bytes of one
+//                 row's codes: 16 Int8 values, 32 FP4 values (even index in
+//                 the low nibble) or 4 float32 values; row_bytes / 16 units
+//     scales [G][panel][kp/64][64 rows][4]     float32 per 16 values (Int8,
+//                 FP4): the scales of four consecutive blocks of a row are
+//                 one 16-byte group
+//     biases [G][rows]                         float32
+//   so one wave-wide 16-byte load (lane = row of a panel) reads 1 KiB of
+//   codes contiguously, and one 16-byte scale load covers four blocks.
 //   activations are fp32 (or bf16 for the MFMA path) with a row stride of
 //   ceil(d/64)*64 resp. ceil(h/64)*64, padding columns zero.
 //
@@ -28,13 +33,28 @@ enum Precision { kFloat64 = 0, kFloat32 = 1, kInt8 = 2, kFP4 = 3 };
 
 constexpr int kValuesPerScale = 16;
 constexpr int kPadK = 64;
+constexpr int kPanelRows = 64;
 
 inline int pad_k(int width) { return (width + kPadK - 1) / kPadK * kPadK; }
+inline int pad_rows(int rows) { return (rows + kPanelRows - 1) / kPanelRows * kPanelRows; }
+
+// Byte offset of 16-byte unit u of row r inside one group's codes.
+__host__ __device__ inline size_t panel_unit_offset(int r, int u, int row_bytes)
+{
+    return (size_t)(r >> 6) * 64 * (size_t)row_bytes + (size_t)u * 1024 + (size_t)(r & 63) * 16;
+}
+
+// Index of the scale of block b of row r inside one group's scales.
+__host__ __device__ inline size_t panel_scale_index(int r, int b, int nblocks)
+{
+    return (size_t)(r >> 6) * 64 * (size_t)nblocks + (size_t)(b >> 2) * 256 + (size_t)(r & 63) * 4 + (b & 3);
+}
 
 // One weight role of all groups on the device.
 struct DeviceMatrix {
     int precision = 0;
     int rows = 0;       // output neurons
+    int rows_p = 0;     // rows padded to whole panels
     int width = 0;      // inputs (unpadded)
     int kp = 0;         // padded inputs
     int row_bytes = 0;  // bytes per padded row
@@ -43,8 +63,8 @@ struct DeviceMatrix {
     void *values = nullptr;
     float *scales = nullptr;
     float *biases = nullptr;
-    size_t group_value_bytes() const { return (size_t)rows * row_bytes; }
-    size_t group_scales() const { return (size_t)rows * nblocks; }
+    size_t group_value_bytes() const { return (size_t)rows_p * row_bytes; }
+    size_t group_scales() const { return (size_t)rows_p * nblocks; }
 };
 
 // Arguments of the expert GEMV kernels (fp32 path).
@@ -58,7 +78,7 @@ struct GemvArgs {
     long long w_group_stride;  // bytes
     long long s_group_stride;  // floats
     int rows;
-    int nblocks;
+    int nblocks;  // kp / 16
     int row_bytes;
     const float *in;
     int ld_in;

@@ -1,381 +1,391 @@
-// fp32 expert kernels for few tokens per expert (decode): a dequantizing
-// GEMV that streams each weight row from HBM once per group of tokens.
+// Expert kernels for few tokens per expert (decode): a dequantizing GEMV
+// that streams each weight row from HBM once per slice of at most 8 tokens,
+// with the multiply-adds on the matrix cores at fp32-level accuracy.
 //
-// Work split: grid (ceil(rows/16), token slices of all groups); every wave
-// owns 4 consecutive output rows of one group (expert) for one slice of at
-// most 8 of its tokens.  A row's K values are covered by the 64
-// lanes in 16-value blocks -- lane l takes blocks l, l+64, ... -- so each
-// load instruction of a wave reads one contiguous run of the row (1 KiB of
-// Int8, 512 B of FP4), coalesced, together with the matching fp32 scales.
-// Per block the lane forms the 16-term partial sum of every token it holds,
-// scales it once (the reference's DotRow order, lowprecision/rows.go:
-// 207-257), and accumulates.  The per-lane partials of all (row, matrix,
-// token) values are then summed across the wave by a transposing butterfly
-// that halves the live values at every exchange.
+// Work split: grid (panels of 64 output rows, token slices of all groups);
+// a workgroup's four waves share one panel and split its K range in four.
+// Lane l of a wave owns row l of the panel, so with the panel layout of the
+// weights every 16-byte load of the wave reads 1 KiB of codes contiguously.
+//
+// Arithmetic: v_mfma_f32_4x4x4_16b_bf16 holds 16 independent 4x4x4
+// products; block b of it multiplies 4 tokens (A, broadcast from lanes 0-3)
+// by 4 k-values of rows 4b..4b+3 (B, one row per lane), so a wave computes
+// 4 tokens x 64 rows per instruction and lane l ends up holding row l's dot
+// products for the 4 tokens -- no cross-lane reduction.  Weight codes are
+// exact in bf16 (Int8 magnitudes <= 127, e2m1 values); the tokens are split
+// as x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), which represents
+// x to about 2^-17 relative, and both halves go through the MFMA with fp32
+// accumulation.  Four chained instructions cover one 16-value scale block;
+// the block sum is then scaled once into an fp32 accumulator, the order of
+// the reference's DotRow (lowprecision/rows.go:207-257).  float32 weights
+// are split the same way (three products: hi*hi, lo*hi, hi*lo) and need no
+// block scaling.
 //
 // Gate/up fuse the SwiGLU epilogue (feedforward/gatedfeedforward.go:49-57):
 // hidden = act_g(gate + b_g) * act_u(up + b_u).  Down adds its bias.
 #include "common.h"
 
-#include <utility>
-
 namespace gtmoe {
 
 namespace {
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;
+
+// Per precision: 16-byte units and scale blocks per pipeline chunk.
 template <int PREC>
-struct RawBlock;
+struct Chunk;
 template <>
-struct RawBlock<kInt8> {
-    uint4 v;
+struct Chunk<kInt8> {
+    static constexpr int U = 4, CB = 4;  // 64 values
 };
 template <>
-struct RawBlock<kFP4> {
-    uint2 v;
+struct Chunk<kFP4> {
+    static constexpr int U = 2, CB = 4;  // 64 values
 };
 template <>
-struct RawBlock<kFloat32> {
-    float4 v[4];
+struct Chunk<kFloat32> {
+    static constexpr int U = 4, CB = 1;  // 16 values
 };
 
-template <int PREC>
-__device__ __forceinline__ void load_raw(RawBlock<PREC> &r, const char *row, int b);
-template <>
-__device__ __forceinline__ void load_raw<kInt8>(RawBlock<kInt8> &r, const char *row, int b)
-{
-    r.v = *reinterpret_cast<const uint4 *>(row + (size_t)b * 16);
-}
-template <>
-__device__ __forceinline__ void load_raw<kFP4>(RawBlock<kFP4> &r, const char *row, int b)
-{
-    r.v = *reinterpret_cast<const uint2 *>(row + (size_t)b * 8);
-}
-template <>
-__device__ __forceinline__ void load_raw<kFloat32>(RawBlock<kFloat32> &r, const char *row, int b)
-{
-    const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 64);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.v[i] = p[i];
-}
-
-template <int PREC>
-__device__ __forceinline__ void zero_raw(RawBlock<PREC> &r)
-{
-    r = RawBlock<PREC>{};
-}
-
-// Codes of one block as floats (Int8 values, FP4 magnitudes with sign, or
-// the float32 weights themselves); the scale is applied by the caller.
-__device__ __forceinline__ void decode(const RawBlock<kInt8> &r, float (&w)[16])
-{
-    const uint32_t d[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[4 * i + j] = (float)(int)(int8_t)(d[i] >> (8 * j));
-}
-__device__ __forceinline__ void decode(const RawBlock<kFP4> &r, float (&w)[16])
-{
-    // e2m1 codes, even value in the low nibble; the hardware conversion
-    // with scale 1.0 yields exactly {0, .5, 1, 1.5, 2, 3, 4, 6} with sign.
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t d[2] = {r.v.x, r.v.y};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 0);
-        const f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 1);
-        const f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 2);
-        const f32x2 f3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d[i], 1.0f, 3);
-        w[8 * i + 0] = f0[0];
-        w[8 * i + 1] = f0[1];
-        w[8 * i + 2] = f1[0];
-        w[8 * i + 3] = f1[1];
-        w[8 * i + 4] = f2[0];
-        w[8 * i + 5] = f2[1];
-        w[8 * i + 6] = f3[0];
-        w[8 * i + 7] = f3[1];
-    }
-}
-__device__ __forceinline__ void decode(const RawBlock<kFloat32> &r, float (&w)[16])
-{
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        w[4 * i + 0] = r.v[i].x;
-        w[4 * i + 1] = r.v[i].y;
-        w[4 * i + 2] = r.v[i].z;
-        w[4 * i + 3] = r.v[i].w;
-    }
-}
-
-// Sum N per-lane values over the 64 lanes of a wave.  Afterwards lane l
-// holds in v[0] the total of value index l / (64 / N).
-//
-// Every exchange halves the live values: the lower lanes of a pair keep
-// values [0, half) and send [half, 2*half), the upper lanes the reverse.
-// The pair loop is expanded at compile time (index sequences) so the array
-// elements stay in registers; a runtime-indexed form lets the compiler fold
-// the per-lane choice into a register-file index, which costs a compare and
-// select per element.
-template <int I, int HALF, int OFF>
-__device__ __forceinline__ void exchange_pair(float *v, bool upper)
-{
-    const float lo = v[I], hi = v[I + HALF];
-    if constexpr (OFF == 32 || OFF == 16) {
-        // gfx950 v_permlane{32,16}_swap: lanes of the upper half of each
-        // 2*OFF group trade `lo` for their partner's `hi`; afterwards every
-        // lane's two registers hold the pair it keeps, whichever half it is in
-        const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false)
-                                 : __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
-        v[I] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    } else {
-        const float send = upper ? lo : hi;
-        const float keep = upper ? hi : lo;
-        v[I] = keep + __shfl_xor(send, OFF);
-    }
-}
-
-template <int HALF, int OFF, int... I>
-__device__ __forceinline__ void exchange_all(float *v, bool upper, std::integer_sequence<int, I...>)
-{
-    (exchange_pair<I, HALF, OFF>(v, upper), ...);
-}
-
-template <int HALF, int OFF>
-__device__ __forceinline__ void halve(float *v, int lane)
-{
-    if constexpr (HALF >= 1) {
-        exchange_all<HALF, OFF>(v, (lane & OFF) != 0, std::make_integer_sequence<int, HALF>{});
-        halve<HALF / 2, OFF / 2>(v, lane);
-    }
-}
-
-template <int N>
-__device__ __forceinline__ void wave_transpose_reduce(float (&v)[N], int lane)
-{
-    halve<N / 2, 32>(v, lane);
-    for (int off = 32 / N; off > 0; off >>= 1) v[0] += __shfl_xor(v[0], off);
-}
-
-template <int N>
-struct Log2 {
-    static constexpr int value = 1 + Log2<N / 2>::value;
+template <int PREC, int MATS>
+struct ChunkRegs {
+    uint4 c[MATS][Chunk<PREC>::U];
+    float4 s[MATS];
 };
-template <>
-struct Log2<1> {
-    static constexpr int value = 0;
-};
+
+template <int I>
+__device__ __forceinline__ uint32_t comp(const uint4 &v)
+{
+    return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
+}
+template <int I>
+__device__ __forceinline__ float compf(const float4 &v)
+{
+    return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ s16x4 as_s16x4(uint32_t lo, uint32_t hi)
+{
+    const u32x2 v = {lo, hi};
+    return __builtin_bit_cast(s16x4, v);
+}
+
+// bf16 bits of two floats that bf16 holds exactly (small integers): their
+// upper halves, packed.
+__device__ __forceinline__ uint32_t upper_halves(float lo, float hi)
+{
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+__device__ __forceinline__ uint32_t bf16_rne_pair(float lo, float hi)
+{
+    const __bf16 a = (__bf16)lo, b = (__bf16)hi;
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// x = hi + lo for two values: hi = bf16(x) rounded to nearest, lo = bf16 of
+// the (exact) remainder.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo)
+{
+    hi = bf16_rne_pair(x0, x1);
+    const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
+    lo = bf16_rne_pair(x0 - h0, x1 - h1);
+}
+
+// B operand of step S (k-values 4S..4S+3) of block J of a chunk.
+template <int J, int S>
+__device__ __forceinline__ s16x4 weights_step(const uint4 (&c)[Chunk<kInt8>::U])
+{
+    const uint32_t d = comp<S>(c[J]);
+    const float f0 = (float)(int)(int8_t)d, f1 = (float)(int)(int8_t)(d >> 8);
+    const float f2 = (float)(int)(int8_t)(d >> 16), f3 = (float)(int)(int8_t)(d >> 24);
+    return as_s16x4(upper_halves(f0, f1), upper_halves(f2, f3));
+}
+template <int J, int S>
+__device__ __forceinline__ s16x4 weights_step(const uint4 (&c)[Chunk<kFP4>::U])
+{
+    // block J is half J&1 of unit J/2; step S is bytes 2S, 2S+1 of it, and
+    // each byte holds two values, the even one in the low nibble
+    const uint32_t d = comp<(J & 1) * 2 + (S >> 1)>(c[J >> 1]);
+    const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, 1.0f, (S & 1) * 2);
+    const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, 1.0f, (S & 1) * 2 + 1);
+    return as_s16x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+template <int S>
+__device__ __forceinline__ void weights_step_f32(const uint4 (&c)[Chunk<kFloat32>::U], s16x4 &hi, s16x4 &lo)
+{
+    const uint4 v = c[S];
+    uint32_t h01, l01, h23, l23;
+    split_pair(__uint_as_float(v.x), __uint_as_float(v.y), h01, l01);
+    split_pair(__uint_as_float(v.z), __uint_as_float(v.w), h23, l23);
+    hi = as_s16x4(h01, h23);
+    lo = as_s16x4(l01, l23);
+}
+
+__device__ __forceinline__ f32x4 mfma4(s16x4 a, s16x4 b, f32x4 c)
+{
+    // CBSZ = 4, ABID = 0: block 0's A (lanes 0-3, the tokens) is used by
+    // all 16 blocks
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 4, 0, 0);
+}
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
-}  // namespace
+// The staged tokens: for every group of 8 k-values, NT tokens' bf16 hi
+// values (16 bytes each), then the same for lo.  Lane reads of one token's
+// 16 bytes for tokens 4q..4q+3 are contiguous and shared by the other lanes.
+template <int NT>
+struct Staged {
+    const uint4 *hi;
+    const uint4 *lo;
+    __device__ __forceinline__ void read(int g8, int t, uint4 &h, uint4 &l) const
+    {
+        h = hi[g8 * NT + t];
+        l = lo[g8 * NT + t];
+    }
+};
 
-// Weight blocks (and their scales) of RIF rows starting at row rb, for each
-// matrix and each of the lane's NB blocks.
-template <int PREC, int NB, int RIF, int MATS>
-__device__ __forceinline__ void load_rows(const GemvArgs &a, int rb, int lane, const char *wb0, const char *wb1,
-                                          const float *sb0, const float *sb1, RawBlock<PREC> (&raw)[RIF][MATS][NB],
-                                          float (&sc)[RIF][MATS][NB])
+template <int PREC, int MATS>
+__device__ __forceinline__ void load_chunk(ChunkRegs<PREC, MATS> &r, const char *const (&w)[MATS],
+                                           const float *const (&sc)[MATS], int ch)
+{
+    constexpr int U = Chunk<PREC>::U;
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            r.c[m][u] = *reinterpret_cast<const uint4 *>(w[m] + (size_t)(ch * U + u) * 1024);
+        if constexpr (PREC != kFloat32) r.s[m] = *reinterpret_cast<const float4 *>(sc[m] + (size_t)ch * 256);
+    }
+}
+
+// One step of one block: A operands of the NQ token quads for k-values
+// 4S..4S+3, against every matrix.
+template <int PREC, int MATS, int NQ, int J, int S>
+__device__ __forceinline__ void block_step(const ChunkRegs<PREC, MATS> &r, const uint4 (&ah)[NQ],
+                                           const uint4 (&al)[NQ], f32x4 (&blk)[MATS][NQ])
 {
 #pragma unroll
-    for (int rr = 0; rr < RIF; ++rr) {
-        const int r = rb + rr;
+    for (int q = 0; q < NQ; ++q) {
+        const s16x4 xh = (S & 1) ? as_s16x4(ah[q].z, ah[q].w) : as_s16x4(ah[q].x, ah[q].y);
+        const s16x4 xl = (S & 1) ? as_s16x4(al[q].z, al[q].w) : as_s16x4(al[q].x, al[q].y);
 #pragma unroll
-        for (int mt = 0; mt < MATS; ++mt) {
-            const char *row = (mt == 0 ? wb0 : wb1) + (size_t)r * a.row_bytes;
-            const float *srow = (mt == 0 ? sb0 : sb1) + (size_t)r * a.nblocks;
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int b = lane + 64 * j;
-                if (r < a.rows && b < a.nblocks) {
-                    load_raw<PREC>(raw[rr][mt][j], row, b);
-                    sc[rr][mt][j] = (PREC == kFloat32) ? 1.0f : srow[b];
-                } else {
-                    zero_raw<PREC>(raw[rr][mt][j]);
-                    sc[rr][mt][j] = 0.f;
-                }
+        for (int m = 0; m < MATS; ++m) {
+            if constexpr (PREC == kFloat32) {
+                s16x4 wh, wl;
+                weights_step_f32<S>(r.c[m], wh, wl);
+                blk[m][q] = mfma4(xh, wh, blk[m][q]);
+                blk[m][q] = mfma4(xl, wh, blk[m][q]);
+                blk[m][q] = mfma4(xh, wl, blk[m][q]);
+            } else {
+                const s16x4 w = weights_step<J, S>(r.c[m]);
+                blk[m][q] = mfma4(xh, w, blk[m][q]);
+                blk[m][q] = mfma4(xl, w, blk[m][q]);
             }
         }
     }
 }
 
-// Dot products of the TC held tokens with RIF loaded rows, reduced across
-// the wave, with the epilogue (SwiGLU or bias) written to the output.
-template <int PREC, int NB, int TC, int RIF, bool GATEUP>
-__device__ __forceinline__ void process_rows(const GemvArgs &a, int p0, int M, int c0, int rb, int lane,
-                                             const float (&xr)[TC][NB][16],
-                                             const RawBlock<PREC> (&raw)[RIF][GATEUP ? 2 : 1][NB],
-                                             const float (&sc)[RIF][GATEUP ? 2 : 1][NB], const float *bb0,
-                                             const float *bb1)
+template <int PREC, int MATS, int NQ, int J>
+__device__ __forceinline__ void chunk_block(const ChunkRegs<PREC, MATS> &r, const Staged<4 * NQ> &xs, int g8,
+                                            int tl, f32x4 (&acc)[MATS][NQ])
 {
-    constexpr int MATS = GATEUP ? 2 : 1;
-    constexpr int NV = RIF * MATS * TC;  // values reduced per exchange round
-    constexpr int SHIFT = 6 - Log2<NV>::value;
-    static_assert(NV <= 64, "too many values per lane");
-    float part[NV];
+    f32x4 blk[MATS][NQ];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) part[i] = 0.f;
+    for (int m = 0; m < MATS; ++m)
 #pragma unroll
-    for (int rr = 0; rr < RIF; ++rr)
+        for (int q = 0; q < NQ; ++q) blk[m][q] = PREC == kFloat32 ? acc[m][q] : f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 ah[NQ], al[NQ];
 #pragma unroll
-        for (int mt = 0; mt < MATS; ++mt)
+    for (int q = 0; q < NQ; ++q) xs.read(g8, 4 * q + tl, ah[q], al[q]);
+    block_step<PREC, MATS, NQ, J, 0>(r, ah, al, blk);
+    block_step<PREC, MATS, NQ, J, 1>(r, ah, al, blk);
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                float w[16];
-                decode(raw[rr][mt][j], w);
+    for (int q = 0; q < NQ; ++q) xs.read(g8 + 1, 4 * q + tl, ah[q], al[q]);
+    block_step<PREC, MATS, NQ, J, 2>(r, ah, al, blk);
+    block_step<PREC, MATS, NQ, J, 3>(r, ah, al, blk);
 #pragma unroll
-                for (int c = 0; c < TC; ++c) {
-                    float bs = 0.f;
+    for (int m = 0; m < MATS; ++m)
 #pragma unroll
-                    for (int q = 0; q < 16; ++q) bs = fmaf(xr[c][j][q], w[q], bs);
-                    float &acc = part[(rr * MATS + mt) * TC + c];
-                    acc = fmaf(bs, sc[rr][mt][j], acc);
-                }
+        for (int q = 0; q < NQ; ++q) {
+            if constexpr (PREC == kFloat32) {
+                acc[m][q] = blk[m][q];
+            } else {
+                const float s = compf<J>(r.s[m]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[m][q][i] = fmaf(blk[m][q][i], s, acc[m][q][i]);
             }
-    wave_transpose_reduce<NV>(part, lane);
-    const int v = lane >> SHIFT;
-    const bool writer = (lane & ((1 << SHIFT) - 1)) == 0;
-    const int c = v % TC;
-    const int m = c0 + c;
-    if (GATEUP) {
-        const float other = __shfl_xor(part[0], TC << SHIFT);
-        const int mt = (v / TC) % 2;
-        const int rr = v / (2 * TC);
-        const int r = rb + rr;
-        if (writer && mt == 0 && m < M && r < a.rows) {
-            float gv = part[0] + bb0[r];
-            float uv = other + bb1[r];
+        }
+}
+
+template <int PREC, int MATS, int NQ>
+__device__ __forceinline__ void compute_chunk(const ChunkRegs<PREC, MATS> &r, const Staged<4 * NQ> &xs, int ch,
+                                              int tl, f32x4 (&acc)[MATS][NQ])
+{
+    constexpr int CB = Chunk<PREC>::CB;
+    const int g8 = ch * CB * 2;  // groups of 8 k-values
+    chunk_block<PREC, MATS, NQ, 0>(r, xs, g8, tl, acc);
+    if constexpr (CB > 1) {
+        chunk_block<PREC, MATS, NQ, 1>(r, xs, g8 + 2, tl, acc);
+        chunk_block<PREC, MATS, NQ, 2>(r, xs, g8 + 4, tl, acc);
+        chunk_block<PREC, MATS, NQ, 3>(r, xs, g8 + 6, tl, acc);
+    }
+}
+
+// One slice of M <= 4*NQ tokens of group g against panel `panel`.
+template <int PREC, bool GATEUP, int NQ>
+__device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, int p0, int M, int panel)
+{
+    constexpr int NT = 4 * NQ;
+    constexpr int MATS = GATEUP ? 2 : 1;
+    constexpr int CB = Chunk<PREC>::CB;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kp = a.nblocks * 16;
+    const int ng8 = kp / 8;
+
+    // stage the slice's token rows as bf16 hi / lo
+    uint4 *xhi = reinterpret_cast<uint4 *>(lds);
+    uint4 *xlo = xhi + (size_t)ng8 * NT;
+    for (int idx = tid; idx < NT * ng8; idx += blockDim.x) {
+        const int t = idx / ng8, g8 = idx - t * ng8;
+        uint4 h = make_uint4(0, 0, 0, 0), l = make_uint4(0, 0, 0, 0);
+        if (t < M) {
+            const int src = GATEUP ? a.tok[p0 + t] : p0 + t;
+            const float4 *p = reinterpret_cast<const float4 *>(a.in + (size_t)src * a.ld_in) + 2 * g8;
+            const float4 v0 = p[0], v1 = p[1];
+            split_pair(v0.x, v0.y, h.x, l.x);
+            split_pair(v0.z, v0.w, h.y, l.y);
+            split_pair(v1.x, v1.y, h.z, l.z);
+            split_pair(v1.z, v1.w, h.w, l.w);
+        }
+        xhi[g8 * NT + t] = h;
+        xlo[g8 * NT + t] = l;
+    }
+    __syncthreads();
+
+    // this wave's chunks of K
+    const int nch = a.nblocks / CB;
+    const int c0 = wave * nch / kWaves, c1 = (wave + 1) * nch / kWaves;
+    const char *w[MATS];
+    const float *sc[MATS];
+    const size_t wpanel = (size_t)panel * 64 * a.row_bytes + (size_t)lane * 16;
+    const size_t spanel = (size_t)panel * 64 * a.nblocks + (size_t)lane * 4;
+    w[0] = reinterpret_cast<const char *>(a.w0) + (size_t)g * a.w_group_stride + wpanel;
+    sc[0] = PREC == kFloat32 ? nullptr : a.s0 + (size_t)g * a.s_group_stride + spanel;
+    if constexpr (GATEUP) {
+        w[1] = reinterpret_cast<const char *>(a.w1) + (size_t)g * a.w_group_stride + wpanel;
+        sc[1] = PREC == kFloat32 ? nullptr : a.s1 + (size_t)g * a.s_group_stride + spanel;
+    }
+    const Staged<NT> xs{xhi, xlo};
+    const int tl = lane & 3;
+
+    f32x4 acc[MATS][NQ];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) acc[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    ChunkRegs<PREC, MATS> r0, r1;
+    if (c0 < c1) load_chunk<PREC, MATS>(r0, w, sc, c0);
+    for (int ch = c0; ch < c1; ch += 2) {
+        if (ch + 1 < c1) load_chunk<PREC, MATS>(r1, w, sc, ch + 1);
+        compute_chunk<PREC, MATS, NQ>(r0, xs, ch, tl, acc);
+        if (ch + 1 < c1) {
+            if (ch + 2 < c1) load_chunk<PREC, MATS>(r0, w, sc, ch + 2);
+            compute_chunk<PREC, MATS, NQ>(r1, xs, ch + 1, tl, acc);
+        }
+    }
+
+    // sum the four K quarters through LDS; wave v then finishes tokens
+    // 4q + v of every quad
+    __syncthreads();  // all reads of the staged tokens are done
+    float *red = reinterpret_cast<float *>(lds);
+    auto slot = [&](int wv, int m, int q, int i) { return (((wv * MATS + m) * NQ + q) * 4 + i) * 64 + lane; };
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[slot(wave, m, q, i)] = acc[m][q][i];
+    __syncthreads();
+    const int row = panel * 64 + lane;
+    if (row >= a.rows) return;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int t = 4 * q + wave;
+        if (t >= M) continue;
+        float v[MATS];
+#pragma unroll
+        for (int m = 0; m < MATS; ++m) {
+            float s = 0.f;
+#pragma unroll
+            for (int wv = 0; wv < kWaves; ++wv) s += red[slot(wv, m, q, wave)];
+            v[m] = s;
+        }
+        float *out = a.out + (size_t)(p0 + t) * a.ld_out + row;
+        if constexpr (GATEUP) {
+            float gv = v[0] + a.b0[(size_t)g * a.rows + row];
+            float uv = v[1] + a.b1[(size_t)g * a.rows + row];
             if (a.clamp > 0.f) {
                 gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
                 uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
             }
-            a.out[(size_t)(p0 + m) * a.ld_out + r] = silu(gv) * uv;
+            *out = silu(gv) * uv;
+        } else {
+            *out = v[0] + a.b0[(size_t)g * a.rows + row];
         }
-    } else {
-        const int rr = v / TC;
-        const int r = rb + rr;
-        if (writer && m < M && r < a.rows) a.out[(size_t)(p0 + m) * a.ld_out + r] = part[0] + bb0[r];
     }
 }
 
-// One chunk of TC tokens (positions p0+c0 .. p0+c0+TC-1, those >= M masked)
-// of a group against the NIT*RIF rows of this wave.  The tokens sit in
-// registers; the rows go through RIF at a time with the weights of the next
-// RIF rows loading while the current ones are computed (two register
-// buffers), so the wave keeps loads in flight through its compute.
-template <int PREC, int NB, int TC, int RIF, int NIT, bool GATEUP>
-__device__ __forceinline__ void gemv_chunk(const GemvArgs &a, int p0, int M, int c0, int r0, int lane,
-                                           const char *wb0, const char *wb1, const float *sb0, const float *sb1,
-                                           const float *bb0, const float *bb1)
-{
-    static_assert(NIT == 1 || NIT % 2 == 0, "row steps come alone or in pairs");
-    constexpr int MATS = GATEUP ? 2 : 1;
-    RawBlock<PREC> raw0[RIF][MATS][NB], raw1[RIF][MATS][NB];
-    float sc0[RIF][MATS][NB], sc1[RIF][MATS][NB];
-    load_rows<PREC, NB, RIF, MATS>(a, r0, lane, wb0, wb1, sb0, sb1, raw0, sc0);
+}  // namespace
 
-    float xr[TC][NB][16];
-#pragma unroll
-    for (int c = 0; c < TC; ++c) {
-        const int m = c0 + c;
-        const int src = (m < M) ? (GATEUP ? a.tok[p0 + m] : p0 + m) : 0;
-        const float *xrow = a.in + (size_t)src * a.ld_in;
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int b = lane + 64 * j;
-            if (m < M && b < a.nblocks) {
-                const float4 *p = reinterpret_cast<const float4 *>(xrow + (size_t)b * 16);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 v = p[q];
-                    xr[c][j][4 * q + 0] = v.x;
-                    xr[c][j][4 * q + 1] = v.y;
-                    xr[c][j][4 * q + 2] = v.z;
-                    xr[c][j][4 * q + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) xr[c][j][q] = 0.f;
-            }
-        }
-    }
-
-    if constexpr (NIT == 1) {
-        process_rows<PREC, NB, TC, RIF, GATEUP>(a, p0, M, c0, r0, lane, xr, raw0, sc0, bb0, bb1);
-        return;
-    }
-#pragma unroll
-    for (int it = 0; it < NIT; it += 2) {
-        load_rows<PREC, NB, RIF, MATS>(a, r0 + (it + 1) * RIF, lane, wb0, wb1, sb0, sb1, raw1, sc1);
-        process_rows<PREC, NB, TC, RIF, GATEUP>(a, p0, M, c0, r0 + it * RIF, lane, xr, raw0, sc0, bb0, bb1);
-        if (it + 2 < NIT) load_rows<PREC, NB, RIF, MATS>(a, r0 + (it + 2) * RIF, lane, wb0, wb1, sb0, sb1, raw0, sc0);
-        process_rows<PREC, NB, TC, RIF, GATEUP>(a, p0, M, c0, r0 + (it + 1) * RIF, lane, xr, raw1, sc1, bb0, bb1);
-    }
-}
-
-// One wave = NIT*RIF output rows of one group over one slice of at most
-// tslice of the group's tokens (blockIdx.y enumerates the slices of all
-// groups; the dispatch wrote their prefix and the slice -> group table).
-// Inside the slice, tokens go through in chunks whose width follows the count
-// left (TCMAX, then 2, then 1), so a group with one or two tokens does no work
-// for absent ones.
-template <int PREC, int NB, int TCMAX, int RIF, int NIT, bool GATEUP>
+// blockIdx.x = panel of 64 output rows, blockIdx.y = token slice (the
+// dispatch wrote the per-group slice prefix and the slice -> group table;
+// slices past the last exit).
+template <int PREC, bool GATEUP>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
-    constexpr int RPW = NIT * RIF;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    extern __shared__ __attribute__((aligned(16))) char lds[];
     const int item = blockIdx.y;
-    if (item >= a.slice_off[a.groups]) return;
+    if (item >= a.slice_off[a.groups]) return;  // workgroup-uniform
     const int g = a.group_of[item];
-    const int r0 = (blockIdx.x * 4 + wave) * RPW;
-    if (r0 >= a.rows) return;
     const int first = (item - a.slice_off[g]) * a.tslice;
     const int p0 = a.goff[g] + first;
     const int M = min(a.goff[g + 1] - a.goff[g] - first, a.tslice);
-    if (M <= 0) return;
-
-    const char *wb0 = reinterpret_cast<const char *>(a.w0) + (size_t)g * a.w_group_stride;
-    const char *wb1 = GATEUP ? reinterpret_cast<const char *>(a.w1) + (size_t)g * a.w_group_stride : nullptr;
-    const float *sb0 = a.s0 + (size_t)g * a.s_group_stride;
-    const float *sb1 = GATEUP ? a.s1 + (size_t)g * a.s_group_stride : nullptr;
-    const float *bb0 = a.b0 + (size_t)g * a.rows;
-    const float *bb1 = GATEUP ? a.b1 + (size_t)g * a.rows : nullptr;
-
-    int c0 = 0;
-    if constexpr (TCMAX >= 4) {
-        for (; M - c0 >= 3; c0 += 4)
-            gemv_chunk<PREC, NB, 4, RIF, NIT, GATEUP>(a, p0, M, c0, r0, lane, wb0, wb1, sb0, sb1, bb0, bb1);
-    }
-    if constexpr (TCMAX >= 2) {
-        for (; M - c0 >= 2; c0 += 2)
-            gemv_chunk<PREC, NB, 2, RIF, NIT, GATEUP>(a, p0, M, c0, r0, lane, wb0, wb1, sb0, sb1, bb0, bb1);
-    }
-    for (; c0 < M; ++c0)
-        gemv_chunk<PREC, NB, 1, RIF, NIT, GATEUP>(a, p0, M, c0, r0, lane, wb0, wb1, sb0, sb1, bb0, bb1);
+    if (M <= 0) return;  // workgroup-uniform
+    if (M <= 4) run_slice<PREC, GATEUP, 1>(a, lds, g, p0, M, blockIdx.x);
+    else run_slice<PREC, GATEUP, 2>(a, lds, g, p0, M, blockIdx.x);
 }
 
 namespace {
 
-// Shapes per K width: NB blocks of 16 per lane, TCMAX tokens in registers,
-// RIF rows per pipeline step, NIT steps per wave.
+// LDS: the staged tokens (2 x 2 bytes per k-value and token) or the
+// cross-wave partial sums, whichever is larger.
+size_t gemv_lds_bytes(int nblocks, bool gateup)
+{
+    const size_t staged = (size_t)nblocks * 16 * 2 * 2 * kGemvSlice;
+    const size_t red = (size_t)kWaves * (gateup ? 2 : 1) * 2 * 4 * 64 * sizeof(float);
+    return staged > red ? staged : red;
+}
+
 template <bool GATEUP, int PREC>
 hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
 {
-    const int nb = (a.nblocks + 63) / 64;
-    constexpr bool F32 = PREC == kFloat32;
-    auto grid = [&](int rows_per_wave) {
-        return dim3((a.rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave), max_slices);
-    };
-    if (nb <= 1) {
-        if constexpr (F32) hipLaunchKernelGGL((gemv_kernel<PREC, 1, 4, 1, 4, GATEUP>), grid(4), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<PREC, 1, 4, 4, 1, GATEUP>), grid(4), dim3(256), 0, s, a);
-    } else if (nb <= 2) {
-        if constexpr (F32) hipLaunchKernelGGL((gemv_kernel<PREC, 2, 2, 1, 4, GATEUP>), grid(4), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((gemv_kernel<PREC, 2, 2, 1, 4, GATEUP>), grid(4), dim3(256), 0, s, a);
-    } else if (nb <= 4) {
-        hipLaunchKernelGGL((gemv_kernel<PREC, 4, 1, 1, 4, GATEUP>), grid(4), dim3(256), 0, s, a);
-    } else {
-        return hipErrorInvalidValue;
+    static_assert(kGemvSlice <= 8, "at most two token quads per slice");
+    if (a.nblocks % Chunk<PREC>::CB) return hipErrorInvalidValue;
+    const size_t lds = gemv_lds_bytes(a.nblocks, GATEUP);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
     }
+    const dim3 grid((a.rows + 63) / 64, max_slices);
+    hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP>), grid, dim3(64 * kWaves), lds, s, a);
     return hipGetLastError();
 }
 

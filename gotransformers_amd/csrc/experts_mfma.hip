@@ -41,22 +41,23 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
 }
 
 // Sixteen weights (one scale block) at block index b of a row, times the
-// block scale, as 16 bf16 in 8 dwords.
+// block scale, as 16 bf16 in 8 dwords.  `row` points at the row's first
+// 16-byte unit in its panel (units of a row are 1 KiB apart), `srow` at its
+// first scale group.
 template <int PREC>
 __device__ __forceinline__ void dequant16(const char *row, const float *srow, int b, uint32_t (&out)[8])
 {
     float w[16];
+    const float s = PREC == kFloat32 ? 1.0f : srow[(size_t)(b >> 2) * 256 + (b & 3)];
     if constexpr (PREC == kInt8) {
-        const uint4 q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 16);
-        const float s = srow[b];
+        const uint4 q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 1024);
         const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) w[4 * i + j] = (float)(int)(int8_t)(d[i] >> (8 * j)) * s;
     } else if constexpr (PREC == kFP4) {
-        const uint2 q = *reinterpret_cast<const uint2 *>(row + (size_t)b * 8);
-        const float s = srow[b];
+        const uint2 q = *reinterpret_cast<const uint2 *>(row + (size_t)(b >> 1) * 1024 + (b & 1) * 8);
         const uint32_t d[2] = {q.x, q.y};
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -74,10 +75,9 @@ __device__ __forceinline__ void dequant16(const char *row, const float *srow, in
             }
         }
     } else {
-        const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 64);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 v = p[i];
+            const float4 v = *reinterpret_cast<const float4 *>(row + (size_t)(4 * b + i) * 1024);
             w[4 * i + 0] = v.x;
             w[4 * i + 1] = v.y;
             w[4 * i + 2] = v.z;
@@ -119,9 +119,12 @@ __global__ __launch_bounds__(256) void mfma_gemm_kernel(MfmaArgs a)
     const int bmat = GATEUP ? (lr >= NEURONS) : 0;
     const int bn = n0 + (GATEUP ? (lr & (NEURONS - 1)) : lr);
     const bool b_ok = bn < a.n;
+    const int brw = b_ok ? bn : 0;
     const char *brow = reinterpret_cast<const char *>(bmat ? a.w1 : a.w0) + (size_t)g * a.w_group_stride +
-                       (size_t)(b_ok ? bn : 0) * a.row_bytes;
-    const float *bsrow = (bmat ? a.s1 : a.s0) + (size_t)g * a.s_group_stride + (size_t)(b_ok ? bn : 0) * a.nblocks;
+                       panel_unit_offset(brw, 0, a.row_bytes);
+    const float *bsrow = PREC == kFloat32 ? nullptr
+                                          : (bmat ? a.s1 : a.s0) + (size_t)g * a.s_group_stride +
+                                                panel_scale_index(brw, 0, a.nblocks);
 
     uint4 av[2];
     uint32_t bv[8];
