@@ -136,7 +136,7 @@ struct Workspace {
     int32_t *pos = nullptr;
     int32_t *goff = nullptr;
     int32_t *tile_off = nullptr;
-    int32_t *group_of = nullptr;  // group of every tile / slice
+    int4 *tile_desc = nullptr;    // (group, first position, positions) of every tile / slice
     int32_t *tok = nullptr;
     float *hidden32 = nullptr;    // [P][hp]
     uint16_t *hidden16 = nullptr;  // [P][hp] bf16
@@ -297,7 +297,7 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
         {(void **)&w.load, (size_t)L->E * 4},           {(void **)&w.offsets, (size_t)(L->E + 1) * 4},
         {(void **)&w.rows, TK * 4},                     {(void **)&w.pos, TK * 4},
         {(void **)&w.goff, (size_t)(L->G + 1) * 4},     {(void **)&w.tile_off, (size_t)(L->G + 1) * 4},
-        {(void **)&w.group_of, ((size_t)L->S * cap + TK) * 4 + (size_t)(L->G + 1) * 4},
+        {(void **)&w.tile_desc, ((size_t)L->S * cap + TK + L->G + 1) * sizeof(int4)},
         {(void **)&w.tok, P * 4},                       {(void **)&w.hidden32, P * L->hp * 4},
         {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
         {(void **)&w.chunk_cnt, (size_t)dispatch_chunks(cap) * L->E * 4},
@@ -393,7 +393,7 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         f.goff = w.goff;
         f.tok = w.tok;
         f.tile_off = w.tile_off;
-        f.group_of = w.group_of;
+        f.tile_desc = w.tile_desc;
         RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, s));
         return GTMOE_OK;
     }
@@ -414,7 +414,7 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
     }
     RUN(ctx, s, "dispatch",
         launch_dispatch(w.chosen, T, L->k, L->E, L->S, bm, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
-                        w.tile_off, w.group_of, w.chunk_cnt, s));
+                        w.tile_off, w.tile_desc, w.chunk_cnt, s));
     return GTMOE_OK;
 }
 
@@ -443,11 +443,8 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         a.in = w.xf;
         a.ld_in = L->dp;
         a.tok = w.tok;
-        a.goff = w.goff;
-        a.slice_off = w.tile_off;
-        a.group_of = w.group_of;
-        a.groups = L->G;
-        a.tslice = kGemvSlice;
+        a.count = w.tile_off + L->G;
+        a.desc = w.tile_desc;
         a.out = w.hidden32;
         a.ld_out = L->hp;
         a.clamp = (float)L->desc.clamp_limit;
@@ -467,11 +464,8 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         b.in = w.hidden32;
         b.ld_in = L->hp;
         b.tok = nullptr;
-        b.goff = w.goff;
-        b.slice_off = w.tile_off;
-        b.group_of = w.group_of;
-        b.groups = L->G;
-        b.tslice = kGemvSlice;
+        b.count = w.tile_off + L->G;
+        b.desc = w.tile_desc;
         b.out = w.slot_out;
         b.ld_out = L->d;
         L->last_gemv[1] = b;
@@ -493,10 +487,8 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         a.a = w.xb;
         a.lda = L->dp;
         a.tok = w.tok;
-        a.goff = w.goff;
-        a.tile_off = w.tile_off;
-        a.group_of = w.group_of;
-        a.groups = L->G;
+        a.count = w.tile_off + L->G;
+        a.desc = w.tile_desc;
         a.out = w.hidden16;
         a.ldo = L->hp;
         a.clamp = (float)L->desc.clamp_limit;
@@ -517,10 +509,8 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         b.a = w.hidden16;
         b.lda = L->hp;
         b.tok = nullptr;
-        b.goff = w.goff;
-        b.tile_off = w.tile_off;
-        b.group_of = w.group_of;
-        b.groups = L->G;
+        b.count = w.tile_off + L->G;
+        b.desc = w.tile_desc;
         b.out = w.slot_out;
         b.ldo = L->d;
         L->last_mfma[1] = b;
@@ -980,7 +970,7 @@ int32_t gtmoe_route_from_logits(gtmoe_layer *L, int32_t tokens, const double *lo
     }
     RUN(ctx, s, "dispatch",
         launch_dispatch(w.chosen, T, L->k, L->E, L->S, mfma_tile_m(), w.load, w.offsets, w.rows, w.pos, w.goff,
-                        w.tok, w.tile_off, w.group_of, w.chunk_cnt, s));
+                        w.tok, w.tile_off, w.tile_desc, w.chunk_cnt, s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
     mark_forward(L, T, L->last_path, s);
     L->relaunch_ready = false;

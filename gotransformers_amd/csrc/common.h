@@ -82,12 +82,9 @@ struct GemvArgs {
     int row_bytes;
     const float *in;
     int ld_in;
-    const int32_t *tok;  // gate/up: token of every position; down: nullptr
-    const int32_t *goff;
-    const int32_t *slice_off;  // [groups+1] prefix of token slices per group
-    const int32_t *group_of;   // group of every slice
-    int groups;
-    int tslice;  // tokens per slice
+    const int32_t *tok;     // gate/up: token of every position; down: nullptr
+    const int32_t *count;   // number of token slices (the rest of the grid exits)
+    const int4 *desc;       // per slice: group, first position, positions, 0
     float *out;
     int ld_out;
     float clamp;
@@ -112,11 +109,9 @@ struct MfmaArgs {
     int nblocks;
     const uint16_t *a;  // bf16 activations
     int lda;
-    const int32_t *tok;  // gate/up: gather by token; down: nullptr
-    const int32_t *goff;
-    const int32_t *tile_off;  // [G+1] exclusive prefix of m-tiles per group
-    const int32_t *group_of;  // group of every m-tile
-    int groups;
+    const int32_t *tok;    // gate/up: gather by token; down: nullptr
+    const int32_t *count;  // number of m-tiles (the rest of the grid exits)
+    const int4 *desc;      // per m-tile: group, first position, positions, 0
     void *out;  // gate/up: bf16 hidden; down: fp32 slot outputs
     int ldo;
     float clamp;
@@ -138,7 +133,8 @@ struct FusedArgs {
     int32_t *chosen;
     double *gates;
     float *gates32;
-    int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off, *group_of;
+    int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off;
+    int4 *tile_desc;
 };
 
 // Launchers (each returns the hipError_t of its launch).
@@ -161,7 +157,7 @@ hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hip
 int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
                            int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
-                           int32_t *tile_off, int32_t *group_of, int32_t *chunk_cnt, hipStream_t s);
+                           int32_t *tile_off, int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s);
 hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
 hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
 hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);

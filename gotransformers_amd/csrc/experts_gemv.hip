@@ -3,7 +3,8 @@
 // with the multiply-adds on the matrix cores at fp32-level accuracy.
 //
 // Work split: grid (panels of 64 output rows, token slices of all groups);
-// a workgroup's four waves share one panel and split its K range in four.
+// a workgroup's NW waves share one panel and split its K range between them
+// (NW = 4 or 8).
 // Lane l of a wave owns row l of the panel, so with the panel layout of the
 // weights every 16-byte load of the wave reads 1 KiB of codes contiguously.
 //
@@ -33,18 +34,16 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;
-
 // Per precision: 16-byte units and scale blocks per pipeline chunk.
 template <int PREC>
 struct Chunk;
 template <>
 struct Chunk<kInt8> {
-    static constexpr int U = 4, CB = 4;  // 64 values
+    static constexpr int U = 2, CB = 2;  // 32 values
 };
 template <>
 struct Chunk<kFP4> {
-    static constexpr int U = 2, CB = 4;  // 64 values
+    static constexpr int U = 1, CB = 2;  // 32 values
 };
 template <>
 struct Chunk<kFloat32> {
@@ -54,16 +53,19 @@ struct Chunk<kFloat32> {
 template <int PREC, int MATS>
 struct ChunkRegs {
     uint4 c[MATS][Chunk<PREC>::U];
-    float4 s[MATS];
+    float s[MATS][Chunk<PREC>::CB];
 };
+
+// Chunks in flight per wave (register ring): about 4 KiB of codes per wave
+// (measured best; deeper rings lose more to occupancy than they gain).
+template <int PREC, int MATS>
+constexpr int ring_depth()
+{
+    return Chunk<PREC>::U * MATS >= 4 ? 1 : 2;
+}
 
 template <int I>
 __device__ __forceinline__ uint32_t comp(const uint4 &v)
-{
-    return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
-}
-template <int I>
-__device__ __forceinline__ float compf(const float4 &v)
 {
     return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
 }
@@ -97,23 +99,22 @@ __device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uin
 }
 
 // B operand of step S (k-values 4S..4S+3) of block J of a chunk.
-template <int J, int S>
-__device__ __forceinline__ s16x4 weights_step(const uint4 (&c)[Chunk<kInt8>::U])
+template <int PREC, int J, int S>
+__device__ __forceinline__ s16x4 weights_step(const uint4 (&c)[Chunk<PREC>::U])
 {
-    const uint32_t d = comp<S>(c[J]);
-    const float f0 = (float)(int)(int8_t)d, f1 = (float)(int)(int8_t)(d >> 8);
-    const float f2 = (float)(int)(int8_t)(d >> 16), f3 = (float)(int)(int8_t)(d >> 24);
-    return as_s16x4(upper_halves(f0, f1), upper_halves(f2, f3));
-}
-template <int J, int S>
-__device__ __forceinline__ s16x4 weights_step(const uint4 (&c)[Chunk<kFP4>::U])
-{
-    // block J is half J&1 of unit J/2; step S is bytes 2S, 2S+1 of it, and
-    // each byte holds two values, the even one in the low nibble
-    const uint32_t d = comp<(J & 1) * 2 + (S >> 1)>(c[J >> 1]);
-    const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, 1.0f, (S & 1) * 2);
-    const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, 1.0f, (S & 1) * 2 + 1);
-    return as_s16x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+    if constexpr (PREC == kInt8) {
+        const uint32_t d = comp<S>(c[J]);
+        const float f0 = (float)(int)(int8_t)d, f1 = (float)(int)(int8_t)(d >> 8);
+        const float f2 = (float)(int)(int8_t)(d >> 16), f3 = (float)(int)(int8_t)(d >> 24);
+        return as_s16x4(upper_halves(f0, f1), upper_halves(f2, f3));
+    } else {
+        // FP4: block J is half J&1 of unit J/2; step S is bytes 2S, 2S+1 of
+        // it, and each byte holds two values, the even one in the low nibble
+        const uint32_t d = comp<(J & 1) * 2 + (S >> 1)>(c[J >> 1]);
+        const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, 1.0f, (S & 1) * 2);
+        const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, 1.0f, (S & 1) * 2 + 1);
+        return as_s16x4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+    }
 }
 template <int S>
 __device__ __forceinline__ void weights_step_f32(const uint4 (&c)[Chunk<kFloat32>::U], s16x4 &hi, s16x4 &lo)
@@ -149,17 +150,36 @@ struct Staged {
     }
 };
 
+// Codes (and scales) of chunk ch of the lane's row, for every matrix.  A
+// chunk of CB blocks starts at block ch*CB; its scales are CB consecutive
+// floats of the row's 4-block scale group.
 template <int PREC, int MATS>
 __device__ __forceinline__ void load_chunk(ChunkRegs<PREC, MATS> &r, const char *const (&w)[MATS],
                                            const float *const (&sc)[MATS], int ch)
 {
-    constexpr int U = Chunk<PREC>::U;
+    constexpr int U = Chunk<PREC>::U, CB = Chunk<PREC>::CB;
 #pragma unroll
     for (int m = 0; m < MATS; ++m) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
             r.c[m][u] = *reinterpret_cast<const uint4 *>(w[m] + (size_t)(ch * U + u) * 1024);
-        if constexpr (PREC != kFloat32) r.s[m] = *reinterpret_cast<const float4 *>(sc[m] + (size_t)ch * 256);
+        if constexpr (PREC != kFloat32) {
+            const int b = ch * CB;
+            const float *p = sc[m] + (size_t)(b >> 2) * 256 + (b & 3);
+            if constexpr (CB == 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(p);
+                r.s[m][0] = v.x;
+                r.s[m][1] = v.y;
+                r.s[m][2] = v.z;
+                r.s[m][3] = v.w;
+            } else if constexpr (CB == 2) {
+                const float2 v = *reinterpret_cast<const float2 *>(p);
+                r.s[m][0] = v.x;
+                r.s[m][1] = v.y;
+            } else {
+                r.s[m][0] = *p;
+            }
+        }
     }
 }
 
@@ -182,7 +202,7 @@ __device__ __forceinline__ void block_step(const ChunkRegs<PREC, MATS> &r, const
                 blk[m][q] = mfma4(xl, wh, blk[m][q]);
                 blk[m][q] = mfma4(xh, wl, blk[m][q]);
             } else {
-                const s16x4 w = weights_step<J, S>(r.c[m]);
+                const s16x4 w = weights_step<PREC, J, S>(r.c[m]);
                 blk[m][q] = mfma4(xh, w, blk[m][q]);
                 blk[m][q] = mfma4(xl, w, blk[m][q]);
             }
@@ -215,7 +235,7 @@ __device__ __forceinline__ void chunk_block(const ChunkRegs<PREC, MATS> &r, cons
             if constexpr (PREC == kFloat32) {
                 acc[m][q] = blk[m][q];
             } else {
-                const float s = compf<J>(r.s[m]);
+                const float s = r.s[m][J];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[m][q][i] = fmaf(blk[m][q][i], s, acc[m][q][i]);
             }
@@ -229,15 +249,15 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<PREC, MATS> &r, co
     constexpr int CB = Chunk<PREC>::CB;
     const int g8 = ch * CB * 2;  // groups of 8 k-values
     chunk_block<PREC, MATS, NQ, 0>(r, xs, g8, tl, acc);
-    if constexpr (CB > 1) {
-        chunk_block<PREC, MATS, NQ, 1>(r, xs, g8 + 2, tl, acc);
+    if constexpr (CB > 1) chunk_block<PREC, MATS, NQ, 1>(r, xs, g8 + 2, tl, acc);
+    if constexpr (CB > 2) {
         chunk_block<PREC, MATS, NQ, 2>(r, xs, g8 + 4, tl, acc);
         chunk_block<PREC, MATS, NQ, 3>(r, xs, g8 + 6, tl, acc);
     }
 }
 
 // One slice of M <= 4*NQ tokens of group g against panel `panel`.
-template <int PREC, bool GATEUP, int NQ>
+template <int PREC, bool GATEUP, int NW, int NQ>
 __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, int p0, int M, int panel)
 {
     constexpr int NT = 4 * NQ;
@@ -246,6 +266,31 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kp = a.nblocks * 16;
     const int ng8 = kp / 8;
+
+    // this wave's chunks of K; the first chunks' loads (and the epilogue's
+    // biases) are issued before the token rows are staged
+    const int nch = a.nblocks / CB;
+    const int c0 = wave * nch / NW, c1 = (wave + 1) * nch / NW;
+    const char *w[MATS];
+    const float *sc[MATS];
+    const size_t wpanel = (size_t)panel * 64 * a.row_bytes + (size_t)lane * 16;
+    const size_t spanel = (size_t)panel * 64 * a.nblocks + (size_t)lane * 4;
+    w[0] = reinterpret_cast<const char *>(a.w0) + (size_t)g * a.w_group_stride + wpanel;
+    sc[0] = PREC == kFloat32 ? nullptr : a.s0 + (size_t)g * a.s_group_stride + spanel;
+    if constexpr (GATEUP) {
+        w[1] = reinterpret_cast<const char *>(a.w1) + (size_t)g * a.w_group_stride + wpanel;
+        sc[1] = PREC == kFloat32 ? nullptr : a.s1 + (size_t)g * a.s_group_stride + spanel;
+    }
+    constexpr int kDepth = ring_depth<PREC, MATS>();
+    ChunkRegs<PREC, MATS> r[kDepth];
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i)
+        if (c0 + i < c1) load_chunk<PREC, MATS>(r[i], w, sc, c0 + i);
+    const int row = panel * 64 + lane;
+    const bool writer = wave < 4 && row < a.rows;
+    float bias[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) bias[m] = writer ? (m == 0 ? a.b0 : a.b1)[(size_t)g * a.rows + row] : 0.f;
 
     // stage the slice's token rows as bf16 hi / lo
     uint4 *xhi = reinterpret_cast<uint4 *>(lds);
@@ -267,19 +312,6 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
     }
     __syncthreads();
 
-    // this wave's chunks of K
-    const int nch = a.nblocks / CB;
-    const int c0 = wave * nch / kWaves, c1 = (wave + 1) * nch / kWaves;
-    const char *w[MATS];
-    const float *sc[MATS];
-    const size_t wpanel = (size_t)panel * 64 * a.row_bytes + (size_t)lane * 16;
-    const size_t spanel = (size_t)panel * 64 * a.nblocks + (size_t)lane * 4;
-    w[0] = reinterpret_cast<const char *>(a.w0) + (size_t)g * a.w_group_stride + wpanel;
-    sc[0] = PREC == kFloat32 ? nullptr : a.s0 + (size_t)g * a.s_group_stride + spanel;
-    if constexpr (GATEUP) {
-        w[1] = reinterpret_cast<const char *>(a.w1) + (size_t)g * a.w_group_stride + wpanel;
-        sc[1] = PREC == kFloat32 ? nullptr : a.s1 + (size_t)g * a.s_group_stride + spanel;
-    }
     const Staged<NT> xs{xhi, xlo};
     const int tl = lane & 3;
 
@@ -289,19 +321,20 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
 #pragma unroll
         for (int q = 0; q < NQ; ++q) acc[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    ChunkRegs<PREC, MATS> r0, r1;
-    if (c0 < c1) load_chunk<PREC, MATS>(r0, w, sc, c0);
-    for (int ch = c0; ch < c1; ch += 2) {
-        if (ch + 1 < c1) load_chunk<PREC, MATS>(r1, w, sc, ch + 1);
-        compute_chunk<PREC, MATS, NQ>(r0, xs, ch, tl, acc);
-        if (ch + 1 < c1) {
-            if (ch + 2 < c1) load_chunk<PREC, MATS>(r0, w, sc, ch + 2);
-            compute_chunk<PREC, MATS, NQ>(r1, xs, ch + 1, tl, acc);
+    // ring of kDepth chunk buffers: once chunk ch is computed, its buffer
+    // takes chunk ch + kDepth
+    for (int ch = c0; ch < c1; ch += kDepth) {
+#pragma unroll
+        for (int j = 0; j < kDepth; ++j) {
+            if (ch + j < c1) {
+                compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
+                if (ch + j + kDepth < c1) load_chunk<PREC, MATS>(r[j], w, sc, ch + j + kDepth);
+            }
         }
     }
 
-    // sum the four K quarters through LDS; wave v then finishes tokens
-    // 4q + v of every quad
+    // sum the NW partial K ranges through LDS; wave v < 4 then finishes
+    // tokens 4q + v of every quad
     __syncthreads();  // all reads of the staged tokens are done
     float *red = reinterpret_cast<float *>(lds);
     auto slot = [&](int wv, int m, int q, int i) { return (((wv * MATS + m) * NQ + q) * 4 + i) * 64 + lane; };
@@ -312,8 +345,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
 #pragma unroll
             for (int i = 0; i < 4; ++i) red[slot(wave, m, q, i)] = acc[m][q][i];
     __syncthreads();
-    const int row = panel * 64 + lane;
-    if (row >= a.rows) return;
+    if (!writer) return;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         const int t = 4 * q + wave;
@@ -323,20 +355,20 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
         for (int m = 0; m < MATS; ++m) {
             float s = 0.f;
 #pragma unroll
-            for (int wv = 0; wv < kWaves; ++wv) s += red[slot(wv, m, q, wave)];
+            for (int wv = 0; wv < NW; ++wv) s += red[slot(wv, m, q, wave)];
             v[m] = s;
         }
         float *out = a.out + (size_t)(p0 + t) * a.ld_out + row;
         if constexpr (GATEUP) {
-            float gv = v[0] + a.b0[(size_t)g * a.rows + row];
-            float uv = v[1] + a.b1[(size_t)g * a.rows + row];
+            float gv = v[0] + bias[0];
+            float uv = v[1] + bias[MATS - 1];
             if (a.clamp > 0.f) {
                 gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
                 uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
             }
             *out = silu(gv) * uv;
         } else {
-            *out = v[0] + a.b0[(size_t)g * a.rows + row];
+            *out = v[0] + bias[0];
         }
     }
 }
@@ -344,32 +376,55 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
 }  // namespace
 
 // blockIdx.x = panel of 64 output rows, blockIdx.y = token slice (the
-// dispatch wrote the per-group slice prefix and the slice -> group table;
-// slices past the last exit).
-template <int PREC, bool GATEUP>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
+// dispatch wrote the slice count and a (group, first position, positions)
+// descriptor per slice; slices past the last exit).
+template <int PREC, bool GATEUP, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int item = blockIdx.y;
-    if (item >= a.slice_off[a.groups]) return;  // workgroup-uniform
-    const int g = a.group_of[item];
-    const int first = (item - a.slice_off[g]) * a.tslice;
-    const int p0 = a.goff[g] + first;
-    const int M = min(a.goff[g + 1] - a.goff[g] - first, a.tslice);
+    const int nslices = *a.count;
+    const int4 dsc = a.desc[item];  // in bounds for every slice of the grid
+    if (item >= nslices) return;    // workgroup-uniform
+    const int g = dsc.x, p0 = dsc.y, M = dsc.z;
     if (M <= 0) return;  // workgroup-uniform
-    if (M <= 4) run_slice<PREC, GATEUP, 1>(a, lds, g, p0, M, blockIdx.x);
-    else run_slice<PREC, GATEUP, 2>(a, lds, g, p0, M, blockIdx.x);
+    if (M <= 4) run_slice<PREC, GATEUP, NW, 1>(a, lds, g, p0, M, blockIdx.x);
+    else run_slice<PREC, GATEUP, NW, 2>(a, lds, g, p0, M, blockIdx.x);
 }
 
 namespace {
 
 // LDS: the staged tokens (2 x 2 bytes per k-value and token) or the
 // cross-wave partial sums, whichever is larger.
-size_t gemv_lds_bytes(int nblocks, bool gateup)
+size_t gemv_lds_bytes(int nblocks, bool gateup, int nw)
 {
     const size_t staged = (size_t)nblocks * 16 * 2 * 2 * kGemvSlice;
-    const size_t red = (size_t)kWaves * (gateup ? 2 : 1) * 2 * 4 * 64 * sizeof(float);
+    const size_t red = (size_t)nw * (gateup ? 2 : 1) * 2 * 4 * 64 * sizeof(float);
     return staged > red ? staged : red;
+}
+
+template <int PREC, bool GATEUP, int NW>
+hipError_t launch_nw(const GemvArgs &a, int max_slices, hipStream_t s)
+{
+    const size_t lds = gemv_lds_bytes(a.nblocks, GATEUP, NW);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const dim3 grid((a.rows + 63) / 64, max_slices);
+    hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW>), grid, dim3(64 * NW), lds, s, a);
+    return hipGetLastError();
+}
+
+// Waves per workgroup: eight when K holds at least two chunks per wave,
+// else four (the epilogue's waves).
+template <int PREC>
+int waves_for(const GemvArgs &a)
+{
+    const int nch = a.nblocks / Chunk<PREC>::CB;
+    return nch >= 16 ? 8 : 4;
 }
 
 template <bool GATEUP, int PREC>
@@ -377,16 +432,8 @@ hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
 {
     static_assert(kGemvSlice <= 8, "at most two token quads per slice");
     if (a.nblocks % Chunk<PREC>::CB) return hipErrorInvalidValue;
-    const size_t lds = gemv_lds_bytes(a.nblocks, GATEUP);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
-    if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    const dim3 grid((a.rows + 63) / 64, max_slices);
-    hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP>), grid, dim3(64 * kWaves), lds, s, a);
-    return hipGetLastError();
+    if (waves_for<PREC>(a) == 8) return launch_nw<PREC, GATEUP, 8>(a, max_slices, s);
+    return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
 }
 
 template <bool GATEUP>

@@ -16,9 +16,10 @@
 // scale blocks) through double-buffered LDS; global loads of the next step
 // are in flight during the MFMAs of the current one.
 //
-// Tiles: blockIdx.x enumerates the m-tiles of all groups (tile_off is the
-// per-group prefix computed by the dispatch kernel; blocks past the last
-// tile exit), blockIdx.y the column tiles.
+// Tiles: blockIdx.x enumerates the m-tiles of all groups (the dispatch
+// kernel wrote their count and a (group, first position, positions)
+// descriptor per tile; blocks past the last tile exit), blockIdx.y the
+// column tiles.
 #include "common.h"
 
 namespace gtmoe {
@@ -99,11 +100,13 @@ __global__ __launch_bounds__(256) void mfma_gemm_kernel(MfmaArgs a)
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BC][LDSK];
 
     const int tile = blockIdx.x;
-    if (tile >= a.tile_off[a.groups]) return;
-    const int g = a.group_of[tile];
-    const int p0 = a.goff[g];
-    const int M = a.goff[g + 1] - p0;
-    const int m0 = (tile - a.tile_off[g]) * BM;
+    const int ntiles = *a.count;
+    const int4 dsc = a.desc[tile];  // in bounds for every tile of the grid
+    if (tile >= ntiles) return;
+    const int g = dsc.x;
+    const int p0 = dsc.y;  // first position of the tile
+    const int M = dsc.z;   // positions in the tile
+    constexpr int m0 = 0;
     constexpr int NEURONS = GATEUP ? BC / 2 : BC;  // output neurons per tile
     const int n0 = blockIdx.y * NEURONS;
 

@@ -171,46 +171,56 @@ __global__ __launch_bounds__(256) void router_small_kernel(const float *__restri
     if (lane == 0) logits[(size_t)t * E + e] = (double)acc + bias[e];
 }
 
-// Many tokens: 64 tokens x 64 experts per workgroup, K staged through LDS in
-// steps of 32, 4x4 outputs per thread.
-__global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ x, int ldx, int T, int d,
-                                                           const float *__restrict__ w, int ldw,
-                                                           const double *__restrict__ bias, int E,
-                                                           double *__restrict__ logits)
+// Many tokens: fp32 matrix cores.  A workgroup computes 32 tokens x 32
+// experts with v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation);
+// its four waves take a quarter of K each and add their partial tiles
+// through LDS.  Lane l supplies row l%32 (token resp. expert) at k-offset
+// 8*(l/32) + s of every 16-value step for the 8 chained instructions s, so a
+// lane's operands are two float4 loads per step.  Rows past T or E read the
+// last valid row and are not written.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ x, int ldx, int T, int kp,
+                                                          const float *__restrict__ w, int ldw,
+                                                          const double *__restrict__ bias, int E,
+                                                          double *__restrict__ logits)
 {
-    __shared__ float xs[32][65];
-    __shared__ float ws[32][65];
-    const int t0 = blockIdx.y * 64, e0 = blockIdx.x * 64;
-    const int tid = threadIdx.x;
-    const int tx = tid & 15, ty = tid >> 4;  // 16 x 16 threads
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < d; k0 += 32) {
-        // 64 rows x 32 values of x and w: 2048 each, 8 per thread
-        for (int i = 0; i < 8; ++i) {
-            int idx = tid + i * 256;
-            int r = idx >> 5, c = idx & 31;
-            int t = t0 + r, e = e0 + r, kk = k0 + c;
-            xs[c][r] = (t < T && kk < d) ? x[(size_t)t * ldx + kk] : 0.f;
-            ws[c][r] = (e < E && kk < d) ? w[(size_t)e * ldw + kk] : 0.f;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < 32; ++kk) {
-            float xv[4], wv[4];
-            for (int i = 0; i < 4; ++i) xv[i] = xs[kk][ty + 16 * i];
-            for (int j = 0; j < 4; ++j) wv[j] = ws[kk][tx + 16 * j];
-            for (int i = 0; i < 4; ++i)
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
-        }
-        __syncthreads();
+    __shared__ float red[4][16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
+    const int r = lane & 31, h = lane >> 5;
+    const float *xr = x + (size_t)min(t0 + r, T - 1) * ldx + 8 * h;
+    const float *wr = w + (size_t)min(e0 + r, E - 1) * ldw + 8 * h;
+    const int n16 = kp / 16;
+    const int k0 = wave * n16 / 4, k1 = (wave + 1) * n16 / 4;
+    floatx16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    for (int kb = k0; kb < k1; ++kb) {
+        const float4 xa = *reinterpret_cast<const float4 *>(xr + kb * 16);
+        const float4 xb = *reinterpret_cast<const float4 *>(xr + kb * 16 + 4);
+        const float4 wa = *reinterpret_cast<const float4 *>(wr + kb * 16);
+        const float4 wb = *reinterpret_cast<const float4 *>(wr + kb * 16 + 4);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, wa.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, wa.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.z, wa.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.w, wa.w, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.x, wb.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.y, wb.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.z, wb.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.w, wb.w, acc, 0, 0, 0);
     }
-    for (int i = 0; i < 4; ++i) {
-        int t = t0 + ty + 16 * i;
-        if (t >= T) continue;
-        for (int j = 0; j < 4; ++j) {
-            int e = e0 + tx + 16 * j;
-            if (e < E) logits[(size_t)t * E + e] = (double)acc[i][j] + bias[e];
-        }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    // accumulator register i of lane l is token row 8*(i/4) + 4*(l/32) + i%4,
+    // expert column l%32; wave v finishes registers 4v..4v+3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 4 * wave + j;
+        const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), e = e0 + r;
+        const float v = red[0][i][lane] + red[1][i][lane] + red[2][i][lane] + red[3][i][lane];
+        if (t < T && e < E) logits[(size_t)t * E + e] = (double)v + bias[e];
     }
 }
 
@@ -224,8 +234,9 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
         dim3 grid((T * E + 3) / 4);
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits);
     } else {
-        dim3 grid((E + 63) / 64, (T + 63) / 64);
-        hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, x, ldx, T, d, w, ldw, bias, E, logits);
+        const int kp = (d + 63) / 64 * 64;
+        dim3 grid((T + 31) / 32, (E + 31) / 32);
+        hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits);
     }
     return hipGetLastError();
 }
@@ -475,7 +486,7 @@ struct DispatchShared {
 __device__ void write_group_tables(int T, int k, int E, int S, int bm, DispatchShared &sh, int32_t *__restrict__ load,
                                    int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
                                    int32_t *__restrict__ tok, int32_t *__restrict__ tile_off,
-                                   int32_t *__restrict__ group_of)
+                                   int4 *__restrict__ tile_desc)
 {
     const int tid = threadIdx.x;
     const int G = S + E;
@@ -495,7 +506,13 @@ __device__ void write_group_tables(int T, int k, int E, int S, int bm, DispatchS
     for (int g = tid; g < G; g += blockDim.x) {
         tile_off[g] = sh.tiles[g];
         const int end = g + 1 < G ? sh.tiles[g + 1] : total_tiles;
-        for (int t = sh.tiles[g]; t < end; ++t) group_of[t] = g;  // tile -> group
+        const int m = g < S ? T : sh.cnt[g - S];
+        const int p = g < S ? g * T : S * T + sh.base[g - S];
+        for (int t = sh.tiles[g]; t < end; ++t) {
+            // tile -> (group, first position, positions)
+            const int first = (t - sh.tiles[g]) * bm;
+            tile_desc[t] = make_int4(g, p + first, min(bm, m - first), 0);
+        }
     }
     if (tid == 0) tile_off[G] = total_tiles;
     for (long long p = tid; p < (long long)S * T; p += blockDim.x) tok[p] = (int32_t)(p % T);
@@ -510,7 +527,7 @@ __device__ void write_group_tables(int T, int k, int E, int S, int bm, DispatchS
 __device__ void dispatch_block(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *__restrict__ load,
                                int32_t *__restrict__ offsets, int32_t *__restrict__ rows, int32_t *__restrict__ pos,
                                int32_t *__restrict__ goff, int32_t *__restrict__ tok,
-                               int32_t *__restrict__ tile_off, int32_t *__restrict__ group_of, DispatchShared &sh)
+                               int32_t *__restrict__ tile_off, int4 *__restrict__ tile_desc, DispatchShared &sh)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ntw = (T + 63) / 64;  // token-waves, <= 16
@@ -543,7 +560,7 @@ __device__ void dispatch_block(const int32_t *chosen, int T, int k, int E, int S
     }
     __syncthreads();
     block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
-    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, group_of);
+    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, tile_desc);
     for (int e = tid; e < E; e += 1024) {
         int acc = sh.base[e];
         for (int w = 0; w < ntw; ++w) {
@@ -575,10 +592,10 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                                                         int bm, int32_t *__restrict__ load, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ rows, int32_t *__restrict__ pos,
                                                         int32_t *__restrict__ goff, int32_t *__restrict__ tok,
-                                                        int32_t *__restrict__ tile_off, int32_t *__restrict__ group_of)
+                                                        int32_t *__restrict__ tile_off, int4 *__restrict__ tile_desc)
 {
     __shared__ DispatchShared sh;
-    dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, group_of, sh);
+    dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, tile_desc, sh);
 }
 
 // Many tokens: chunks of 256 tokens (4 waves) per workgroup.
@@ -605,7 +622,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int T, int k, int E
                                                              int32_t *__restrict__ chunk_cnt, int32_t *__restrict__ load,
                                                              int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
                                                              int32_t *__restrict__ tok, int32_t *__restrict__ tile_off,
-                                                             int32_t *__restrict__ group_of)
+                                                             int4 *__restrict__ tile_desc)
 {
     __shared__ DispatchShared sh;
     const int tid = threadIdx.x;
@@ -617,7 +634,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int T, int k, int E
     }
     __syncthreads();
     block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
-    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, group_of);
+    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, tile_desc);
     // each chunk's first position per expert
     for (int e = tid; e < E; e += 1024) {
         int acc = sh.base[e];
@@ -672,17 +689,17 @@ int dispatch_chunks(int T) { return (T + kChunk - 1) / kChunk; }
 
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load, int32_t *offsets,
                            int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok, int32_t *tile_off,
-                           int32_t *group_of, int32_t *chunk_cnt, hipStream_t s)
+                           int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s)
 {
     if (T <= 1024) {  // one workgroup: token-waves x experts over its 16 waves
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows,
-                           pos, goff, tok, tile_off, group_of);
+                           pos, goff, tok, tile_off, tile_desc);
         return hipGetLastError();
     }
     const int chunks = dispatch_chunks(T);
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, chunk_cnt);
     hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, T, k, E, S, bm, chunks, chunk_cnt, load,
-                       offsets, goff, tok, tile_off, group_of);
+                       offsets, goff, tok, tile_off, tile_desc);
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, S, chunk_cnt, rows,
                        pos, tok);
     return hipGetLastError();
@@ -848,7 +865,7 @@ hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hip
     else e = a.norm ? launch_token_typed<float, true>(a, hash, s) : launch_token_typed<float, false>(a, hash, s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a.chosen, a.T, a.k, a.E, a.S, a.bm, a.load,
-                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off, a.group_of);
+                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off, a.tile_desc);
     return hipGetLastError();
 }
 
