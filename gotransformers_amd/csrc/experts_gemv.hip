@@ -83,10 +83,14 @@ __device__ __forceinline__ uint32_t upper_halves(float lo, float hi)
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to bf16 (nearest even) and packed, lo in the low half:
+// one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t bf16_rne_pair(float lo, float hi)
 {
-    const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 // x = hi + lo for two values: hi = bf16(x) rounded to nearest, lo = bf16 of
@@ -134,7 +138,8 @@ __device__ __forceinline__ f32x4 mfma4(s16x4 a, s16x4 b, f32x4 c)
     return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 4, 0, 0);
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// x * sigmoid(x) with the hardware exp and reciprocal (about 1 ulp each)
+__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // The staged tokens: for every group of 8 k-values, NT tokens' bf16 hi
 // values (16 bytes each), then the same for lo.  Lane reads of one token's

@@ -41,13 +41,17 @@ constexpr int BN = 256;    // weight rows per tile (gate/up: 128 neurons x 2)
 constexpr int BK = 64;     // K per pipeline step (4 scale blocks)
 constexpr int LDA = BK + 8;  // LDS row stride in bf16 (144 bytes)
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to bf16 (nearest even) and packed, lo in the low half:
+// one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
 {
-    const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// x * sigmoid(x) with the hardware exp and reciprocal (about 1 ulp each)
+__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // Codes of the two scale blocks a lane dequantizes per K step, per column
 // tile, and their scales.
@@ -229,44 +233,62 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     }
 
     // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows
-    // 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r
+    // 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r.  Full tiles
+    // (the common case) take a path without per-row checks.
     const int rq = h * 4;
+    const bool full = M >= BM;
     if constexpr (GATEUP) {
         const int n = ncol[0];
         if (n < a.n) {
             const float bg = a.b0[(size_t)g * a.n + n], bu = a.b1[(size_t)g * a.n + n];
-            uint16_t *out = reinterpret_cast<uint16_t *>(a.out);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
-                    if (m < M) {
-                        float gv = acc[i][0][r] + bg;
-                        float uv = acc[i][1][r] + bu;
-                        if (a.clamp > 0.f) {
-                            gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
-                            uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
-                        }
-                        const __bf16 hv = (__bf16)(silu(gv) * uv);
-                        out[(size_t)(p0 + m) * a.ldo + n] = __builtin_bit_cast(uint16_t, hv);
-                    }
+            uint16_t *out = reinterpret_cast<uint16_t *>(a.out) + (size_t)p0 * a.ldo + n;
+            auto emit = [&](int i, int r) {
+                const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
+                float gv = acc[i][0][r] + bg;
+                float uv = acc[i][1][r] + bu;
+                if (a.clamp > 0.f) {
+                    gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
+                    uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
                 }
+                const __bf16 hv = (__bf16)(silu(gv) * uv);
+                out[(size_t)m * a.ldo] = __builtin_bit_cast(uint16_t, hv);
+            };
+            if (full) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) emit(i, r);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (i * 32 + 8 * (r >> 2) + rq + (r & 3) < M) emit(i, r);
+            }
         }
     } else {
-        float *out = reinterpret_cast<float *>(a.out);
+        float *out = reinterpret_cast<float *>(a.out) + (size_t)p0 * a.ldo;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int n = ncol[j];
             if (n >= a.n) continue;
             const float bd = a.b0[(size_t)g * a.n + n];
+            auto emit = [&](int i, int r) {
+                const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
+                out[(size_t)m * a.ldo + n] = acc[i][j][r] + bd;
+            };
+            if (full) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
-                    if (m < M) out[(size_t)(p0 + m) * a.ldo + n] = acc[i][j][r] + bd;
-                }
+                    for (int r = 0; r < 16; ++r) emit(i, r);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (i * 32 + 8 * (r >> 2) + rq + (r & 3) < M) emit(i, r);
+            }
         }
     }
 }
