@@ -140,7 +140,7 @@ struct Workspace {
     int32_t *tok = nullptr;
     float *hidden32 = nullptr;    // [P][hp]
     uint16_t *hidden16 = nullptr;  // [P][hp] bf16
-    float *slot_out = nullptr;    // [P][d]
+    float *slot_out = nullptr;    // [P][d] fp32 (fp32 path) or bf16 (MFMA path)
     int32_t *chunk_cnt = nullptr;  // [chunks][E] scratch of the many-token dispatch
 };
 
@@ -362,6 +362,13 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
     const bool need_f32 = path == GTMOE_PATH_FP32 || !hash;
     float *xf = need_f32 ? w.xf : nullptr;
     uint16_t *xb = path == GTMOE_PATH_BF16 ? w.xb : nullptr;
+    // fp32 rows for the router: an fp32 input whose rows are already a
+    // multiple of 64 wide is read in place on the bf16 path
+    const float *xr = w.xf;
+    if (path == GTMOE_PATH_BF16 && !in.f64 && !in.norm && L->d == L->dp) {
+        xf = nullptr;
+        xr = (const float *)in.x;
+    }
     // the dispatch's per-group tile prefix counts MFMA m-tiles on the bf16
     // path and token slices on the fp32 path
     const int bm = path == GTMOE_PATH_BF16 ? mfma_tile_m() : kGemvSlice;
@@ -409,7 +416,7 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
     if (hash) {
         RUN(ctx, s, "hash_route", launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
     } else {
-        RUN(ctx, s, "router", launch_router(w.xf, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s));
+        RUN(ctx, s, "router", launch_router(xr, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s));
         RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
     }
     RUN(ctx, s, "dispatch",
@@ -849,7 +856,9 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     rc = prepare_and_route(L, T, Inputs{w.x64, true, false}, w.ids, path, s);
     if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
-    RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, nullptr, nullptr, w.y64, s));
+    RUN(ctx, s, "combine",
+        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr, nullptr,
+                       w.y64, s));
     HIP_TRY(ctx, hipMemcpyAsync(outputs, w.y64, sizeof(double) * T * L->d, hipMemcpyDeviceToHost, s));
     L->last_load.assign(L->E, 0);
     HIP_TRY(ctx, hipMemcpyAsync(L->last_load.data(), w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost, s));
@@ -887,7 +896,9 @@ int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs
     rc = prepare_and_route(L, T, Inputs{inputs, false, false}, token_ids, path, s);
     if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
-    RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, nullptr, outputs, nullptr, s));
+    RUN(ctx, s, "combine",
+        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr, outputs,
+                       nullptr, s));
     mark_forward(L, T, path, s);
     return GTMOE_OK;
 }
@@ -1013,7 +1024,9 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
         rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s);
         if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
         if (rc != GTMOE_OK) return rc;
-        RUN(ctx, s, "combine", launch_combine(T, L->d, L->S, L->k, w.slot_out, w.pos, w.gates32, x, x, nullptr, s));
+        RUN(ctx, s, "combine",
+            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, x, x, nullptr,
+                           s));
         mark_forward(L, T, path, s);
     }
     return GTMOE_OK;

@@ -112,7 +112,7 @@ struct MfmaArgs {
     const int32_t *tok;    // gate/up: gather by token; down: nullptr
     const int32_t *count;  // number of m-tiles (the rest of the grid exits)
     const int4 *desc;      // per m-tile: group, first position, positions, 0
-    void *out;  // gate/up: bf16 hidden; down: fp32 slot outputs
+    void *out;  // bf16: gate/up hidden rows, down slot outputs
     int ldo;
     float clamp;
 };
@@ -163,7 +163,7 @@ hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hi
 hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 hipError_t launch_mfma_down(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 int mfma_tile_m();
-hipError_t launch_combine(int T, int d, int S, int k, const float *slot_out, const int32_t *pos,
+hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool slot_bf16, const int32_t *pos,
                           const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s);
 hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s);
 hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);

@@ -8,7 +8,7 @@
 //            epilogue applies the SwiGLU (feedforward/gatedfeedforward.go:
 //            49-57) and writes bf16 hidden rows.
 //   down     A = hidden rows (bf16, contiguous per group), B = 256 down rows;
-//            the epilogue adds the bias and writes fp32 slot outputs.
+//            the epilogue adds the bias and writes bf16 slot outputs.
 // Four waves split the columns: each wave owns all 128 positions x 64
 // columns (4 x 2 MFMA tiles of 32 x 32; for gate/up its two column tiles are
 // gate and up of the same 32 neurons, so both values of a neuron land in
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             }
         }
     } else {
-        float *out = reinterpret_cast<float *>(a.out) + (size_t)p0 * a.ldo;
+        uint16_t *out = reinterpret_cast<uint16_t *>(a.out) + (size_t)p0 * a.ldo;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int n = ncol[j];
@@ -275,7 +275,8 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             const float bd = a.b0[(size_t)g * a.n + n];
             auto emit = [&](int i, int r) {
                 const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
-                out[(size_t)m * a.ldo + n] = acc[i][j][r] + bd;
+                const __bf16 v = (__bf16)(acc[i][j][r] + bd);
+                out[(size_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, v);
             };
             if (full) {
 #pragma unroll

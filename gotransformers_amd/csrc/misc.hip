@@ -5,29 +5,69 @@ namespace gtmoe {
 
 namespace {
 
-// float -> bf16, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ uint16_t to_bf16(float f)
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Four floats as bf16 (nearest even), packed in 8 bytes.
+__device__ __forceinline__ uint2 to_bf16x4(float a, float b, float c, float d)
 {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c, d}, bf16x2)));
+}
+
+// Four consecutive values of a row (zeros past d); rows with d % 4 == 0
+// are read with vector loads.
+__device__ __forceinline__ void load_row4(const float *row, int j, int d, bool vec, float (&v)[4])
+{
+    if (vec && j < d) {
+        const float4 q = *reinterpret_cast<const float4 *>(row + j);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = j + i < d ? row[j + i] : 0.f;
+    }
+}
+__device__ __forceinline__ void load_row4(const double *row, int j, int d, bool vec, float (&v)[4])
+{
+    if (vec && j < d) {
+        const double2 a = *reinterpret_cast<const double2 *>(row + j);
+        const double2 b = *reinterpret_cast<const double2 *>(row + j + 2);
+        v[0] = (float)a.x;
+        v[1] = (float)a.y;
+        v[2] = (float)b.x;
+        v[3] = (float)b.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = j + i < d ? (float)row[j + i] : 0.f;
+    }
+}
+
+__device__ __forceinline__ void store_row4(float *xf, uint16_t *xb, size_t of, size_t ob, const float (&v)[4])
+{
+    if (xf) *reinterpret_cast<float4 *>(xf + of) = make_float4(v[0], v[1], v[2], v[3]);
+    if (xb) *reinterpret_cast<uint2 *>(xb + ob) = to_bf16x4(v[0], v[1], v[2], v[3]);
 }
 
 }  // namespace
 
 // One row per workgroup: padded fp32 copy (ldf columns, zeros past d) and/or
-// padded bf16 copy.  Either output may be null.
+// padded bf16 copy.  Either output may be null; ldf and ldb are multiples of
+// 64.  Each thread handles four consecutive columns per step.
 template <typename InT>
 __global__ __launch_bounds__(256) void convert_inputs_kernel(const InT *__restrict__ x, int d, float *__restrict__ xf,
                                                              int ldf, uint16_t *__restrict__ xb, int ldb)
 {
     const int t = blockIdx.x;
     const int ld = xf ? ldf : ldb;
-    for (int j = threadIdx.x; j < ld; j += blockDim.x) {
-        const float v = j < d ? (float)x[(size_t)t * d + j] : 0.f;
-        if (xf) xf[(size_t)t * ldf + j] = v;
-        if (xb) xb[(size_t)t * ldb + j] = to_bf16(v);
+    const InT *row = x + (size_t)t * d;
+    const bool vec = (d & 3) == 0;
+    for (int j = threadIdx.x * 4; j < ld; j += 1024) {
+        float v[4];
+        load_row4(row, j, d, vec, v);
+        store_row4(xf, xb, (size_t)t * ldf + j, (size_t)t * ldb + j, v);
     }
 }
 
@@ -56,18 +96,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     __shared__ float partial[4];
     const int t = blockIdx.x;
     const float *row = x + (size_t)t * d;
+    const bool vec = (d & 3) == 0;
     float ss = 0.f;
-    for (int j = threadIdx.x; j < d; j += 256) ss = fmaf(row[j], row[j], ss);
+    for (int j = threadIdx.x * 4; j < d; j += 1024) {
+        float v[4];
+        load_row4(row, j, d, vec, v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss = fmaf(v[i], v[i], ss);
+    }
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
     if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
     __syncthreads();
     const float total = partial[0] + partial[1] + partial[2] + partial[3];
     const float inv = 1.0f / sqrtf(total / (float)d + 1e-6f);
     const int ld = xf ? ldf : ldb;
-    for (int j = threadIdx.x; j < ld; j += 256) {
-        const float v = j < d ? row[j] * inv * w[j] : 0.f;
-        if (xf) xf[(size_t)t * ldf + j] = v;
-        if (xb) xb[(size_t)t * ldb + j] = to_bf16(v);
+    for (int j = threadIdx.x * 4; j < ld; j += 1024) {
+        float v[4], g[4];
+        load_row4(row, j, d, vec, v);
+        load_row4(w, j, d, vec, g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = v[i] * inv * g[i];
+        store_row4(xf, xb, (size_t)t * ldf + j, (size_t)t * ldb + j, v);
     }
 }
 
@@ -79,12 +128,24 @@ hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *x
     return hipGetLastError();
 }
 
+// Slot rows are fp32 (fp32 path) or bf16 (MFMA path).
+__device__ __forceinline__ float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ float4 load4(const uint16_t *p)
+{
+    const uint2 v = *reinterpret_cast<const uint2 *>(p);
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                       __uint_as_float(v.y & 0xffff0000u));
+}
+__device__ __forceinline__ float load1(const float *p) { return *p; }
+__device__ __forceinline__ float load1(const uint16_t *p) { return __uint_as_float((uint32_t)*p << 16); }
+
 // Weighted combine (mixtureofexperts.go:182-205) in the reference's order:
 // out = 0, + each shared expert's row, then + gate_i * routed row for the
 // slots in chosen order.  With a residual: out = residual + that sum
 // (transformer/block.go:77).  Writes fp32 and/or float64 output.  Grid
 // (T, ceil(d / 1024)); each thread owns four consecutive columns.
-__global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k, const float *__restrict__ slot_out,
+template <typename SlotT>
+__global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k, const SlotT *__restrict__ slot_out,
                                                       const int32_t *__restrict__ pos,
                                                       const float *__restrict__ gates32,
                                                       const float *__restrict__ residual, float *__restrict__ out32,
@@ -104,7 +165,7 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     if (n == 4 && (d & 3) == 0) {
         for (int s = 0; s < S; ++s) {
-            const float4 v = *reinterpret_cast<const float4 *>(slot_out + ((size_t)s * T + t) * d + j0);
+            const float4 v = load4(slot_out + ((size_t)s * T + t) * d + j0);
             acc[0] += v.x;
             acc[1] += v.y;
             acc[2] += v.z;
@@ -113,7 +174,7 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             if (i < k) {
-                const float4 v = *reinterpret_cast<const float4 *>(slot_out + (size_t)p[i] * d + j0);
+                const float4 v = load4(slot_out + (size_t)p[i] * d + j0);
                 acc[0] = fmaf(g[i], v.x, acc[0]);
                 acc[1] = fmaf(g[i], v.y, acc[1]);
                 acc[2] = fmaf(g[i], v.z, acc[2]);
@@ -121,10 +182,10 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
             }
     } else {
         for (int q = 0; q < n; ++q) {
-            for (int s = 0; s < S; ++s) acc[q] += slot_out[((size_t)s * T + t) * d + j0 + q];
+            for (int s = 0; s < S; ++s) acc[q] += load1(slot_out + ((size_t)s * T + t) * d + j0 + q);
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (i < k) acc[q] = fmaf(g[i], slot_out[(size_t)p[i] * d + j0 + q], acc[q]);
+                if (i < k) acc[q] = fmaf(g[i], load1(slot_out + (size_t)p[i] * d + j0 + q), acc[q]);
         }
     }
     for (int q = 0; q < n; ++q) {
@@ -136,12 +197,17 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
     }
 }
 
-hipError_t launch_combine(int T, int d, int S, int k, const float *slot_out, const int32_t *pos, const float *gates32,
-                          const float *residual, float *out32, double *out64, hipStream_t s)
+hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool slot_bf16, const int32_t *pos,
+                          const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s)
 {
     if (T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel, dim3(T, (d + 1023) / 1024), dim3(256), 0, s, T, d, S, k, slot_out, pos, gates32,
-                       residual, out32, out64);
+    const dim3 grid(T, (d + 1023) / 1024);
+    if (slot_bf16)
+        hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, dim3(256), 0, s, T, d, S, k,
+                           static_cast<const uint16_t *>(slot_out), pos, gates32, residual, out32, out64);
+    else
+        hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, s, T, d, S, k,
+                           static_cast<const float *>(slot_out), pos, gates32, residual, out32, out64);
     return hipGetLastError();
 }
 
