@@ -152,8 +152,9 @@ hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *c
                              float *gates32, hipStream_t s);
 bool fused_route_fits(int T, int k, int kp);
 hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s);
-// Dispatch: one workgroup up to 1024 tokens, else count / scan / scatter over
-// chunks of 256 tokens using chunk_cnt [dispatch_chunks(T)][E] as scratch.
+// Dispatch: one workgroup up to 1024 tokens, else a count and a placement
+// launch over chunks of 256 tokens using chunk_cnt [dispatch_chunks(T)][E]
+// as scratch.
 int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
                            int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,

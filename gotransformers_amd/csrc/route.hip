@@ -196,11 +196,22 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
     floatx16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    // operands of step kb + 1 load while step kb multiplies
+    float4 xa, xb, wa, wb;
+    if (k0 < k1) {
+        xa = *reinterpret_cast<const float4 *>(xr + k0 * 16);
+        xb = *reinterpret_cast<const float4 *>(xr + k0 * 16 + 4);
+        wa = *reinterpret_cast<const float4 *>(wr + k0 * 16);
+        wb = *reinterpret_cast<const float4 *>(wr + k0 * 16 + 4);
+    }
     for (int kb = k0; kb < k1; ++kb) {
-        const float4 xa = *reinterpret_cast<const float4 *>(xr + kb * 16);
-        const float4 xb = *reinterpret_cast<const float4 *>(xr + kb * 16 + 4);
-        const float4 wa = *reinterpret_cast<const float4 *>(wr + kb * 16);
-        const float4 wb = *reinterpret_cast<const float4 *>(wr + kb * 16 + 4);
+        float4 nxa = xa, nxb = xb, nwa = wa, nwb = wb;
+        if (kb + 1 < k1) {
+            nxa = *reinterpret_cast<const float4 *>(xr + (kb + 1) * 16);
+            nxb = *reinterpret_cast<const float4 *>(xr + (kb + 1) * 16 + 4);
+            nwa = *reinterpret_cast<const float4 *>(wr + (kb + 1) * 16);
+            nwb = *reinterpret_cast<const float4 *>(wr + (kb + 1) * 16 + 4);
+        }
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, wa.x, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, wa.y, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.z, wa.z, acc, 0, 0, 0);
@@ -209,6 +220,10 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.y, wb.y, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.z, wb.z, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.w, wb.w, acc, 0, 0, 0);
+        xa = nxa;
+        xb = nxb;
+        wa = nwa;
+        wb = nwb;
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
@@ -450,27 +465,6 @@ __device__ int block_exclusive_scan(const int *vals, int *out, int n, int *wave_
     return *total_slot;
 }
 
-// Ranks of a chunk of tokens inside their experts.  Each of the block's
-// threads holds one token's k chosen experts in ce[] (-1 when absent); on
-// return rk[i] is the number of lower tokens of the same wave with expert
-// ce[i], and wave_cnt[w][e] the count of expert e in wave w.
-__device__ __forceinline__ void wave_ranks(const int (&ce)[kMaxK], int (&rk)[kMaxK], int E, int lane, int wave,
-                                           int (*wave_cnt)[kMaxExperts])
-{
-    for (int e = 0; e < E; ++e) {
-        int match = -1;
-#pragma unroll
-        for (int i = 0; i < kMaxK; ++i)
-            if (ce[i] == e) match = i;
-        const unsigned long long b = __ballot(match >= 0);
-        if (lane == 0) wave_cnt[wave][e] = __popcll(b);
-        const int r = __popcll(b & ((1ULL << lane) - 1ULL));
-#pragma unroll
-        for (int i = 0; i < kMaxK; ++i)
-            if (i == match) rk[i] = r;
-    }
-}
-
 struct DispatchShared {
     int cnt[kScanMax];
     int base[kScanMax];
@@ -618,68 +612,94 @@ __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(const int32_t *_
     for (int e = threadIdx.x; e < E; e += kChunk) chunk_cnt[(size_t)blockIdx.x * E + e] = cnt[e];
 }
 
-__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int T, int k, int E, int S, int bm, int chunks,
-                                                             int32_t *__restrict__ chunk_cnt, int32_t *__restrict__ load,
-                                                             int32_t *__restrict__ offsets, int32_t *__restrict__ goff,
-                                                             int32_t *__restrict__ tok, int32_t *__restrict__ tile_off,
-                                                             int4 *__restrict__ tile_desc)
+// Placement of one chunk of kChunk tokens, 16 waves.  Every workgroup sums
+// the per-chunk counts itself (threads split the chunks of each expert), so
+// the totals, the experts' offsets and its own chunk's start need no
+// separate scan launch; workgroup 0 also writes the group tables.  Ranks
+// inside the chunk come from wave ballots, with the (token-wave, expert)
+// pairs spread over the 16 waves.  No atomic decides a position: the LDS
+// atomics only add up counts.
+__global__ __launch_bounds__(1024) void dispatch_place_kernel(const int32_t *__restrict__ chosen, int T, int k, int E,
+                                                              int S, int bm, int chunks,
+                                                              const int32_t *__restrict__ chunk_cnt,
+                                                              int32_t *__restrict__ load, int32_t *__restrict__ offsets,
+                                                              int32_t *__restrict__ rows, int32_t *__restrict__ pos,
+                                                              int32_t *__restrict__ goff, int32_t *__restrict__ tok,
+                                                              int32_t *__restrict__ tile_off,
+                                                              int4 *__restrict__ tile_desc)
 {
     __shared__ DispatchShared sh;
-    const int tid = threadIdx.x;
-    // per-expert totals
+    __shared__ int before[kMaxExperts];
+    __shared__ int rank_lds[kChunk][kMaxK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = blockIdx.x;
     for (int e = tid; e < E; e += 1024) {
-        int acc = 0;
-        for (int c = 0; c < chunks; ++c) acc += chunk_cnt[(size_t)c * E + e];
-        sh.cnt[e] = acc;
+        sh.cnt[e] = 0;
+        before[e] = 0;
+    }
+    __syncthreads();
+    // totals over all chunks and over the chunks before this one
+    const int per = 1024 / E;  // threads per expert (E <= 256)
+    if (tid < per * E) {
+        const int e = tid % E, j = tid / E;
+        int tot = 0, bef = 0;
+        int cc = j;
+        for (; cc + 3 * per < chunks; cc += 4 * per) {
+            const int n0 = chunk_cnt[(size_t)cc * E + e], n1 = chunk_cnt[(size_t)(cc + per) * E + e];
+            const int n2 = chunk_cnt[(size_t)(cc + 2 * per) * E + e], n3 = chunk_cnt[(size_t)(cc + 3 * per) * E + e];
+            tot += n0 + n1 + n2 + n3;
+            bef += (cc < c ? n0 : 0) + (cc + per < c ? n1 : 0) + (cc + 2 * per < c ? n2 : 0) + (cc + 3 * per < c ? n3 : 0);
+        }
+        for (; cc < chunks; cc += per) {
+            const int n = chunk_cnt[(size_t)cc * E + e];
+            tot += n;
+            bef += cc < c ? n : 0;
+        }
+        atomicAdd(&sh.cnt[e], tot);
+        atomicAdd(&before[e], bef);
     }
     __syncthreads();
     block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
-    write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, tile_desc);
-    // each chunk's first position per expert
+    if (c == 0) write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, tile_desc);
+
+    // ranks inside the chunk: wave w covers token-wave w/4 and the experts
+    // e = w%4 (mod 4)
+    const int tw = wave >> 2, sub = wave & 3;
+    const int tl = tw * 64 + lane;
+    const int t = c * kChunk + tl;
+    int ce[kMaxK];
+#pragma unroll
+    for (int i = 0; i < kMaxK; ++i) ce[i] = (t < T && i < k) ? chosen[(size_t)t * k + i] : -1;
+    for (int e = sub; e < E; e += 4) {
+        int match = -1;
+#pragma unroll
+        for (int i = 0; i < kMaxK; ++i)
+            if (ce[i] == e) match = i;
+        const unsigned long long b = __ballot(match >= 0);
+        if (lane == 0) sh.wave_cnt[tw][e] = __popcll(b);
+        if (match >= 0) rank_lds[tl][match] = __popcll(b & ((1ULL << lane) - 1ULL));
+    }
+    __syncthreads();
+    // first position of each (token-wave, expert)
     for (int e = tid; e < E; e += 1024) {
-        int acc = sh.base[e];
-        for (int c = 0; c < chunks; ++c) {
-            const int n = chunk_cnt[(size_t)c * E + e];
-            chunk_cnt[(size_t)c * E + e] = acc;
+        int acc = sh.base[e] + before[e];
+#pragma unroll
+        for (int w = 0; w < kChunk / 64; ++w) {
+            const int n = sh.wave_cnt[w][e];
+            sh.wave_cnt[w][e] = acc;
             acc += n;
         }
     }
-}
-
-__global__ __launch_bounds__(kChunk) void dispatch_scatter_kernel(const int32_t *__restrict__ chosen, int T, int k, int E,
-                                                                  int S, const int32_t *__restrict__ chunk_base,
-                                                                  int32_t *__restrict__ rows, int32_t *__restrict__ pos,
-                                                                  int32_t *__restrict__ tok)
-{
-    __shared__ int wave_cnt[kChunk / 64][kMaxExperts];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = blockIdx.x * kChunk + tid;
-    const bool valid = t < T;
-    int ce[kMaxK], rk[kMaxK];
-#pragma unroll
-    for (int i = 0; i < kMaxK; ++i) {
-        ce[i] = (valid && i < k) ? chosen[(size_t)t * k + i] : -1;
-        rk[i] = 0;
-    }
-    wave_ranks(ce, rk, E, lane, wave, wave_cnt);
     __syncthreads();
-    for (int e = tid; e < E; e += kChunk) {
-        int acc = chunk_base[(size_t)blockIdx.x * E + e];
-        for (int w = 0; w < kChunk / 64; ++w) {
-            const int c = wave_cnt[w][e];
-            wave_cnt[w][e] = acc;
-            acc += c;
-        }
-    }
-    __syncthreads();
-    if (valid) {
-#pragma unroll
-        for (int i = 0; i < kMaxK; ++i) {
-            if (i < k) {
-                const int p = wave_cnt[wave][ce[i]] + rk[i];
-                rows[p] = t;
-                pos[(size_t)t * k + i] = p;
-                tok[(size_t)S * T + p] = t;
+    if (tid < kChunk) {
+        const int tt = c * kChunk + tid;
+        if (tt < T) {
+            for (int i = 0; i < k; ++i) {
+                const int e = chosen[(size_t)tt * k + i];
+                const int p = sh.wave_cnt[tid >> 6][e] + rank_lds[tid][i];
+                rows[p] = tt;
+                pos[(size_t)tt * k + i] = p;
+                tok[(size_t)S * T + p] = tt;
             }
         }
     }
@@ -698,10 +718,8 @@ hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, in
     }
     const int chunks = dispatch_chunks(T);
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, chunk_cnt);
-    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, T, k, E, S, bm, chunks, chunk_cnt, load,
-                       offsets, goff, tok, tile_off, tile_desc);
-    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, S, chunk_cnt, rows,
-                       pos, tok);
+    hipLaunchKernelGGL(dispatch_place_kernel, dim3(chunks), dim3(1024), 0, s, chosen, T, k, E, S, bm, chunks,
+                       chunk_cnt, load, offsets, rows, pos, goff, tok, tile_off, tile_desc);
     return hipGetLastError();
 }
 
