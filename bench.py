@@ -147,6 +147,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="replay each step as a recorded HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (for PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -186,10 +187,23 @@ def main():
     sptr = stream.cuda_stream
     torch.cuda.set_stream(stream)
 
+    graphs = []
+    if args.graph:  # the step recorded once per weight copy and replayed as a HIP graph
+        if c["layers"] > 1:
+            graphs = [gt.Graph.capture_stack(layers, T, x.data_ptr(), path=gt.PATH_AUTO)]
+        else:
+            graphs = [gt.Graph.capture_forward(m, T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO)
+                      for m in layers]
+
     def step(i):
         if c["layers"] > 1:
             x.copy_(x0)
-            gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
+            if graphs:
+                graphs[0].launch(stream=sptr)
+            else:
+                gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
+        elif graphs:
+            graphs[i % c["copies"]].launch(stream=sptr)
         else:
             layers[i % c["copies"]].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
 
@@ -260,6 +274,8 @@ def main():
     roof.update({"kernel": dominant, "algorithmic_per_launch": per_launch, "mean_launch_us": kmean_s * 1e6,
                  "launches": klaunch})
 
+    for g in graphs:
+        g.destroy()
     for m in layers:
         m.destroy()
     ctx.close()
@@ -288,7 +304,8 @@ def main():
                    "shared_experts": c["S"], "top_k": c["k"], "expert_hidden": c["h"],
                    "expert_weights": f"{c['prec']} per-16 fp32 scales", "layers_per_step": step_layers,
                    "weight_copies": c["copies"],
-                   "path": "fp32 dequant-GEMV" if decode else "bf16 MFMA grouped GEMM"},
+                   "path": "fp32 dequant-GEMV" if decode else "bf16 MFMA grouped GEMM",
+                   "hip_graph": bool(graphs)},
         "roofline": roof,
         "cpu_baseline": cpu,
         "detail": {

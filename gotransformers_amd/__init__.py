@@ -34,6 +34,7 @@ EXPORTED = [
     "gtmoe_forward_device", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
     "gtmoe_route_from_logits", "gtmoe_stack_forward", "gtmoe_stack_forward_device", "gtmoe_timing_enable",
     "gtmoe_timing_reset", "gtmoe_timing_read", "gtmoe_last_path", "gtmoe_relaunch",
+    "gtmoe_graph_capture_forward", "gtmoe_graph_capture_stack", "gtmoe_graph_launch", "gtmoe_graph_destroy",
 ]
 
 
@@ -97,6 +98,10 @@ def library():
         "gtmoe_timing_read": ([P, i32, P, P, P, P], i32),
         "gtmoe_last_path": ([P, P], i32),
         "gtmoe_relaunch": ([P, i32, P], i32),
+        "gtmoe_graph_capture_forward": ([P, i32, P, P, P, u32, P], i32),
+        "gtmoe_graph_capture_stack": ([P, i32, i32, P, P, u32, P], i32),
+        "gtmoe_graph_launch": ([P, P], i32),
+        "gtmoe_graph_destroy": ([P], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -376,3 +381,41 @@ def stack_forward_device(layers, tokens, x_ptr, token_ids_ptr=None, path=PATH_AU
     ctx = layers[0].ctx
     ctx.check(library().gtmoe_stack_forward_device(_layer_array(layers), len(layers), tokens, x_ptr, token_ids_ptr,
                                                    path, stream))
+
+
+class Graph:
+    """One recorded forward (a layer's forward_device or a stack's
+    stack_forward_device) replayed as a HIP graph.  The recorded device
+    buffers must stay alive and in place; refill them between launches."""
+
+    def __init__(self, ctx, handle, layers):
+        self.ctx, self.handle, self._layers = ctx, handle, layers
+
+    @classmethod
+    def capture_forward(cls, layer, tokens, inputs_ptr, outputs_ptr, token_ids_ptr=None, path=PATH_AUTO):
+        h = C.c_void_p()
+        layer.ctx.check(library().gtmoe_graph_capture_forward(layer.handle, tokens, inputs_ptr, token_ids_ptr,
+                                                              outputs_ptr, path, C.byref(h)))
+        return cls(layer.ctx, h, [layer])
+
+    @classmethod
+    def capture_stack(cls, layers, tokens, x_ptr, token_ids_ptr=None, path=PATH_AUTO):
+        h = C.c_void_p()
+        ctx = layers[0].ctx
+        ctx.check(library().gtmoe_graph_capture_stack(_layer_array(layers), len(layers), tokens, x_ptr,
+                                                      token_ids_ptr, path, C.byref(h)))
+        return cls(ctx, h, list(layers))
+
+    def launch(self, stream=None):
+        self.ctx.check(library().gtmoe_graph_launch(self.handle, stream))
+
+    def destroy(self):
+        if self.handle:
+            library().gtmoe_graph_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()

@@ -572,6 +572,58 @@ int32_t check_layer_call(gtmoe_layer *L)
 
 }  // namespace
 
+// ---- HIP graphs of a whole forward ------------------------------------------
+
+struct gtmoe_graph {
+    gtmoe_context *ctx = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<gtmoe_layer *> layers;
+    std::vector<int> paths;
+    int T = 0;
+};
+
+namespace {
+
+void free_graph(gtmoe_graph *g)
+{
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
+// Records `record(s)` on a private capture stream into an instantiated graph.
+template <class F>
+int32_t capture(gtmoe_context *ctx, F &&record, gtmoe_graph *g)
+{
+    hipStream_t cs = nullptr;
+    HIP_TRY(ctx, hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+    const bool timing = ctx->timing;
+    ctx->timing = false;  // no event nodes in the graph
+    hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed);
+    int32_t rc = e == hipSuccess ? record(cs) : fail(ctx, GTMOE_ERR_DEVICE, "hipStreamBeginCapture: %s",
+                                                      hipGetErrorString(e));
+    hipGraph_t graph = nullptr;
+    if (e == hipSuccess) {
+        const hipError_t e2 = hipStreamEndCapture(cs, &graph);
+        if (rc == GTMOE_OK && e2 != hipSuccess)
+            rc = fail(ctx, GTMOE_ERR_DEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e2));
+    }
+    ctx->timing = timing;
+    (void)hipStreamDestroy(cs);
+    if (rc != GTMOE_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    g->graph = graph;
+    e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) return fail(ctx, GTMOE_ERR_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    return GTMOE_OK;
+}
+
+}  // namespace
+
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
@@ -868,6 +920,42 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     return GTMOE_OK;
 }
 
+// Checks of gtmoe_forward_device's arguments; leaves the resolved path.
+static int32_t check_forward_device(gtmoe_layer *L, int32_t T, const float *inputs, const int64_t *token_ids,
+                                    const float *outputs, uint32_t flags, int *path)
+{
+    gtmoe_context *ctx = L->ctx;
+    if (T < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "negative number of tokens");
+    if (T > 0 && (!inputs || !outputs)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "inputs or outputs are null");
+    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
+    if (L->desc.use_hash_routing && T > 0 && !token_ids)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: hash routing needs one token ID per row");
+    *path = choose_path(L, T, flags);
+    if (*path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
+    return ensure_workspace(L, T);
+}
+
+// The kernels of one device forward, enqueued on s.
+static int32_t forward_device_run(gtmoe_layer *L, int32_t T, const float *inputs, const int64_t *token_ids,
+                                  float *outputs, int path, hipStream_t s)
+{
+    gtmoe_context *ctx = L->ctx;
+    if (T == 0) {
+        mark_forward(L, 0, path, s);
+        return GTMOE_OK;
+    }
+    Workspace &w = L->ws;
+    int32_t rc = prepare_and_route(L, T, Inputs{inputs, false, false}, token_ids, path, s);
+    if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
+    if (rc != GTMOE_OK) return rc;
+    RUN(ctx, s, "combine",
+        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr, outputs,
+                       nullptr, s));
+    mark_forward(L, T, path, s);
+    return GTMOE_OK;
+}
+
 int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs, const int64_t *token_ids,
                              float *outputs, uint32_t flags, void *stream)
 {
@@ -876,31 +964,11 @@ int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs
     gtmoe_context *ctx = L->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    const int T = tokens;
-    if (T < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "negative number of tokens");
-    if (T > 0 && (!inputs || !outputs)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "inputs or outputs are null");
-    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
-    if (L->desc.use_hash_routing && T > 0 && !token_ids)
-        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: hash routing needs one token ID per row");
-    const int path = choose_path(L, T, flags);
-    if (path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
-        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
-    rc = ensure_workspace(L, T);
+    int path = 0;
+    rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
     if (rc != GTMOE_OK) return rc;
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    if (T == 0) {
-        mark_forward(L, 0, path, s);
-        return GTMOE_OK;
-    }
-    Workspace &w = L->ws;
-    rc = prepare_and_route(L, T, Inputs{inputs, false, false}, token_ids, path, s);
-    if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
-    if (rc != GTMOE_OK) return rc;
-    RUN(ctx, s, "combine",
-        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr, outputs,
-                       nullptr, s));
-    mark_forward(L, T, path, s);
-    return GTMOE_OK;
+    return forward_device_run(L, tokens, inputs, token_ids, outputs, path, s);
 }
 
 int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen, double *gates, int32_t *load,
@@ -1098,6 +1166,96 @@ int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers,
             return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "hash routing needs one token ID per row");
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     return stack_run(layers, n_layers, tokens, x, token_ids, flags, s);
+}
+
+int32_t gtmoe_graph_capture_forward(gtmoe_layer *L, int32_t tokens, const float *inputs, const int64_t *token_ids,
+                                    float *outputs, uint32_t flags, gtmoe_graph **graph)
+{
+    if (!graph) return GTMOE_ERR_INVALID_ARGUMENT;
+    *graph = nullptr;
+    int32_t rc = check_layer_call(L);
+    if (rc != GTMOE_OK) return rc;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int path = 0;
+    rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
+    if (rc != GTMOE_OK) return rc;
+    gtmoe_graph *g = new gtmoe_graph;
+    g->ctx = ctx;
+    g->layers = {L};
+    g->paths = {path};
+    g->T = tokens;
+    rc = capture(ctx, [&](hipStream_t cs) { return forward_device_run(L, tokens, inputs, token_ids, outputs, path, cs); },
+                 g);
+    if (rc != GTMOE_OK) {
+        free_graph(g);
+        return rc;
+    }
+    *graph = g;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_graph_capture_stack(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, float *x,
+                                  const int64_t *token_ids, uint32_t flags, gtmoe_graph **graph)
+{
+    if (!graph) return GTMOE_ERR_INVALID_ARGUMENT;
+    *graph = nullptr;
+    gtmoe_context *ctx = nullptr;
+    int32_t rc = stack_common(layers, n_layers, tokens, &ctx);
+    if (rc != GTMOE_OK) return rc;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
+    if (tokens > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
+    gtmoe_graph *g = new gtmoe_graph;
+    g->ctx = ctx;
+    g->T = tokens;
+    for (int l = 0; l < n_layers; ++l) {
+        gtmoe_layer *L = layers[l];
+        if (L->desc.use_hash_routing && tokens > 0 && !token_ids) {
+            free_graph(g);
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "hash routing needs one token ID per row");
+        }
+        rc = ensure_workspace(L, tokens);  // allocations happen before the capture
+        if (rc != GTMOE_OK) {
+            free_graph(g);
+            return rc;
+        }
+        g->layers.push_back(L);
+        g->paths.push_back(choose_path(L, tokens, flags));
+    }
+    rc = capture(ctx, [&](hipStream_t cs) { return stack_run(layers, n_layers, tokens, x, token_ids, flags, cs); }, g);
+    if (rc != GTMOE_OK) {
+        free_graph(g);
+        return rc;
+    }
+    *graph = g;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_graph_launch(gtmoe_graph *g, void *stream)
+{
+    if (!g || !g->exec) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = g->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    HIP_TRY(ctx, hipGraphLaunch(g->exec, s));
+    for (size_t i = 0; i < g->layers.size(); ++i) mark_forward(g->layers[i], g->T, g->paths[i], s);
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_graph_destroy(gtmoe_graph *g)
+{
+    if (!g) return GTMOE_OK;
+    gtmoe_context *ctx = g->ctx;
+    {
+        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+        (void)hipSetDevice(ctx->device);
+        free_graph(g);
+    }
+    return GTMOE_OK;
 }
 
 int32_t gtmoe_timing_enable(gtmoe_context *ctx, int32_t enabled)

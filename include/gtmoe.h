@@ -61,6 +61,7 @@ enum gtmoe_path { GTMOE_PATH_AUTO = 0, GTMOE_PATH_FP32 = 1, GTMOE_PATH_BF16 = 2 
 
 typedef struct gtmoe_context gtmoe_context;
 typedef struct gtmoe_layer gtmoe_layer;
+typedef struct gtmoe_graph gtmoe_graph;
 
 /* The shape of one MixtureOfExperts.  Mirrors the arguments of
  * NewMixtureOfExperts / NewClampedMixtureOfExperts
@@ -202,6 +203,25 @@ int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_
  * place), enqueued on `stream` without synchronising. */
 int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, float *x,
                                    const int64_t *token_ids, uint32_t flags, void *stream);
+
+/* ---- one forward as a HIP graph ----------------------------------------------
+ * The decode step replayed without per-kernel launches: the kernels of
+ * gtmoe_forward_device (one layer) or gtmoe_stack_forward_device (a stack)
+ * for a fixed token count are recorded once into an instantiated hipGraph
+ * and replayed by gtmoe_graph_launch on any stream.  The graph keeps the
+ * device pointers it was recorded with: the caller refills the same buffers
+ * between replays and keeps them alive; the layers must not be destroyed or
+ * re-uploaded with other shapes while the graph exists.  Each replay counts
+ * as a forward of every recorded layer (gtmoe_last_routing etc. read it).
+ * Workspace is sized before recording; no replay allocates.  There is no
+ * reference counterpart (the reference has no device graph); this serves
+ * the block step of transformer/block.go:76-77,117 for decode. */
+int32_t gtmoe_graph_capture_forward(gtmoe_layer *layer, int32_t tokens, const float *inputs,
+                                    const int64_t *token_ids, float *outputs, uint32_t flags, gtmoe_graph **graph);
+int32_t gtmoe_graph_capture_stack(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, float *x,
+                                  const int64_t *token_ids, uint32_t flags, gtmoe_graph **graph);
+int32_t gtmoe_graph_launch(gtmoe_graph *graph, void *stream);
+int32_t gtmoe_graph_destroy(gtmoe_graph *graph);
 
 /* ---- measurement -----------------------------------------------------------
  * Per-kernel timing with HIP events, the counterpart of the Vulkan

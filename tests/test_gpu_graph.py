@@ -1,0 +1,119 @@
+"""A whole forward recorded as a HIP graph and replayed: every replay must
+equal the eager forward bit for bit (the same kernels on the same buffers),
+with the program's own eager work and synchronisations between replays, and
+after the inputs are refilled in place.  The eager results are checked
+against the oracle as in the other GPU tests."""
+import numpy as np
+import pytest
+
+import gotransformers_amd as gt
+import oracle
+from tests.moe_fixtures import FP4, INT8, make_moe
+from tests.test_gpu_parity import rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = gt.Context(0)
+    yield c
+    c.close()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+@pytest.mark.parametrize("T,path", [(16, gt.PATH_FP32), (1, gt.PATH_FP32), (64, gt.PATH_BF16)])
+def test_graph_forward_replays_equal_eager(ctx, T, path):
+    say(f"graph forward T={T} path={path}")
+    spec = make_moe(gt.encode_rows, d=256, h=512, E=8, k=2, S=1, precision=INT8, seed=21)
+    rng = np.random.default_rng(22)
+    x0 = rng.standard_normal((T, 256))
+    x1 = rng.standard_normal((T, 256))
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        xa, ya = dev(x0), torch.empty(T, 256, device="cuda")
+        m.forward_device(T, xa.data_ptr(), ya.data_ptr(), path=path)
+        torch.cuda.synchronize()
+        eager0 = ya.cpu().numpy().copy()
+        r0 = m.last_routing()
+        xb, yb = dev(x1), torch.empty(T, 256, device="cuda")
+        m.forward_device(T, xb.data_ptr(), yb.data_ptr(), path=path)
+        torch.cuda.synchronize()
+        eager1 = yb.cpu().numpy().copy()
+
+        xg, yg = dev(x0), torch.empty(T, 256, device="cuda")
+        with gt.Graph.capture_forward(m, T, xg.data_ptr(), yg.data_ptr(), path=path) as g:
+            for rep in range(3):
+                yg.fill_(float("nan"))
+                torch.cuda.synchronize()
+                g.launch()
+                torch.cuda.synchronize()
+                assert np.array_equal(yg.cpu().numpy(), eager0), rep
+                # eager work of the program between replays
+                m.forward_device(T, xb.data_ptr(), yb.data_ptr(), path=path)
+                torch.cuda.synchronize()
+            g.launch()
+            torch.cuda.synchronize()
+            r = m.last_routing()
+            assert np.array_equal(r.chosen, r0.chosen)
+            assert np.array_equal(r.load, r0.load)
+            xg.copy_(xb)  # refill the recorded input in place
+            torch.cuda.synchronize()
+            g.launch()
+            torch.cuda.synchronize()
+            assert np.array_equal(yg.cpu().numpy(), eager1)
+    finally:
+        m.destroy()
+    ref = oracle.moe_forward_routed(spec, x0, r0.chosen, r0.gates)
+    tol = 1e-4 if path == gt.PATH_FP32 else 2e-2
+    assert rel_err(eager0, ref.outputs) <= tol
+
+
+@pytest.mark.parametrize("T,path", [(8, gt.PATH_FP32), (96, gt.PATH_BF16)])
+def test_graph_stack_replays_equal_eager(ctx, T, path):
+    say(f"graph stack T={T} path={path}")
+    d = 128
+    specs = [make_moe(gt.encode_rows, d=d, h=192, E=6, k=2, S=1, precision=FP4, seed=30 + i) for i in range(3)]
+    rng = np.random.default_rng(31)
+    x0 = rng.standard_normal((T, d))
+    layers = [gt.MixtureOfExperts.from_spec(ctx, s) for s in specs]
+    try:
+        for i, m in enumerate(layers):
+            m.set_norm_weights(1.0 + 0.1 * rng.standard_normal(d))
+        xe = dev(x0)
+        gt.stack_forward_device(layers, T, xe.data_ptr(), path=path)
+        torch.cuda.synchronize()
+        eager = xe.cpu().numpy().copy()
+
+        xg = dev(x0)
+        with gt.Graph.capture_stack(layers, T, xg.data_ptr(), path=path) as g:
+            for rep in range(3):
+                xg.copy_(dev(x0))  # the stack updates x in place: reset it
+                torch.cuda.synchronize()
+                g.launch()
+                torch.cuda.synchronize()
+                assert np.array_equal(xg.cpu().numpy(), eager), rep
+                xe.copy_(dev(x0))
+                gt.stack_forward_device(layers, T, xe.data_ptr(), path=path)
+                torch.cuda.synchronize()
+    finally:
+        for m in layers:
+            m.destroy()
+    assert np.all(np.isfinite(eager))
+
+
+def test_graph_capture_rejects_bad_arguments(ctx):
+    spec = make_moe(gt.encode_rows, d=64, h=64, E=4, k=2, S=0, precision=INT8, seed=40)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        with pytest.raises(gt.InvalidArgument):
+            gt.Graph.capture_forward(m, -1, 0, 0)
+        with pytest.raises(gt.InvalidArgument):
+            gt.Graph.capture_forward(m, 4, 0, 0)  # null buffers
+    finally:
+        m.destroy()
