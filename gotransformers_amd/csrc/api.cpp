@@ -297,7 +297,7 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
         {(void **)&w.load, (size_t)L->E * 4},           {(void **)&w.offsets, (size_t)(L->E + 1) * 4},
         {(void **)&w.rows, TK * 4},                     {(void **)&w.pos, TK * 4},
         {(void **)&w.goff, (size_t)(L->G + 1) * 4},     {(void **)&w.tile_off, (size_t)(L->G + 1) * 4},
-        {(void **)&w.tile_desc, ((size_t)L->S * cap + TK + L->G + 1) * sizeof(int4)},
+        {(void **)&w.tile_desc, ((size_t)L->S * cap + TK + L->G + 1 + 8) * sizeof(int4)},
         {(void **)&w.tok, P * 4},                       {(void **)&w.hidden32, P * L->hp * 4},
         {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
         {(void **)&w.chunk_cnt, (size_t)dispatch_chunks(cap) * L->E * 4},

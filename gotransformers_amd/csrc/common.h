@@ -112,6 +112,7 @@ struct MfmaArgs {
     const int32_t *tok;    // gate/up: gather by token; down: nullptr
     const int32_t *count;  // number of m-tiles (the rest of the grid exits)
     const int4 *desc;      // per m-tile: group, first position, positions, 0
+    int ntiles_n;          // column tiles (set by the launcher)
     void *out;  // bf16: gate/up hidden rows, down slot outputs
     int ldo;
     float clamp;

@@ -21,10 +21,13 @@
 // the two steps.  The activations are read from LDS in the same permuted K
 // order.  The next step's global loads are in flight during the MFMAs.
 //
-// Tiles: blockIdx.x enumerates the m-tiles of all groups (the dispatch
-// kernel wrote their count and a (group, first position, positions)
-// descriptor per tile; blocks past the last tile exit), blockIdx.y the
-// column tiles.
+// Tiles: the m-tiles of all groups (the dispatch kernel wrote their count
+// and a (group, first position, positions) descriptor per tile; blocks past
+// the last tile exit) times the column tiles, in a 1-D grid ordered for the
+// XCDs: the hardware hands block b to XCD b % 8, so block b takes m-tile
+// 8*(j / NT) + b % 8 and column tile j % NT with j = b / 8 -- the column
+// tiles of one m-tile run back to back on one XCD and find its activation
+// rows in that XCD's L2.
 #include "common.h"
 
 namespace gtmoe {
@@ -132,9 +135,11 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
 {
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDA];
 
-    const int tile = blockIdx.x;
+    const int j8 = blockIdx.x >> 3;
+    const int tile = (j8 / a.ntiles_n) * 8 + (blockIdx.x & 7);
+    const int ntile = j8 % a.ntiles_n;
     const int ntiles = *a.count;
-    const int4 dsc = a.desc[tile];  // in bounds for every tile of the grid
+    const int4 dsc = a.desc[tile];  // in bounds: the table has 8 entries of slack past the largest tile count
     if (tile >= ntiles) return;
     const int g = dsc.x;
     const int p0 = dsc.y;  // first position of the tile
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     int ncol[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int n = GATEUP ? blockIdx.y * (BN / 2) + wave * 32 + col : blockIdx.y * BN + wave * 64 + j * 32 + col;
+        const int n = GATEUP ? ntile * (BN / 2) + wave * 32 + col : ntile * BN + wave * 64 + j * 32 + col;
         ncol[j] = n;
         const int nr = min(n, a.n - 1);
         const void *w = GATEUP ? (j ? a.w1 : a.w0) : a.w0;
@@ -304,11 +309,13 @@ hipError_t launch_mfma(const MfmaArgs &a, int precision, int max_tiles, hipStrea
     if (max_tiles <= 0) return hipSuccess;
     if (a.kp % BK != 0) return hipErrorInvalidValue;
     constexpr int COLS = GATEUP ? BN / 2 : BN;  // output columns per tile
-    dim3 grid(max_tiles, (a.n + COLS - 1) / COLS);
+    MfmaArgs b = a;
+    b.ntiles_n = (a.n + COLS - 1) / COLS;
+    const dim3 grid((unsigned)((max_tiles + 7) / 8 * 8 * b.ntiles_n));
     switch (precision) {
-    case kInt8: hipLaunchKernelGGL((mfma_gemm_kernel<kInt8, GATEUP>), grid, dim3(256), 0, s, a); break;
-    case kFP4: hipLaunchKernelGGL((mfma_gemm_kernel<kFP4, GATEUP>), grid, dim3(256), 0, s, a); break;
-    case kFloat32: hipLaunchKernelGGL((mfma_gemm_kernel<kFloat32, GATEUP>), grid, dim3(256), 0, s, a); break;
+    case kInt8: hipLaunchKernelGGL((mfma_gemm_kernel<kInt8, GATEUP>), grid, dim3(256), 0, s, b); break;
+    case kFP4: hipLaunchKernelGGL((mfma_gemm_kernel<kFP4, GATEUP>), grid, dim3(256), 0, s, b); break;
+    case kFloat32: hipLaunchKernelGGL((mfma_gemm_kernel<kFloat32, GATEUP>), grid, dim3(256), 0, s, b); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
