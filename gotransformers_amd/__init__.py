@@ -35,6 +35,9 @@ EXPORTED = [
     "gtmoe_route_from_logits", "gtmoe_stack_forward", "gtmoe_stack_forward_device", "gtmoe_timing_enable",
     "gtmoe_timing_reset", "gtmoe_timing_read", "gtmoe_last_path", "gtmoe_relaunch",
     "gtmoe_graph_capture_forward", "gtmoe_graph_capture_stack", "gtmoe_graph_launch", "gtmoe_graph_destroy",
+    "gtmoe_weights_file_open", "gtmoe_weights_file_close", "gtmoe_weights_file_error", "gtmoe_weights_file_count",
+    "gtmoe_weights_file_entry", "gtmoe_weights_file_find", "gtmoe_weights_file_values", "gtmoe_weights_file_rows",
+    "gtmoe_layer_load_weights",
 ]
 
 
@@ -102,6 +105,15 @@ def library():
         "gtmoe_graph_capture_stack": ([P, i32, i32, P, P, u32, P], i32),
         "gtmoe_graph_launch": ([P, P], i32),
         "gtmoe_graph_destroy": ([P], i32),
+        "gtmoe_weights_file_open": ([C.c_char_p, P, P, i32], i32),
+        "gtmoe_weights_file_close": ([P], i32),
+        "gtmoe_weights_file_error": ([P], C.c_char_p),
+        "gtmoe_weights_file_count": ([P, P], i32),
+        "gtmoe_weights_file_entry": ([P, i32, P, i32, P, P, P, P, P], i32),
+        "gtmoe_weights_file_find": ([P, C.c_char_p, P], i32),
+        "gtmoe_weights_file_values": ([P, i32, P, C.c_int64], i32),
+        "gtmoe_weights_file_rows": ([P, i32, P, C.c_int64, P, C.c_int64], i32),
+        "gtmoe_layer_load_weights": ([P, P, C.c_char_p], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -269,6 +281,11 @@ class MixtureOfExperts:
         s = _rows_struct(rows)
         self.ctx.check(library().gtmoe_upload_rows(self.handle, ROLES[(kind, which)], index, C.byref(s), b.ctypes.data))
 
+    def load_weights(self, weights_file, name):
+        """LoadBinary of this layer's parameters, named `name`.shared<i>...,
+        `name`.expert<i>... and `name`.router..., from an open WeightsFile."""
+        self.ctx.check(library().gtmoe_layer_load_weights(self.handle, weights_file.handle, name.encode()))
+
     def upload_router(self, rows, biases):
         b = np.ascontiguousarray(biases, np.float64)
         s = _rows_struct(rows)
@@ -419,3 +436,102 @@ class Graph:
 
     def __exit__(self, *exc):
         self.destroy()
+
+
+# --------------------------------------------------------------------------
+# binary weights files
+# --------------------------------------------------------------------------
+
+STORED_FLOAT64, STORED_FLOAT32, STORED_BFLOAT16, STORED_ROWS = 1, 2, 3, 4
+
+
+class WeightsFile:
+    """An opened GoTransformers binary weights file (weightfile/binaryfile.go).
+
+    values(name) is ReadBinary's float64 list for a plain parameter;
+    rows(name) is the lowprecision.Rows of a compressed one, as a namespace
+    with precision, rows, width, values and scales in gtmoe_rows storage.
+    Opening raises InvalidArgument with the reference's message for a file
+    ReadBinaryKeepingCompressed refuses."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        err = C.create_string_buffer(1024)
+        code = library().gtmoe_weights_file_open(os.fsencode(path), C.byref(h), err, len(err))
+        if code != OK:
+            raise InvalidArgument(code, err.value.decode(errors="replace"))
+        self.handle = h
+        self.path = path
+
+    def close(self):
+        if self.handle:
+            library().gtmoe_weights_file_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _check(self, code):
+        if code != OK:
+            msg = library().gtmoe_weights_file_error(self.handle)
+            raise InvalidArgument(code, msg.decode(errors="replace") if msg else "")
+
+    def __len__(self):
+        n = C.c_int32(0)
+        self._check(library().gtmoe_weights_file_count(self.handle, C.byref(n)))
+        return n.value
+
+    def entry(self, index):
+        name = C.create_string_buffer(4096)
+        stored, prec = C.c_int32(), C.c_int32()
+        rows, width, count = C.c_int64(), C.c_int64(), C.c_int64()
+        self._check(library().gtmoe_weights_file_entry(self.handle, index, name, len(name), C.byref(stored),
+                                                        C.byref(prec), C.byref(rows), C.byref(width),
+                                                        C.byref(count)))
+        return SimpleNamespace(name=name.value.decode(errors="replace"), stored_as=stored.value,
+                               precision=prec.value, rows=rows.value, width=width.value, count=count.value)
+
+    def entries(self):
+        return [self.entry(i) for i in range(len(self))]
+
+    def names(self):
+        return [e.name for e in self.entries()]
+
+    def find(self, name):
+        i = C.c_int32(-1)
+        self._check(library().gtmoe_weights_file_find(self.handle, name.encode(), C.byref(i)))
+        return i.value
+
+    def _index(self, name):
+        i = self.find(name)
+        if i < 0:
+            raise KeyError(name)
+        return i
+
+    def values(self, name):
+        i = self._index(name)
+        out = np.empty(self.entry(i).count, np.float64)
+        self._check(library().gtmoe_weights_file_values(self.handle, i, out.ctypes.data, out.size))
+        return out
+
+    def rows(self, name):
+        i = self._index(name)
+        e = self.entry(i)
+        if e.stored_as != STORED_ROWS:
+            raise InvalidArgument(ERR_INVALID_ARGUMENT, f"parameter {name!r} holds plain values, not compressed rows")
+        blocks = (e.width + 15) // 16
+        if e.precision == FLOAT64:
+            vals, scales = np.empty(e.rows * e.width, np.float64), None
+        elif e.precision == FLOAT32:
+            vals, scales = np.empty(e.rows * e.width, np.float32), None
+        elif e.precision == INT8:
+            vals, scales = np.empty(e.rows * e.width, np.int8), np.empty(e.rows * blocks, np.float32)
+        else:
+            vals, scales = np.empty(e.rows * ((e.width + 1) // 2), np.uint8), np.empty(e.rows * blocks, np.float32)
+        self._check(library().gtmoe_weights_file_rows(self.handle, i, vals.ctypes.data, vals.nbytes,
+                                                       None if scales is None else scales.ctypes.data,
+                                                       0 if scales is None else scales.size))
+        return SimpleNamespace(precision=e.precision, rows=e.rows, width=e.width, values=vals, scales=scales)

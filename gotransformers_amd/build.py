@@ -26,6 +26,7 @@ SOURCES = [
     ("misc.hip", []),
     ("api.cpp", []),
     ("encode.cpp", ["-ffp-contract=off"]),
+    ("weightfile.cpp", []),
 ]
 
 

@@ -16,6 +16,7 @@
 
 #include "common.h"
 #include "gtmoe.h"
+#include "weightfile.h"
 
 using namespace gtmoe;
 
@@ -254,7 +255,7 @@ int32_t check_rows(gtmoe_context *ctx, const gtmoe_rows *r, int rows, int width)
 // Decoded float64 value i of row `row` (Rows.Row, lowprecision/rows.go:87-119).
 double decoded_value(const gtmoe_rows *r, int row, int i)
 {
-    static const double kFp4[8] = {0, 0.5, 1, 1.5, 2, 3, 4, 6};
+    static const double kFp4[16] = {0, 0.5, 1, 1.5, 2, 3, 4, 6, 0, -0.5, -1, -1.5, -2, -3, -4, -6};
     const size_t blocks = (size_t)(r->width + 15) / 16;
     switch (r->precision) {
     case GTMOE_FLOAT64: return ((const double *)r->values)[(size_t)row * r->width + i];
@@ -265,8 +266,7 @@ double decoded_value(const gtmoe_rows *r, int row, int i)
     default: {
         const uint8_t byte = ((const uint8_t *)r->values)[(size_t)row * ((r->width + 1) / 2) + i / 2];
         const uint8_t code = (i % 2) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 15);
-        const double v = kFp4[code & 7] * (double)r->scales[row * blocks + i / 16];
-        return (code & 8) ? -v : v;
+        return kFp4[code] * (double)r->scales[row * blocks + i / 16];
     }
     }
 }
@@ -1345,6 +1345,131 @@ int32_t gtmoe_last_path(const gtmoe_layer *L, int32_t *path)
 {
     if (!L || !path) return GTMOE_ERR_INVALID_ARGUMENT;
     *path = L->last_path;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_load_weights(gtmoe_layer *L, gtmoe_weights_file *f, const char *name)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (!f || !name) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "weights file or layer name is null");
+
+    // MixtureOfExperts.Parameters order (mixtureofexperts.go:312-324):
+    // shared experts, routed experts, then the router unless hash routing
+    struct Item {
+        std::string base;
+        int role, index;
+        int rows, width;
+        int w, b;  // file entries of .weights and .biases
+    };
+    std::vector<Item> items;
+    const std::string n(name);
+    const char *which[3] = {"gate", "up", "down"};
+    for (int kind = 0; kind < 2; ++kind) {
+        const int count = kind == 0 ? L->S : L->E;
+        for (int i = 0; i < count; ++i)
+            for (int j = 0; j < 3; ++j) {
+                const std::string base = n + (kind == 0 ? ".shared" : ".expert") + std::to_string(i + 1) + "." +
+                                         which[j];
+                const int role = (kind == 0 ? GTMOE_ROLE_SHARED_GATE : GTMOE_ROLE_ROUTED_GATE) + j;
+                items.push_back({base, role, i, j == 2 ? L->d : L->h, j == 2 ? L->h : L->d, -1, -1});
+            }
+    }
+    if (!L->desc.use_hash_routing) items.push_back({n + ".router", GTMOE_ROLE_ROUTER, 0, L->E, L->d, -1, -1});
+
+    // every parameter is checked before any is uploaded, as
+    // CopyIntoKeepingCompressed does (weightfile/weightfile.go:69-108)
+    for (Item &it : items) {
+        const std::string wn = it.base + ".weights", bn = it.base + ".biases";
+        it.w = file_find(f, wn);
+        it.b = file_find(f, bn);
+        if (it.w < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "there is no saved parameter named \"%s\"", wn.c_str());
+        if (it.b < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "there is no saved parameter named \"%s\"", bn.c_str());
+        const FileEntryInfo bi = file_info(f, it.b), wi = file_info(f, it.w);
+        if (bi.count != (uint64_t)it.rows)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                        "saved parameter \"%s\" has %llu values but the parameter it's loading into has %d", bn.c_str(),
+                        (unsigned long long)bi.count, it.rows);
+        const uint64_t want = (uint64_t)it.rows * (uint64_t)it.width;
+        if (it.role == GTMOE_ROLE_ROUTER) {
+            // an uncompressed layer: plain values, or compressed rows of any
+            // shape with as many values (decoded, like Rows.AllValues)
+            if (wi.count != want)
+                return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                            "saved parameter \"%s\" has %llu values but the parameter it's loading into has %llu",
+                            wn.c_str(), (unsigned long long)wi.count, (unsigned long long)want);
+            continue;
+        }
+        if (wi.stored_as != kStoredRows)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                        "parameter \"%s\" is compressed but the file holds it as plain numbers, load it into an "
+                        "uncompressed parameter and compress it again",
+                        wn.c_str());
+        if (wi.rows != (uint64_t)it.rows || wi.width != (uint64_t)it.width)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                        "saved parameter \"%s\" is %llux%llu compressed values but the parameter it's loading into is "
+                        "%dx%d",
+                        wn.c_str(), (unsigned long long)wi.rows, (unsigned long long)wi.width, it.rows, it.width);
+        if (wi.precision != L->desc.precision)
+            return fail(ctx, GTMOE_ERR_UNSUPPORTED,
+                        "saved parameter \"%s\" is at precision %d; the layer's experts are at precision %d on the GPU",
+                        wn.c_str(), wi.precision, L->desc.precision);
+        const uint64_t blocks = ((uint64_t)it.width + 15) / 16;
+        const uint64_t want_codes = wi.precision == GTMOE_INT8  ? want
+                                    : wi.precision == GTMOE_FP4 ? (uint64_t)it.rows * (((uint64_t)it.width + 1) / 2)
+                                                                : want * 4;
+        const uint64_t want_scales = wi.precision == GTMOE_FLOAT32 ? 0 : (uint64_t)it.rows * blocks;
+        if (wi.code_bytes != want_codes || wi.scale_count != want_scales)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                        "saved parameter \"%s\" holds %llu value bytes and %llu scales, %dx%d rows need %llu and %llu",
+                        wn.c_str(), (unsigned long long)wi.code_bytes, (unsigned long long)wi.scale_count, it.rows,
+                        it.width, (unsigned long long)want_codes, (unsigned long long)want_scales);
+    }
+
+    std::vector<double> biases, plain;
+    std::vector<uint8_t> codes;
+    std::vector<float> scales;
+    std::string err;
+    for (const Item &it : items) {
+        if (file_values(f, it.b, biases, err) != GTMOE_OK) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "%s", err.c_str());
+        const FileEntryInfo wi = file_info(f, it.w);
+        gtmoe_rows r{};
+        r.rows = it.rows;
+        r.width = it.width;
+        if (wi.stored_as == kStoredRows) {
+            if (file_rows(f, it.w, codes, scales, err) != GTMOE_OK)
+                return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "%s", err.c_str());
+            gtmoe_rows stored{};
+            stored.precision = wi.precision;
+            stored.rows = (int32_t)wi.rows;
+            stored.width = (int32_t)wi.width;
+            stored.values = codes.data();
+            stored.values_bytes = codes.size();
+            stored.scales = scales.data();
+            stored.scale_count = scales.size();
+            if (it.role == GTMOE_ROLE_ROUTER && (wi.rows != (uint64_t)it.rows || wi.width != (uint64_t)it.width)) {
+                // reshape through the decoded values
+                plain.resize((size_t)wi.count);
+                for (uint64_t row = 0; row < wi.rows; ++row)
+                    for (uint64_t i = 0; i < wi.width; ++i)
+                        plain[(size_t)(row * wi.width + i)] = decoded_value(&stored, (int)row, (int)i);
+                r.precision = GTMOE_FLOAT64;
+                r.values = plain.data();
+                r.values_bytes = plain.size() * sizeof(double);
+            } else {
+                r = stored;
+            }
+        } else {
+            if (file_values(f, it.w, plain, err) != GTMOE_OK)
+                return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "%s", err.c_str());
+            r.precision = GTMOE_FLOAT64;
+            r.values = plain.data();
+            r.values_bytes = plain.size() * sizeof(double);
+        }
+        const int32_t rc = gtmoe_upload_rows(L, it.role, it.index, &r, biases.data());
+        if (rc != GTMOE_OK) return rc;
+    }
     return GTMOE_OK;
 }
 

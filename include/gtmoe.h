@@ -62,6 +62,7 @@ enum gtmoe_path { GTMOE_PATH_AUTO = 0, GTMOE_PATH_FP32 = 1, GTMOE_PATH_BF16 = 2 
 typedef struct gtmoe_context gtmoe_context;
 typedef struct gtmoe_layer gtmoe_layer;
 typedef struct gtmoe_graph gtmoe_graph;
+typedef struct gtmoe_weights_file gtmoe_weights_file;
 
 /* The shape of one MixtureOfExperts.  Mirrors the arguments of
  * NewMixtureOfExperts / NewClampedMixtureOfExperts
@@ -248,6 +249,59 @@ int32_t gtmoe_last_path(const gtmoe_layer *layer, int32_t *path);
  * GTMOE_KERNEL_DOWN of the path the last forward took. */
 enum gtmoe_kernel { GTMOE_KERNEL_GATEUP = 0, GTMOE_KERNEL_DOWN = 1 };
 int32_t gtmoe_relaunch(gtmoe_layer *layer, int32_t kernel, void *stream);
+
+/* ---- binary weights files ----------------------------------------------------
+ * Reading GoTransformers binary weights files, "GOTRANSFORMERS-WEIGHTS-1" and
+ * "-2" (weightfile/binaryfile.go:13-21, layout written at :63-138).  Opening
+ * indexes the file and checks it as ReadBinaryKeepingCompressed does
+ * (binaryfile.go:157-372, with RowsFromSnapshot, lowprecision/rows.go:172-203);
+ * values are read from the file when asked for.  These are host calls and need
+ * no context.  On failure gtmoe_weights_file_open writes the reference's
+ * message, prefixed by the path, into `error` (when error_capacity > 0) and
+ * returns GTMOE_ERR_INVALID_ARGUMENT; later calls leave theirs in
+ * gtmoe_weights_file_error. */
+enum gtmoe_stored_as {
+    GTMOE_STORED_FLOAT64 = 1,
+    GTMOE_STORED_FLOAT32 = 2,
+    GTMOE_STORED_BFLOAT16 = 3,
+    GTMOE_STORED_ROWS = 4 /* lowprecision.Rows: precision, rows, width */
+};
+int32_t gtmoe_weights_file_open(const char *path, gtmoe_weights_file **out, char *error, int32_t error_capacity);
+int32_t gtmoe_weights_file_close(gtmoe_weights_file *file);
+const char *gtmoe_weights_file_error(const gtmoe_weights_file *file);
+/* Parameters in file order.  entry: name (NUL-terminated, cut to capacity),
+ * stored_as, precision (-1 unless ROWS), rows and width (0 unless ROWS), and
+ * count = values, or rows*width.  Any output may be NULL.  find: index of a
+ * name, -1 when absent. */
+int32_t gtmoe_weights_file_count(const gtmoe_weights_file *file, int32_t *count);
+int32_t gtmoe_weights_file_entry(const gtmoe_weights_file *file, int32_t index, char *name, int32_t name_capacity,
+                                 int32_t *stored_as, int32_t *precision, int64_t *rows, int64_t *width,
+                                 int64_t *count);
+int32_t gtmoe_weights_file_find(const gtmoe_weights_file *file, const char *name, int32_t *index);
+/* A plain parameter's `count` values as float64, float32 and bfloat16
+ * widened as readFloat32Values / readBFloat16Values do (binaryfile.go:309-331,
+ * weightfile/precision.go:73-75).  The savedValues map of ReadBinary. */
+int32_t gtmoe_weights_file_values(gtmoe_weights_file *file, int32_t index, double *out, int64_t count);
+/* A compressed parameter's storage as in gtmoe_rows: the list its precision
+ * reads (float64, float32, int8 or packed FP4 bytes; values_bytes long) and its
+ * scale_count float32 scales.  The savedCompressedValues map of
+ * ReadBinaryKeepingCompressed. */
+int32_t gtmoe_weights_file_rows(gtmoe_weights_file *file, int32_t index, void *values, int64_t values_bytes,
+                                float *scales, int64_t scale_count);
+
+/* LoadBinary into one MixtureOfExperts (weightfile/weightfile.go:118-124 over
+ * MixtureOfExperts.Parameters, mixtureofexperts.go:312-324): the parameters
+ * "<name>.shared<i>.{gate,up,down}.{weights,biases}",
+ * "<name>.expert<i>.{gate,up,down}.{weights,biases}" (i from 1,
+ * mixtureofexperts.go:60-67) and, without hash routing,
+ * "<name>.router.{weights,biases}" are moved from the file into the layer's
+ * device buffers.  Every parameter is checked before any is uploaded, with
+ * the messages of checkSavedParameterFits (weightfile.go:69-87): expert
+ * weights must be compressed rows of the layer's shape; the router takes
+ * plain values or compressed rows of as many values.  Expert rows at a
+ * precision other than the layer's return GTMOE_ERR_UNSUPPORTED (the
+ * reference would switch the layer's precision). */
+int32_t gtmoe_layer_load_weights(gtmoe_layer *layer, gtmoe_weights_file *file, const char *name);
 
 #ifdef __cplusplus
 }
