@@ -306,8 +306,11 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
     for (const Part &p : parts) total += align_up(p.bytes, 256);
     void *base = nullptr;
     HIP_TRY(ctx, hipMalloc(&base, total));
-    // zero once: padding columns of the activation buffers are never written
+    // zero once: padding columns of the activation buffers are never written.
+    // hipMemset runs on the null stream, which does not order against the
+    // non-blocking streams the forward runs on: wait for it here.
     HIP_TRY(ctx, hipMemset(base, 0, total));
+    HIP_TRY(ctx, hipDeviceSynchronize());
     size_t off = 0;
     for (const Part &p : parts) {
         *p.ptr = (char *)base + off;
@@ -747,6 +750,8 @@ int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtm
             hipMalloc(&L->router_wn, rw) != hipSuccess || hipMemset(L->router_wn, 0, rw) != hipSuccess)
             rc = fail(ctx, GTMOE_ERR_OUT_OF_MEMORY, "cannot allocate the router");
     }
+    // the zeroing memsets above run on the null stream (see ensure_workspace)
+    if (rc == GTMOE_OK && hipDeviceSynchronize() != hipSuccess) rc = fail(ctx, GTMOE_ERR_DEVICE, "device sync failed");
     if (rc != GTMOE_OK) {
         gtmoe_layer_destroy(L);
         return rc;
