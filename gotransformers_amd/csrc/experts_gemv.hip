@@ -56,13 +56,25 @@ struct ChunkRegs {
     float s[MATS][Chunk<PREC>::CB];
 };
 
-// Chunks in flight per wave (register ring): about 4 KiB of codes per wave
-// (measured best; deeper rings lose more to occupancy than they gain).
-template <int PREC, int MATS>
+// Chunks in flight per wave (register ring).
+template <int PREC, int MATS, int NQ>
 constexpr int ring_depth()
 {
-    return Chunk<PREC>::U * MATS >= 4 ? 1 : 2;
+    return 2;
 }
+
+// One weight matrix's panel as buffer resources: the panel's codes (64 rows
+// side by side in 16-byte units) and its scales.  The resources live in
+// scalar registers; a lane addresses its row with one 32-bit offset and a
+// chunk with a scalar offset, so the loads cost one vector register of
+// address in all, and a load past the panel returns zeros.
+struct PanelSrc {
+    __amdgpu_buffer_rsrc_t codes;
+    __amdgpu_buffer_rsrc_t scales;
+};
+
+// descriptor word 3 for raw (untyped) buffer access on CDNA
+constexpr int kRawBufferWord3 = 0x00020000;
 
 template <int I>
 __device__ __forceinline__ uint32_t comp(const uint4 &v)
@@ -157,32 +169,33 @@ struct Staged {
 
 // Codes (and scales) of chunk ch of the lane's row, for every matrix.  A
 // chunk of CB blocks starts at block ch*CB; its scales are CB consecutive
-// floats of the row's 4-block scale group.
+// floats of the row's 4-block scale group.  vo = lane * 16; ch is uniform
+// across the wave.
 template <int PREC, int MATS>
-__device__ __forceinline__ void load_chunk(ChunkRegs<PREC, MATS> &r, const char *const (&w)[MATS],
-                                           const float *const (&sc)[MATS], int ch)
+__device__ __forceinline__ void load_chunk(ChunkRegs<PREC, MATS> &r, const PanelSrc (&src)[MATS], uint32_t vo, int ch)
 {
     constexpr int U = Chunk<PREC>::U, CB = Chunk<PREC>::CB;
 #pragma unroll
     for (int m = 0; m < MATS; ++m) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            r.c[m][u] = *reinterpret_cast<const uint4 *>(w[m] + (size_t)(ch * U + u) * 1024);
+            r.c[m][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src[m].codes, vo,
+                                                                                        (ch * U + u) * 1024, 0));
         if constexpr (PREC != kFloat32) {
             const int b = ch * CB;
-            const float *p = sc[m] + (size_t)(b >> 2) * 256 + (b & 3);
+            const int so = (b >> 2) * 1024 + (b & 3) * 4;
             if constexpr (CB == 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(p);
+                const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(src[m].scales, vo, so, 0));
                 r.s[m][0] = v.x;
                 r.s[m][1] = v.y;
                 r.s[m][2] = v.z;
                 r.s[m][3] = v.w;
             } else if constexpr (CB == 2) {
-                const float2 v = *reinterpret_cast<const float2 *>(p);
+                const float2 v = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(src[m].scales, vo, so, 0));
                 r.s[m][0] = v.x;
                 r.s[m][1] = v.y;
             } else {
-                r.s[m][0] = *p;
+                r.s[m][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src[m].scales, vo, so, 0));
             }
         }
     }
@@ -268,7 +281,8 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
     constexpr int NT = 4 * NQ;
     constexpr int MATS = GATEUP ? 2 : 1;
     constexpr int CB = Chunk<PREC>::CB;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kp = a.nblocks * 16;
     const int ng8 = kp / 8;
 
@@ -276,46 +290,109 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
     // biases) are issued before the token rows are staged
     const int nch = a.nblocks / CB;
     const int c0 = wave * nch / NW, c1 = (wave + 1) * nch / NW;
-    const char *w[MATS];
-    const float *sc[MATS];
-    const size_t wpanel = (size_t)panel * 64 * a.row_bytes + (size_t)lane * 16;
-    const size_t spanel = (size_t)panel * 64 * a.nblocks + (size_t)lane * 4;
-    w[0] = reinterpret_cast<const char *>(a.w0) + (size_t)g * a.w_group_stride + wpanel;
-    sc[0] = PREC == kFloat32 ? nullptr : a.s0 + (size_t)g * a.s_group_stride + spanel;
-    if constexpr (GATEUP) {
-        w[1] = reinterpret_cast<const char *>(a.w1) + (size_t)g * a.w_group_stride + wpanel;
-        sc[1] = PREC == kFloat32 ? nullptr : a.s1 + (size_t)g * a.s_group_stride + spanel;
+    PanelSrc src[MATS];
+    {
+        const size_t wpanel = (size_t)panel * 64 * a.row_bytes;
+        const int wbytes = 64 * a.row_bytes;
+        src[0].codes = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char *>(reinterpret_cast<const char *>(a.w0)) + (size_t)g * a.w_group_stride + wpanel, 0, wbytes,
+            kRawBufferWord3);
+        if constexpr (GATEUP)
+            src[1].codes = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<char *>(reinterpret_cast<const char *>(a.w1)) + (size_t)g * a.w_group_stride + wpanel, 0,
+                wbytes, kRawBufferWord3);
+        if constexpr (PREC != kFloat32) {
+            const size_t spanel = (size_t)panel * 64 * a.nblocks;
+            const int sbytes = 64 * a.nblocks * 4;
+            src[0].scales = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(a.s0) + (size_t)g * a.s_group_stride + spanel, 0, sbytes, kRawBufferWord3);
+            if constexpr (GATEUP)
+                src[1].scales = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<float *>(a.s1) + (size_t)g * a.s_group_stride + spanel, 0, sbytes, kRawBufferWord3);
+        }
     }
-    constexpr int kDepth = ring_depth<PREC, MATS>();
+    const uint32_t vo = (uint32_t)lane * 16;
+
+    // The wave stages the slice's tokens for its own K range only (groups of
+    // 8 k-values [g0, g0 + gn)) as bf16 hi / lo, so no workgroup barrier is
+    // needed before the main loop.  Item i of a lane is token lane % NT
+    // (64 is a multiple of NT) at group g0 + (lane + 64 i) / NT: the lanes'
+    // 16-byte LDS stores are contiguous.  The token loads are issued before
+    // the weight prefetch, the conversion after it, so the wait for the
+    // tokens overlaps the first weight chunks' latency.  Padding tokens
+    // (t >= M) read past the input buffer and get zeros.
+    const int g0 = c0 * CB * 2, gn = (c1 - c0) * CB * 2;
+    const int items = NT * gn;
+    const int ipl = (items + 63) / 64;  // items per lane, <= NT
+    const int t = lane % NT;
+    uint32_t rowoff = 0x80000000u;  // past the buffer: zeros
+    if (t < M) {
+        const int srow = GATEUP ? a.tok[p0 + t] : p0 + t;
+        rowoff = (uint32_t)srow * (uint32_t)a.ld_in * 4u;
+    }
+    const __amdgpu_buffer_rsrc_t xin =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.in), 0, 0x7fffffff, kRawBufferWord3);
+    auto token_off = [&](int idx) {
+        return idx < items ? rowoff + (uint32_t)(g0 + idx / NT) * 32u : 0x80000000u;
+    };
+    auto stage = [&](int idx, const float4 &v0, const float4 &v1, uint4 *xhi, uint4 *xlo) {
+        uint4 h, l;
+        split_pair(v0.x, v0.y, h.x, l.x);
+        split_pair(v0.z, v0.w, h.y, l.y);
+        split_pair(v1.x, v1.y, h.z, l.z);
+        split_pair(v1.z, v1.w, h.w, l.w);
+        const int at = (g0 + idx / NT) * NT + t;
+        xhi[at] = h;
+        xlo[at] = l;
+    };
+    // the first kEarly items per lane go ahead of the weight prefetch (all
+    // of them up to 2 KiB of K per wave); any others are staged after it
+    constexpr int kEarly = 2;
+    float4 xv[kEarly][2];
+#pragma unroll
+    for (int i = 0; i < kEarly; ++i) {
+        if (i < ipl) {  // wave-uniform
+            const uint32_t off = token_off(lane + 64 * i);
+            xv[i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 0, 0));
+            xv[i][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 16, 0));
+        }
+    }
+
+    constexpr int kDepth = ring_depth<PREC, MATS, NQ>();
+    // Every load of the ring is issued unconditionally, so that the compiler
+    // can count the loads in flight and wait for one chunk at a time (loads
+    // under a branch make it wait for all of them).  Past the wave's last
+    // chunk the ring re-loads that chunk: cache hits, never used.
+    const int clast = c1 > c0 ? c1 - 1 : c0;
     ChunkRegs<PREC, MATS> r[kDepth];
 #pragma unroll
-    for (int i = 0; i < kDepth; ++i)
-        if (c0 + i < c1) load_chunk<PREC, MATS>(r[i], w, sc, c0 + i);
+    for (int i = 0; i < kDepth; ++i) load_chunk<PREC, MATS>(r[i], src, vo, min(c0 + i, clast));
     const int row = panel * 64 + lane;
     const bool writer = wave < 4 && row < a.rows;
     float bias[MATS];
 #pragma unroll
     for (int m = 0; m < MATS; ++m) bias[m] = writer ? (m == 0 ? a.b0 : a.b1)[(size_t)g * a.rows + row] : 0.f;
 
-    // stage the slice's token rows as bf16 hi / lo
     uint4 *xhi = reinterpret_cast<uint4 *>(lds);
     uint4 *xlo = xhi + (size_t)ng8 * NT;
-    for (int idx = tid; idx < NT * ng8; idx += blockDim.x) {
-        const int t = idx / ng8, g8 = idx - t * ng8;
-        uint4 h = make_uint4(0, 0, 0, 0), l = make_uint4(0, 0, 0, 0);
-        if (t < M) {
-            const int src = GATEUP ? a.tok[p0 + t] : p0 + t;
-            const float4 *p = reinterpret_cast<const float4 *>(a.in + (size_t)src * a.ld_in) + 2 * g8;
-            const float4 v0 = p[0], v1 = p[1];
-            split_pair(v0.x, v0.y, h.x, l.x);
-            split_pair(v0.z, v0.w, h.y, l.y);
-            split_pair(v1.x, v1.y, h.z, l.z);
-            split_pair(v1.z, v1.w, h.w, l.w);
-        }
-        xhi[g8 * NT + t] = h;
-        xlo[g8 * NT + t] = l;
+#pragma unroll
+    for (int i = 0; i < kEarly; ++i) {
+        const int idx = lane + 64 * i;
+        if (i < ipl && idx < items) stage(idx, xv[i][0], xv[i][1], xhi, xlo);
     }
-    __syncthreads();
+    for (int i = kEarly; i < ipl; ++i) {
+        const int idx = lane + 64 * i;
+        const uint32_t off = token_off(idx);
+        const float4 v0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 0, 0));
+        const float4 v1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 16, 0));
+        if (idx < items) stage(idx, v0, v1, xhi, xlo);
+    }
+    // the wave reads back only what it wrote; LDS operations of a wave are
+    // performed in order, so a wait for its own stores is enough
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     const Staged<NT> xs{xhi, xlo};
     const int tl = lane & 3;
@@ -331,10 +408,8 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
     for (int ch = c0; ch < c1; ch += kDepth) {
 #pragma unroll
         for (int j = 0; j < kDepth; ++j) {
-            if (ch + j < c1) {
-                compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
-                if (ch + j + kDepth < c1) load_chunk<PREC, MATS>(r[j], w, sc, ch + j + kDepth);
-            }
+            if (ch + j < c1) compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
+            load_chunk<PREC, MATS>(r[j], src, vo, min(ch + j + kDepth, clast));
         }
     }
 
