@@ -452,6 +452,7 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         a.row_bytes = L->gate.row_bytes;
         a.in = w.xf;
         a.ld_in = L->dp;
+        a.in_rows = w.cap;
         a.tok = w.tok;
         a.count = w.tile_off + L->G;
         a.desc = w.tile_desc;
@@ -473,6 +474,7 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         b.row_bytes = L->down.row_bytes;
         b.in = w.hidden32;
         b.ld_in = L->hp;
+        b.in_rows = (long long)w.cap * (L->S + L->k);
         b.tok = nullptr;
         b.count = w.tile_off + L->G;
         b.desc = w.tile_desc;
@@ -496,6 +498,7 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         a.nblocks = L->gate.nblocks;
         a.a = w.xb;
         a.lda = L->dp;
+        a.a_rows = w.cap;
         a.tok = w.tok;
         a.count = w.tile_off + L->G;
         a.desc = w.tile_desc;
@@ -518,6 +521,7 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         b.nblocks = L->down.nblocks;
         b.a = w.hidden16;
         b.lda = L->hp;
+        b.a_rows = (long long)w.cap * (L->S + L->k);
         b.tok = nullptr;
         b.count = w.tile_off + L->G;
         b.desc = w.tile_desc;

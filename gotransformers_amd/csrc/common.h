@@ -82,6 +82,7 @@ struct GemvArgs {
     int row_bytes;
     const float *in;
     int ld_in;
+    long long in_rows;      // rows of the input buffer (bounds its loads)
     const int32_t *tok;     // gate/up: token of every position; down: nullptr
     const int32_t *count;   // number of token slices (the rest of the grid exits)
     const int4 *desc;       // per slice: group, first position, positions, 0
@@ -109,6 +110,7 @@ struct MfmaArgs {
     int nblocks;
     const uint16_t *a;  // bf16 activations
     int lda;
+    long long a_rows;   // rows of the activation buffer (bounds its loads)
     const int32_t *tok;    // gate/up: gather by token; down: nullptr
     const int32_t *count;  // number of m-tiles (the rest of the grid exits)
     const int4 *desc;      // per m-tile: group, first position, positions, 0

@@ -330,8 +330,8 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
         const int srow = GATEUP ? a.tok[p0 + t] : p0 + t;
         rowoff = (uint32_t)srow * (uint32_t)a.ld_in * 4u;
     }
-    const __amdgpu_buffer_rsrc_t xin =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.in), 0, 0x7fffffff, kRawBufferWord3);
+    const __amdgpu_buffer_rsrc_t xin = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.in), 0, (int)(a.in_rows * a.ld_in * 4), kRawBufferWord3);
     auto token_off = [&](int idx) {
         return idx < items ? rowoff + (uint32_t)(g0 + idx / NT) * 32u : 0x80000000u;
     };
@@ -520,6 +520,8 @@ template <bool GATEUP>
 hipError_t launch_any(const GemvArgs &a, int precision, int max_slices, hipStream_t s)
 {
     if (max_slices <= 0) return hipSuccess;
+    // the input rows are read through a buffer resource with 32-bit offsets
+    if (a.in_rows <= 0 || a.in_rows * a.ld_in * 4 > 0x7fffffffLL) return hipErrorInvalidValue;
     switch (precision) {
     case kInt8: return launch_prec<GATEUP, kInt8>(a, max_slices, s);
     case kFP4: return launch_prec<GATEUP, kFP4>(a, max_slices, s);

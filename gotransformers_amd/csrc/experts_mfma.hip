@@ -28,6 +28,8 @@
 // 8*(j / NT) + b % 8 and column tile j % NT with j = b / 8 -- the column
 // tiles of one m-tile run back to back on one XCD and find its activation
 // rows in that XCD's L2.
+#include <type_traits>
+
 #include "common.h"
 
 namespace gtmoe {
@@ -75,20 +77,38 @@ struct BRaw<kFloat32> {
     uint4 q[2][4];
 };
 
-// Block b of the lane's row (`row` = its first unit, `srow` = its first
-// scale group in the panel layout).
+// descriptor word 3 for raw (untyped) buffer access on CDNA
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// One group's weight matrix as buffer resources (codes and scales in the
+// panel layout).  Loads past the group read zeros: column tiles past the
+// matrix need no clamping.
+struct GroupSrc {
+    __amdgpu_buffer_rsrc_t codes;
+    __amdgpu_buffer_rsrc_t scales;
+};
+
+// Block b = 4m + 2p + h of the K step's lane row, where m = k0 / 64 and h =
+// lane / 32 (the lane's half).  vo / vs: the lane's byte offsets of its row
+// (plus its half's share) in the codes / scales; the rest is scalar.
 template <int PREC>
-__device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const char *row, const float *srow, int b)
+__device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc &src, uint32_t vo, uint32_t vs,
+                                           int m, int p)
 {
     if constexpr (PREC == kInt8) {
-        r.q[i] = *reinterpret_cast<const uint4 *>(row + (size_t)b * 1024);
-        r.s[i] = srow[(size_t)(b >> 2) * 256 + (b & 3)];
+        // unit b, scale (b >> 2, b & 3); vo carries h * 1024, vs h * 4
+        r.q[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, (4 * m + 2 * p) * 1024, 0));
+        r.s[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.scales, vs, (m * 256 + 2 * p) * 4, 0));
     } else if constexpr (PREC == kFP4) {
-        r.q[i] = *reinterpret_cast<const uint2 *>(row + (size_t)(b >> 1) * 1024 + (b & 1) * 8);
-        r.s[i] = srow[(size_t)(b >> 2) * 256 + (b & 3)];
+        // unit b >> 1 = 2m + p, byte (b & 1) * 8; vo carries h * 8
+        r.q[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.codes, vo, (2 * m + p) * 1024, 0));
+        r.s[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.scales, vs, (m * 256 + 2 * p) * 4, 0));
     } else {
+        // units 4b .. 4b + 3; vo carries 4h * 1024
 #pragma unroll
-        for (int u = 0; u < 4; ++u) r.q[i][u] = *reinterpret_cast<const uint4 *>(row + (size_t)(4 * b + u) * 1024);
+        for (int u = 0; u < 4; ++u)
+            r.q[i][u] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, ((4 * m + 2 * p) * 4 + u) * 1024, 0));
     }
 }
 
@@ -148,47 +168,42 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, h = lane >> 5;
 
-    // activations: thread -> one row, half of the K step (32 values)
+    // activations: thread -> one row, half of the K step (32 values); rows
+    // past the tile read past the buffer and get zeros
     const int ar = tid >> 1, ah = tid & 1;
-    const bool a_ok = ar < M;
-    const uint16_t *arow =
-        a.a + (size_t)(a_ok ? (GATEUP ? a.tok[p0 + ar] : p0 + ar) : 0) * a.lda + ah * 32;
+    const __amdgpu_buffer_rsrc_t asrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(a.a), 0, (int)(a.a_rows * a.lda * 2), kRawBufferWord3);
+    uint32_t aoff = 0x80000000u;
+    if (ar < M) aoff = ((uint32_t)(GATEUP ? a.tok[p0 + ar] : p0 + ar) * (uint32_t)a.lda + ah * 32) * 2u;
 
-    // weights: the wave's two column tiles; rows past n read row n-1 and are
-    // not written
-    const char *brow[2];
-    const float *bsrow[2];
+    // weights: the wave's two column tiles (gate/up: the same 32 neurons of
+    // gate and up; down: 64 consecutive rows), a group's matrices as buffer
+    // resources; columns past n read zeros and are not written
+    GroupSrc bsrc[2];
+    uint32_t bvo[2], bvs[2];
     int ncol[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = GATEUP ? ntile * (BN / 2) + wave * 32 + col : ntile * BN + wave * 64 + j * 32 + col;
         ncol[j] = n;
-        const int nr = min(n, a.n - 1);
         const void *w = GATEUP ? (j ? a.w1 : a.w0) : a.w0;
         const float *sc = GATEUP ? (j ? a.s1 : a.s0) : a.s0;
-        brow[j] = reinterpret_cast<const char *>(w) + (size_t)g * a.w_group_stride + panel_unit_offset(nr, 0, a.row_bytes);
-        bsrow[j] = PREC == kFloat32 ? nullptr : sc + (size_t)g * a.s_group_stride + panel_scale_index(nr, 0, a.nblocks);
+        bsrc[j].codes = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char *>(reinterpret_cast<const char *>(w)) + (size_t)g * a.w_group_stride, 0,
+            (int)a.w_group_stride, kRawBufferWord3);
+        const uint32_t rowoff = (uint32_t)(n / 64) * 64u * (uint32_t)a.row_bytes + (uint32_t)(n % 64) * 16u;
+        if constexpr (PREC == kInt8) bvo[j] = rowoff + h * 1024u;
+        else if constexpr (PREC == kFP4) bvo[j] = rowoff + h * 8u;
+        else bvo[j] = rowoff + h * 4096u;
+        if constexpr (PREC != kFloat32) {
+            bsrc[j].scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(sc) + (size_t)g * a.s_group_stride, 0,
+                                                             (int)(a.s_group_stride * 4), kRawBufferWord3);
+            bvs[j] = ((uint32_t)(n / 64) * 64u * (uint32_t)a.nblocks + (uint32_t)(n % 64) * 4u + h) * 4u;
+        } else {
+            bsrc[j].scales = bsrc[j].codes;
+            bvs[j] = 0;
+        }
     }
-
-    uint4 av[4];
-    BRaw<PREC> bq[2];
-    auto load_a = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            av[i] = a_ok ? *reinterpret_cast<const uint4 *>(arow + k0 + 8 * i) : make_uint4(0, 0, 0, 0);
-    };
-    auto load_b = [&](int k0) {
-        // pair p of the step: this lane's block is 2p + h
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int p = 0; p < 2; ++p) load_block<PREC>(bq[j], p, brow[j], bsrow[j], k0 / 16 + 2 * p + h);
-    };
-    auto store_a = [&](int buf) {
-        uint4 *pa = reinterpret_cast<uint4 *>(&As[buf][ar][ah * 32]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pa[i] = av[i];
-    };
 
     floatx16 acc[4][2];
 #pragma unroll
@@ -198,44 +213,105 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    load_a(0);
-    load_b(0);
-    store_a(0);
-    __syncthreads();
-    int buf = 0;
-    for (int k0 = 0; k0 < a.kp; k0 += BK) {
-        const bool more = k0 + BK < a.kp;
-        bf16x8 bf[2][2][2];  // [tile][pair][step]
+    // Software pipeline of distance 2: during step k the loads of step k+2
+    // are in flight (A into registers av[k % 2], B into bq[k % 2]) and A of
+    // step k+1 waits in av[(k+1) % 2] to be stored to LDS at the end of the
+    // step.  The loop is unrolled by two so the stage indices are constants;
+    // every load is issued unconditionally (steps past the end re-load the
+    // last step: cache hits, never used) so that the compiler waits for each
+    // stage's loads alone, and a scheduling barrier keeps the refill of a
+    // stage behind the instructions that consume it.
+    const int nsteps = a.kp / BK;
+    uint4 av[2][4];
+    BRaw<PREC> bq[2][2];  // [stage][column tile]
+    auto load_a = [&](uint4 (&v)[4], int step) {
+        const int k0 = min(step, nsteps - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(asrc, aoff, k0 * 2 + 16 * i, 0));
+    };
+    auto load_b = [&](BRaw<PREC> (&q)[2], int step) {
+        const int m = min(step, nsteps - 1);
+        // pair p of the step: this lane's block is 2p + h
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int p = 0; p < 2; ++p)
+            for (int p = 0; p < 2; ++p) load_block<PREC>(q[j], p, bsrc[j], bvo[j], bvs[j], m, p);
+    };
+    auto store_a = [&](int buf, const uint4 (&v)[4]) {
+        uint4 *pa = reinterpret_cast<uint4 *>(&As[buf][ar][ah * 32]);
 #pragma unroll
-                for (int st = 0; st < 2; ++st) bf[j][p][st] = dequant_half<PREC>(bq[j], p, st);
-        if (more) {
-            load_a(k0 + BK);
-            load_b(k0 + BK);
+        for (int i = 0; i < 4; ++i) pa[i] = v[i];
+    };
+    // The K step is done in two halves (pair p = 0, 1: 16 MFMAs each, K
+    // values of scale blocks 2p and 2p + 1).  While the MFMAs of one half run,
+    // the same wave dequantizes the B operands of the next half, so the VALU
+    // work hides under the matrix cores: the scheduling groups below ask for
+    // one MFMA, then four VALU instructions, in turn.
+    auto dequant_pair = [&](const BRaw<PREC> (&q)[2], int p, bf16x8 (&out)[2][2]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) out[j][s2] = dequant_half<PREC>(q[j], p, s2);
+    };
+    auto mfma_pair = [&](int buf, int p, const bf16x8 (&bfp)[2][2]) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            // k-values of this MFMA step: lanes of half h carry values
+            // 8s2..8s2+7 of block 2p + h of the K step
+            const int kk = 16 * (2 * p + h) + 8 * s2;
+            bf16x8 af[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][i * 32 + col][kk]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfp[j][s2], acc[i][j], 0, 0, 0);
         }
+    };
+    auto interleave = [&]() {
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int s2 = 0; s2 < 2; ++s2) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the LDS reads of the A operands
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                // k-values of this MFMA step: lanes of half h carry values
-                // 8st..8st+7 of block 2p + h of the K step
-                const int kk = 16 * (2 * p + h) + 8 * st;
-                bf16x8 af[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][i * 32 + col][kk]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j][p][st], acc[i][j], 0, 0, 0);
+            for (int m = 0; m < 8; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
             }
-        if (more) store_a(buf ^ 1);
+        }
+    };
+    bf16x8 bfa[2][2], bfb[2][2];  // B operands of the current and the next half step
+    // step k of the pipeline (ST = k % 2); bfa holds pair 0 of step k
+    auto step = [&](auto st_tag, int k) {
+        constexpr int ST = decltype(st_tag)::value;
+        mfma_pair(ST, 0, bfa);
+        dequant_pair(bq[ST], 1, bfb);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(av[ST], k + 2);
+        load_b(bq[ST], k + 2);
+        mfma_pair(ST, 1, bfb);
+        dequant_pair(bq[ST ^ 1], 0, bfa);  // pair 0 of step k + 1 (past the end: unused)
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + 1 < nsteps) store_a(ST ^ 1, av[ST ^ 1]);
         __syncthreads();
-        buf ^= 1;
+    };
+
+    load_a(av[0], 0);
+    load_b(bq[0], 0);
+    load_a(av[1], 1);
+    load_b(bq[1], 1);
+    store_a(0, av[0]);
+    dequant_pair(bq[0], 0, bfa);
+    __syncthreads();
+    int k = 0;
+    for (; k + 1 < nsteps; k += 2) {
+        step(std::integral_constant<int, 0>{}, k);
+        step(std::integral_constant<int, 1>{}, k + 1);
     }
+    if (k < nsteps) step(std::integral_constant<int, 0>{}, k);
 
     // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows
     // 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r.  Full tiles
@@ -308,6 +384,11 @@ hipError_t launch_mfma(const MfmaArgs &a, int precision, int max_tiles, hipStrea
 {
     if (max_tiles <= 0) return hipSuccess;
     if (a.kp % BK != 0) return hipErrorInvalidValue;
+    // activations and each group's weights are read through buffer resources
+    // with 32-bit offsets
+    if (a.a_rows <= 0 || a.a_rows * a.lda * 2 > 0x7fffffffLL || a.w_group_stride > 0x7fffffffLL ||
+        a.s_group_stride * 4 > 0x7fffffffLL)
+        return hipErrorInvalidValue;
     constexpr int COLS = GATEUP ? BN / 2 : BN;  // output columns per tile
     MfmaArgs b = a;
     b.ntiles_n = (a.n + COLS - 1) / COLS;
