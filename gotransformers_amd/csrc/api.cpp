@@ -357,7 +357,8 @@ struct Inputs {
 // Input preparation, routing and dispatch.  Few tokens: one fused launch.
 // Otherwise: convert or RMSNorm into ws.xf / ws.xb, router and top-k (or hash
 // routing), then the dispatch.  token_ids: device pointer (hash routing).
-int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t *token_ids, int path, hipStream_t s)
+int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t *token_ids, int path, hipStream_t s,
+                          float *zero_out = nullptr)
 {
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
@@ -404,9 +405,11 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         f.tok = w.tok;
         f.tile_off = w.tile_off;
         f.tile_desc = w.tile_desc;
+        f.zero_out = zero_out;
         RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, s));
         return GTMOE_OK;
     }
+    if (zero_out) RUN(ctx, s, "zero_out", launch_fill_i32(reinterpret_cast<int32_t *>(zero_out), T * L->d, 0, s));
     if (in.norm) {
         RUN(ctx, s, "rmsnorm", launch_rmsnorm((const float *)in.x, T, L->d, L->norm_w, xf, L->dp, xb, L->dp, s));
     } else if (in.f64) {
@@ -430,7 +433,7 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
 
 // The expert kernels over the dispatched positions, reading ws.xf (fp32
 // path) or ws.xb (bf16 path); leaves the slot outputs in ws.slot_out.
-int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
+int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s, float *final_out = nullptr)
 {
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
@@ -480,6 +483,15 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s)
         b.desc = w.tile_desc;
         b.out = w.slot_out;
         b.ld_out = L->d;
+        if (final_out) {
+            b.final_out = final_out;
+            b.tok_all = w.tok;
+            b.chosen = w.chosen;
+            b.gates32 = w.gates32;
+            b.T = T;
+            b.k = L->k;
+            b.S = L->S;
+        }
         L->last_gemv[1] = b;
         RUN(ctx, s, "gemv_down", launch_gemv_down(b, L->down.precision, max_tiles, s));
     } else {
@@ -955,12 +967,16 @@ static int32_t forward_device_run(gtmoe_layer *L, int32_t T, const float *inputs
         return GTMOE_OK;
     }
     Workspace &w = L->ws;
-    int32_t rc = prepare_and_route(L, T, Inputs{inputs, false, false}, token_ids, path, s);
-    if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
+    // With at most two contributions per output row the fp32 path folds the
+    // combine into the down kernel (order-independent adds onto zeroed rows).
+    float *fold = path == GTMOE_PATH_FP32 && L->S + L->k <= 2 ? outputs : nullptr;
+    int32_t rc = prepare_and_route(L, T, Inputs{inputs, false, false}, token_ids, path, s, fold);
+    if (rc == GTMOE_OK) rc = run_experts(L, T, path, s, fold);
     if (rc != GTMOE_OK) return rc;
-    RUN(ctx, s, "combine",
-        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr, outputs,
-                       nullptr, s));
+    if (!fold)
+        RUN(ctx, s, "combine",
+            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr,
+                           outputs, nullptr, s));
     mark_forward(L, T, path, s);
     return GTMOE_OK;
 }

@@ -89,6 +89,15 @@ struct GemvArgs {
     float *out;
     int ld_out;
     float clamp;
+    // down only, when every output row has at most two contributions (shared
+    // experts + routed slots <= 2): instead of writing slot rows, add
+    // weight * row into final[token][:] (zeroed beforehand).  Two fp32 terms
+    // added onto zero give the same bits in either order.
+    float *final_out;        // [T][d] or nullptr
+    const int32_t *tok_all;  // token of every position
+    const int32_t *chosen;   // [T][k]
+    const float *gates32;    // [T][k]
+    int T, k, S;
 };
 
 // Tokens per work slice of the GEMV path (the dispatch's tile size there).
@@ -138,6 +147,7 @@ struct FusedArgs {
     float *gates32;
     int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off;
     int4 *tile_desc;
+    float *zero_out;  // [T][d] rows zeroed by the token's workgroup, or nullptr
 };
 
 // Launchers (each returns the hipError_t of its launch).

@@ -447,6 +447,19 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
                 uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
             }
             *out = silu(gv) * uv;
+        } else if (a.final_out) {
+            // the combine of mixtureofexperts.go:192-205 for at most two
+            // contributions per row: shared experts with weight 1, a routed
+            // expert with its token's gate for it
+            const int tk = a.tok_all[p0 + t];
+            float wgt = 1.0f;
+            if (g >= a.S) {
+                const int e = g - a.S;
+                for (int j = 0; j < a.k; ++j)
+                    if (a.chosen[(size_t)tk * a.k + j] == e) wgt = a.gates32[(size_t)tk * a.k + j];
+            }
+            __hip_atomic_fetch_add(a.final_out + (size_t)tk * a.rows + row, wgt * (v[0] + bias[0]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         } else {
             *out = v[0] + bias[0];
         }

@@ -842,6 +842,8 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
         if (a.xf) a.xf[(size_t)t * a.kp + i] = v;
         if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
     }
+    if (a.zero_out)
+        for (int i = threadIdx.x; i < a.d; i += 1024) a.zero_out[(size_t)t * a.d + i] = 0.f;
     __syncthreads();
     if (wave == 0) {
         if (HASH) {

@@ -246,7 +246,11 @@ int32_t gtmoe_last_path(const gtmoe_layer *layer, int32_t *path);
  * events gives the kernel's duration free of per-launch event skew -- the
  * per-dispatch timing of Recorder.MeasureTime (gpu/compute.go:670-694) for a
  * single program.  kernel: GTMOE_KERNEL_GATEUP (gate/up + SwiGLU) or
- * GTMOE_KERNEL_DOWN of the path the last forward took. */
+ * GTMOE_KERNEL_DOWN of the path the last forward took.  When the last
+ * forward was a gtmoe_forward_device on the fp32 path of a layer with at
+ * most two experts per token in all (shared + routed), its down kernel adds
+ * the weighted rows straight into the caller's outputs (the combine is
+ * folded into it), so launching it again adds them once more. */
 enum gtmoe_kernel { GTMOE_KERNEL_GATEUP = 0, GTMOE_KERNEL_DOWN = 1 };
 int32_t gtmoe_relaunch(gtmoe_layer *layer, int32_t kernel, void *stream);
 

@@ -27,10 +27,12 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
 
 
-@pytest.mark.parametrize("T,path", [(16, gt.PATH_FP32), (1, gt.PATH_FP32), (64, gt.PATH_BF16)])
-def test_graph_forward_replays_equal_eager(ctx, T, path):
-    say(f"graph forward T={T} path={path}")
-    spec = make_moe(gt.encode_rows, d=256, h=512, E=8, k=2, S=1, precision=INT8, seed=21)
+@pytest.mark.parametrize("T,path,S", [(16, gt.PATH_FP32, 1), (1, gt.PATH_FP32, 1), (64, gt.PATH_BF16, 1),
+                                      (16, gt.PATH_FP32, 0), (3, gt.PATH_FP32, 0)])
+def test_graph_forward_replays_equal_eager(ctx, T, path, S):
+    # S = 0 with top-2: the combine is folded into the down kernel
+    say(f"graph forward T={T} path={path} S={S}")
+    spec = make_moe(gt.encode_rows, d=256, h=512, E=8, k=2, S=S, precision=INT8, seed=21)
     rng = np.random.default_rng(22)
     x0 = rng.standard_normal((T, 256))
     x1 = rng.standard_normal((T, 256))

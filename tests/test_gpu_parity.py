@@ -16,6 +16,8 @@ import pytest
 
 import gotransformers_amd as gt
 import oracle
+
+torch = pytest.importorskip("torch")
 from tests.moe_fixtures import FLOAT32, FP4, INT8, make_moe, zipf_router_bias
 
 pytestmark = pytest.mark.gpu
@@ -166,6 +168,42 @@ def test_c2_int8_decode(ctx, T):
     e = rel_err(y, ref.outputs)
     say(f"C2 T={T} max rel err {e:.3e}")
     assert e <= FP32_TOL
+
+
+@pytest.mark.parametrize("name,cfg,prec,T", [
+    ("C2 top-2", dict(d=1024, h=2048, E=16, k=2, S=0), INT8, 1),
+    ("C2 top-2", dict(d=1024, h=2048, E=16, k=2, S=0), INT8, 32),
+    ("top-2, two slices per expert", dict(d=4, h=6, E=4, k=2, S=0), FP4, 29),
+    ("top-1 with one shared", dict(d=37, h=53, E=5, k=1, S=1), INT8, 29),
+])
+def test_device_forward_folds_two_term_combine(ctx, name, cfg, prec, T):
+    """With at most two contributions per output row (shared + routed <= 2)
+    the fp32 device forward adds them straight into the zeroed outputs from
+    the down kernel; fp32 addition of two terms onto zero does not depend on
+    their order, so repeated forwards are bit-identical, and the result
+    matches the oracle and the host-path forward (which runs the combine
+    kernel)."""
+    say(f"folded combine {name} T={T}")
+    spec = make_moe(gt.encode_rows, precision=prec, seed=9, std=0.1, bias_std=0.02, **cfg)
+    x = np.random.default_rng(10 + T).normal(size=(T, cfg["d"]))
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        xd = torch.from_numpy(x.astype(np.float32)).cuda()
+        y1 = torch.full((T, cfg["d"]), float("nan"), device="cuda")
+        y2 = torch.full((T, cfg["d"]), float("nan"), device="cuda")
+        m.forward_device(T, xd.data_ptr(), y1.data_ptr(), path=gt.PATH_FP32)
+        m.forward_device(T, xd.data_ptr(), y2.data_ptr(), path=gt.PATH_FP32)
+        torch.cuda.synchronize()
+        r = m.last_routing()
+        a, b = y1.cpu().numpy(), y2.cpu().numpy()
+        host = m.forward(x.astype(np.float32).astype(np.float64), path=gt.PATH_FP32)
+    finally:
+        m.destroy()
+    assert np.array_equal(a, b)
+    assert np.all(np.isfinite(a))
+    ref = oracle.moe_forward_routed(spec, x.astype(np.float32).astype(np.float64), r.chosen, r.gates)
+    assert rel_err(a, ref.outputs) <= FP32_TOL
+    assert rel_err(a, host) <= 1e-6
 
 
 # --------------------------------------------------------------------------- reference invariants on the device
