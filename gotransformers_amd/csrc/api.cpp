@@ -172,6 +172,10 @@ struct gtmoe_layer {
     hipStream_t last_stream = nullptr;
     std::vector<int32_t> last_load;
     bool load_on_host = false;
+    // the decode path's expert kernels found their own tokens: the dispatch
+    // tables (load, rows_for_expert, offsets) are built only when read
+    bool skipped_dispatch = false;  // by the forward being enqueued
+    bool dispatch_pending = false;  // by the last forward
 };
 
 namespace {
@@ -406,9 +410,12 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         f.tile_off = w.tile_off;
         f.tile_desc = w.tile_desc;
         f.zero_out = zero_out;
-        RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, s));
+        // the fp32 path's kernels find their own tokens from the choices
+        L->skipped_dispatch = path == GTMOE_PATH_FP32 && T <= kSelfDispatchMaxTokens;
+        RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, !L->skipped_dispatch, s));
         return GTMOE_OK;
     }
+    L->skipped_dispatch = false;
     if (zero_out) RUN(ctx, s, "zero_out", launch_fill_i32(reinterpret_cast<int32_t *>(zero_out), T * L->d, 0, s));
     if (in.norm) {
         RUN(ctx, s, "rmsnorm", launch_rmsnorm((const float *)in.x, T, L->d, L->norm_w, xf, L->dp, xb, L->dp, s));
@@ -438,8 +445,21 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s, float *final
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
     const int bm = path == GTMOE_PATH_BF16 ? mfma_tile_m() : kGemvSlice;
-    // upper bound of the tiles / slices over all groups
-    const int max_tiles = L->S * ((T + bm - 1) / bm) + (T * L->k + bm - 1) / bm + L->E;
+    // upper bound of the tiles / slices over all groups; without dispatch
+    // tables, the shared slices plus two workgroups per routed expert
+    const bool self = path == GTMOE_PATH_FP32 && L->skipped_dispatch;
+    const int max_tiles = self ? L->S * ((T + bm - 1) / bm) + 2 * L->E
+                               : L->S * ((T + bm - 1) / bm) + (T * L->k + bm - 1) / bm + L->E;
+    auto set_self = [&](GemvArgs &g) {
+        g.self_dispatch = 1;
+        g.shared_slices = (T + kGemvSlice - 1) / kGemvSlice;
+        g.T = T;
+        g.k = L->k;
+        g.S = L->S;
+        g.E = L->E;
+        g.chosen = w.chosen;
+        g.gates32 = w.gates32;
+    };
     if (path == GTMOE_PATH_FP32) {
         GemvArgs a{};
         a.w0 = L->gate.values;
@@ -462,6 +482,7 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s, float *final
         a.out = w.hidden32;
         a.ld_out = L->hp;
         a.clamp = (float)L->desc.clamp_limit;
+        if (self) set_self(a);
         L->last_gemv[0] = a;
         L->last_max_tiles = max_tiles;
         L->relaunch_ready = true;
@@ -492,6 +513,7 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s, float *final
             b.k = L->k;
             b.S = L->S;
         }
+        if (self) set_self(b);
         L->last_gemv[1] = b;
         RUN(ctx, s, "gemv_down", launch_gemv_down(b, L->down.precision, max_tiles, s));
     } else {
@@ -551,6 +573,22 @@ void mark_forward(gtmoe_layer *L, int T, int path, hipStream_t s)
     L->last_path = path;
     L->last_stream = s;
     L->load_on_host = false;
+    L->dispatch_pending = T > 0 && L->skipped_dispatch;
+}
+
+// Build the dispatch tables of the last forward if its kernels skipped them
+// (the same kernel as a forward's dispatch, so the tables are identical).
+int32_t ensure_dispatch(gtmoe_layer *L)
+{
+    if (!L->dispatch_pending) return GTMOE_OK;
+    gtmoe_context *ctx = L->ctx;
+    Workspace &w = L->ws;
+    hipStream_t s = L->last_stream;
+    RUN(ctx, s, "dispatch",
+        launch_dispatch(w.chosen, L->last_T, L->k, L->E, L->S, kGemvSlice, w.load, w.offsets, w.rows, w.pos, w.goff,
+                        w.tok, w.tile_off, w.tile_desc, w.chunk_cnt, s));
+    L->dispatch_pending = false;
+    return GTMOE_OK;
 }
 
 int32_t fetch_load(gtmoe_layer *L)
@@ -558,6 +596,8 @@ int32_t fetch_load(gtmoe_layer *L)
     gtmoe_context *ctx = L->ctx;
     if (L->last_T < 0) return fail(ctx, GTMOE_ERR_NOT_READY, "call Forward before reading the expert load");
     if (L->load_on_host) return GTMOE_OK;
+    int32_t rc = ensure_dispatch(L);
+    if (rc != GTMOE_OK) return rc;
     L->last_load.assign(L->E, 0);
     if (L->last_T > 0) {
         HIP_TRY(ctx, hipStreamSynchronize(L->last_stream));
@@ -599,6 +639,7 @@ struct gtmoe_graph {
     hipGraphExec_t exec = nullptr;
     std::vector<gtmoe_layer *> layers;
     std::vector<int> paths;
+    std::vector<char> skipped;  // per layer: its recorded forward builds no dispatch tables
     int T = 0;
 };
 
@@ -930,14 +971,19 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
     RUN(ctx, s, "combine",
-        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr, nullptr,
+        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos, w.gates32, nullptr, nullptr,
                        w.y64, s));
     HIP_TRY(ctx, hipMemcpyAsync(outputs, w.y64, sizeof(double) * T * L->d, hipMemcpyDeviceToHost, s));
-    L->last_load.assign(L->E, 0);
-    HIP_TRY(ctx, hipMemcpyAsync(L->last_load.data(), w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost, s));
+    // the load comes back with the outputs unless the dispatch was skipped
+    // (then it is built when read)
+    const bool load_now = !L->skipped_dispatch;
+    if (load_now) {
+        L->last_load.assign(L->E, 0);
+        HIP_TRY(ctx, hipMemcpyAsync(L->last_load.data(), w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost, s));
+    }
     HIP_TRY(ctx, hipStreamSynchronize(s));
     mark_forward(L, T, path, s);
-    L->load_on_host = true;
+    L->load_on_host = load_now;
     return GTMOE_OK;
 }
 
@@ -975,7 +1021,7 @@ static int32_t forward_device_run(gtmoe_layer *L, int32_t T, const float *inputs
     if (rc != GTMOE_OK) return rc;
     if (!fold)
         RUN(ctx, s, "combine",
-            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, nullptr,
+            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos, w.gates32, nullptr,
                            outputs, nullptr, s));
     mark_forward(L, T, path, s);
     return GTMOE_OK;
@@ -1011,6 +1057,8 @@ int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen,
         if (expert_offsets) memset(expert_offsets, 0, sizeof(int32_t) * (L->E + 1));
         return GTMOE_OK;
     }
+    int32_t rc = ensure_dispatch(L);
+    if (rc != GTMOE_OK) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(L->last_stream));
     const size_t tk = (size_t)T * L->k;
     Workspace &w = L->ws;
@@ -1076,6 +1124,7 @@ int32_t gtmoe_route_from_logits(gtmoe_layer *L, int32_t tokens, const double *lo
         launch_dispatch(w.chosen, T, L->k, L->E, L->S, mfma_tile_m(), w.load, w.offsets, w.rows, w.pos, w.goff,
                         w.tok, w.tile_off, w.tile_desc, w.chunk_cnt, s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
+    L->skipped_dispatch = false;
     mark_forward(L, T, L->last_path, s);
     L->relaunch_ready = false;
     return gtmoe_last_routing(L, nullptr, chosen, gates, load, rows_for_expert, expert_offsets);
@@ -1118,7 +1167,7 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
         if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
         if (rc != GTMOE_OK) return rc;
         RUN(ctx, s, "combine",
-            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, w.pos, w.gates32, x, x, nullptr,
+            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos, w.gates32, x, x, nullptr,
                            s));
         mark_forward(L, T, path, s);
     }
@@ -1217,6 +1266,7 @@ int32_t gtmoe_graph_capture_forward(gtmoe_layer *L, int32_t tokens, const float 
         free_graph(g);
         return rc;
     }
+    g->skipped = {(char)L->skipped_dispatch};
     *graph = g;
     return GTMOE_OK;
 }
@@ -1255,6 +1305,7 @@ int32_t gtmoe_graph_capture_stack(gtmoe_layer *const *layers, int32_t n_layers, 
         free_graph(g);
         return rc;
     }
+    for (int l = 0; l < n_layers; ++l) g->skipped.push_back((char)layers[l]->skipped_dispatch);
     *graph = g;
     return GTMOE_OK;
 }
@@ -1267,7 +1318,10 @@ int32_t gtmoe_graph_launch(gtmoe_graph *g, void *stream)
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     HIP_TRY(ctx, hipGraphLaunch(g->exec, s));
-    for (size_t i = 0; i < g->layers.size(); ++i) mark_forward(g->layers[i], g->T, g->paths[i], s);
+    for (size_t i = 0; i < g->layers.size(); ++i) {
+        g->layers[i]->skipped_dispatch = g->skipped[i] != 0;
+        mark_forward(g->layers[i], g->T, g->paths[i], s);
+    }
     return GTMOE_OK;
 }
 

@@ -98,10 +98,21 @@ struct GemvArgs {
     const int32_t *chosen;   // [T][k]
     const float *gates32;    // [T][k]
     int T, k, S;
+    // Few tokens (self_dispatch): no dispatch tables.  Grid row y < S *
+    // shared_slices is a slice of 8 tokens of a shared expert; the next 2E
+    // rows are two workgroups per routed expert e (rows y and y + E), which
+    // find e's (token, slot) entries in `chosen` and take every other pass
+    // of 8.  Rows are indexed directly: shared expert s, token t at s*T + t;
+    // routed entry t*k + j at S*T + t*k + j.  list_off: LDS offset of the
+    // entry list (set by the launcher; room for T*k entries).
+    int self_dispatch, shared_slices, list_off, E;
 };
 
 // Tokens per work slice of the GEMV path (the dispatch's tile size there).
 constexpr int kGemvSlice = 8;
+// Up to this many tokens the fp32 path's expert kernels find their own
+// tokens in the routing choices and no dispatch launch runs.
+constexpr int kSelfDispatchMaxTokens = 64;
 
 // Arguments of the grouped MFMA GEMM kernels (bf16 path).
 struct MfmaArgs {
@@ -164,7 +175,7 @@ hipError_t launch_topk(const double *logits, int T, int E, int k, const double *
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,
                              float *gates32, hipStream_t s);
 bool fused_route_fits(int T, int k, int kp);
-hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s);
+hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, bool dispatch, hipStream_t s);
 // Dispatch: one workgroup up to 1024 tokens, else a count and a placement
 // launch over chunks of 256 tokens using chunk_cnt [dispatch_chunks(T)][E]
 // as scratch.

@@ -274,14 +274,48 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<PREC, MATS> &r, co
     }
 }
 
+// Where the M rows of a slice come from: positions p0 .. p0 + M - 1 of the
+// dispatch (kByPosition), the routed (token, slot) entries list[0 .. M) of one
+// expert, entry i = token * k + slot (kByEntry), or tokens t0 .. t0 + M - 1 of
+// shared expert s (kShared).
+enum { kByPosition = 0, kByEntry = 1, kShared = 2 };
+struct SliceSrc {
+    int mode;
+    int p0;
+    const int *list;
+    int t0, s;
+};
+
+// input row (token row for gate/up, hidden row for down) and output row of
+// slice token t
+template <bool GATEUP, int MODE>
+__device__ __forceinline__ int slice_in_row(const GemvArgs &a, const SliceSrc &sl, int t)
+{
+    if constexpr (MODE == kByPosition) return GATEUP ? a.tok[sl.p0 + t] : sl.p0 + t;
+    else if constexpr (MODE == kByEntry) return GATEUP ? sl.list[t] / a.k : a.S * a.T + sl.list[t];
+    else return GATEUP ? sl.t0 + t : sl.s * a.T + sl.t0 + t;
+}
+template <int MODE>
+__device__ __forceinline__ int slice_out_row(const GemvArgs &a, const SliceSrc &sl, int t)
+{
+    if constexpr (MODE == kByPosition) return sl.p0 + t;
+    else if constexpr (MODE == kByEntry) return a.S * a.T + sl.list[t];
+    else return sl.s * a.T + sl.t0 + t;
+}
+
 // One slice of M <= 4*NQ tokens of group g against panel `panel`.
-template <int PREC, bool GATEUP, int NW, int NQ>
-__device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, int p0, int M, int panel)
+template <int PREC, bool GATEUP, int NW, int NQ, int MODE>
+__device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, const SliceSrc &sl, int M, int panel)
 {
     constexpr int NT = 4 * NQ;
     constexpr int MATS = GATEUP ? 2 : 1;
     constexpr int CB = Chunk<PREC>::CB;
-    const int tid = threadIdx.x, lane = tid & 63;
+    // the empty asm hides where tid comes from, so that a caller's loop over
+    // slices cannot hoist the lane-dependent set-up out of the loop and keep
+    // it live across the main loop (that costs about 16 VGPRs)
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kp = a.nblocks * 16;
     const int ng8 = kp / 8;
@@ -326,10 +360,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
     const int ipl = (items + 63) / 64;  // items per lane, <= NT
     const int t = lane % NT;
     uint32_t rowoff = 0x80000000u;  // past the buffer: zeros
-    if (t < M) {
-        const int srow = GATEUP ? a.tok[p0 + t] : p0 + t;
-        rowoff = (uint32_t)srow * (uint32_t)a.ld_in * 4u;
-    }
+    if (t < M) rowoff = (uint32_t)slice_in_row<GATEUP, MODE>(a, sl, t) * (uint32_t)a.ld_in * 4u;
     const __amdgpu_buffer_rsrc_t xin = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(a.in), 0, (int)(a.in_rows * a.ld_in * 4), kRawBufferWord3);
     auto token_off = [&](int idx) {
@@ -438,7 +469,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
             for (int wv = 0; wv < NW; ++wv) s += red[slot(wv, m, q, wave)];
             v[m] = s;
         }
-        float *out = a.out + (size_t)(p0 + t) * a.ld_out + row;
+        float *out = a.out + (size_t)slice_out_row<MODE>(a, sl, t) * a.ld_out + row;
         if constexpr (GATEUP) {
             float gv = v[0] + bias[0];
             float uv = v[1] + bias[MATS - 1];
@@ -451,12 +482,20 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
             // the combine of mixtureofexperts.go:192-205 for at most two
             // contributions per row: shared experts with weight 1, a routed
             // expert with its token's gate for it
-            const int tk = a.tok_all[p0 + t];
+            int tk;
             float wgt = 1.0f;
-            if (g >= a.S) {
-                const int e = g - a.S;
-                for (int j = 0; j < a.k; ++j)
-                    if (a.chosen[(size_t)tk * a.k + j] == e) wgt = a.gates32[(size_t)tk * a.k + j];
+            if constexpr (MODE == kByEntry) {
+                tk = sl.list[t] / a.k;
+                wgt = a.gates32[sl.list[t]];
+            } else if constexpr (MODE == kShared) {
+                tk = sl.t0 + t;
+            } else {
+                tk = a.tok_all[sl.p0 + t];
+                if (g >= a.S) {
+                    const int e = g - a.S;
+                    for (int j = 0; j < a.k; ++j)
+                        if (a.chosen[(size_t)tk * a.k + j] == e) wgt = a.gates32[(size_t)tk * a.k + j];
+                }
             }
             __hip_atomic_fetch_add(a.final_out + (size_t)tk * a.rows + row, wgt * (v[0] + bias[0]), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -471,18 +510,71 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, i
 // blockIdx.x = panel of 64 output rows, blockIdx.y = token slice (the
 // dispatch wrote the slice count and a (group, first position, positions)
 // descriptor per slice; slices past the last exit).
-template <int PREC, bool GATEUP, int NW>
+template <int PREC, bool GATEUP, int NW, bool SELF>
 __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const int item = blockIdx.y;
-    const int nslices = *a.count;
-    const int4 dsc = a.desc[item];  // in bounds for every slice of the grid
-    if (item >= nslices) return;    // workgroup-uniform
-    const int g = dsc.x, p0 = dsc.y, M = dsc.z;
-    if (M <= 0) return;  // workgroup-uniform
-    if (M <= 4) run_slice<PREC, GATEUP, NW, 1>(a, lds, g, p0, M, blockIdx.x);
-    else run_slice<PREC, GATEUP, NW, 2>(a, lds, g, p0, M, blockIdx.x);
+    const int y = blockIdx.y;
+    if constexpr (!SELF) {
+        const int nslices = *a.count;
+        const int4 dsc = a.desc[y];  // in bounds for every slice of the grid
+        if (y >= nslices) return;    // workgroup-uniform
+        const SliceSrc sl{kByPosition, dsc.y, nullptr, 0, 0};
+        if (dsc.z <= 0) return;  // workgroup-uniform
+        if (dsc.z <= 4) run_slice<PREC, GATEUP, NW, 1, kByPosition>(a, lds, dsc.x, sl, dsc.z, blockIdx.x);
+        else run_slice<PREC, GATEUP, NW, 2, kByPosition>(a, lds, dsc.x, sl, dsc.z, blockIdx.x);
+        return;
+    } else {
+        const int nsh = a.S * a.shared_slices;
+        if (y < nsh) {  // 8 tokens of a shared expert
+            const int s = y / a.shared_slices;
+            const SliceSrc sl{kShared, 0, nullptr, (y - s * a.shared_slices) * kGemvSlice, s};
+            const int m = min(kGemvSlice, a.T - sl.t0);
+            if (m <= 4) run_slice<PREC, GATEUP, NW, 1, kShared>(a, lds, s, sl, m, blockIdx.x);
+            else run_slice<PREC, GATEUP, NW, 2, kShared>(a, lds, s, sl, m, blockIdx.x);
+            return;
+        }
+        // routed expert e: its entries in token order (the order of the
+        // reference's rowsForExpert, mixtureofexperts.go:175-180), found by
+        // wave 0 with ballots over `chosen` (four loads in flight per
+        // round); this workgroup takes passes par, par + 2, ... of 8
+        // entries.  Rows [nsh, nsh + E) are the first halves, [nsh + E,
+        // nsh + 2E) the second, so the second halves (mostly without work at
+        // decode loads) are dispatched after every first half.
+        const int e = (y - nsh) % a.E, par = (y - nsh) / a.E;  // y < nsh + 2E
+        int *list = reinterpret_cast<int *>(lds + a.list_off);
+        int *count = list + a.T * a.k;
+        if (threadIdx.x < 64) {
+            const int lane = threadIdx.x;
+            const int n = a.T * a.k;
+            int c = 0;
+            for (int b0 = 0; b0 < n; b0 += 256) {
+                int ch[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ch[j] = a.chosen[min(b0 + j * 64 + lane, n - 1)];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = b0 + j * 64 + lane;
+                    const bool hit = i < n && ch[j] == e;
+                    const unsigned long long bal = __ballot(hit);
+                    if (hit) list[c + __popcll(bal & ((1ull << lane) - 1ull))] = i;
+                    c += __popcll(bal);
+                }
+            }
+            if (lane == 0) *count = c;
+        }
+        __syncthreads();
+        const int c = __builtin_amdgcn_readfirstlane(*count);
+        for (int first = par * kGemvSlice; first < c; first += 2 * kGemvSlice) {
+            const SliceSrc sl{kByEntry, 0, list + first, 0, 0};
+            const int m = min(kGemvSlice, c - first);
+            int g = a.S + e, panel = blockIdx.x;
+            asm volatile("" : "+s"(g), "+s"(panel));  // as for tid in run_slice
+            if (m <= 4) run_slice<PREC, GATEUP, NW, 1, kByEntry>(a, lds, g, sl, m, panel);
+            else run_slice<PREC, GATEUP, NW, 2, kByEntry>(a, lds, g, sl, m, panel);
+            __syncthreads();  // the next pass re-stages the LDS
+        }
+    }
 }
 
 namespace {
@@ -497,17 +589,25 @@ size_t gemv_lds_bytes(int nblocks, bool gateup, int nw)
 }
 
 template <int PREC, bool GATEUP, int NW>
-hipError_t launch_nw(const GemvArgs &a, int max_slices, hipStream_t s)
+hipError_t launch_nw(const GemvArgs &a0, int max_slices, hipStream_t s)
 {
-    const size_t lds = gemv_lds_bytes(a.nblocks, GATEUP, NW);
+    GemvArgs a = a0;
+    size_t lds = gemv_lds_bytes(a.nblocks, GATEUP, NW);
+    if (a.self_dispatch) {
+        // the routed expert's entry list and its length after the slice's LDS
+        a.list_off = (int)((lds + 15) / 16 * 16);
+        lds = (size_t)a.list_off + ((size_t)a.T * a.k + 1) * sizeof(int);
+    }
     if (lds > 160 * 1024) return hipErrorInvalidValue;
+    const void *fn = a.self_dispatch ? reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW, true>)
+                                     : reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW, false>);
     if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
     const dim3 grid((a.rows + 63) / 64, max_slices);
-    hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW>), grid, dim3(64 * NW), lds, s, a);
+    if (a.self_dispatch) hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW, true>), grid, dim3(64 * NW), lds, s, a);
+    else hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW, false>), grid, dim3(64 * NW), lds, s, a);
     return hipGetLastError();
 }
 

@@ -141,7 +141,9 @@ __device__ __forceinline__ float load1(const uint16_t *p) { return __uint_as_flo
 
 // Weighted combine (mixtureofexperts.go:182-205) in the reference's order:
 // out = 0, + each shared expert's row, then + gate_i * routed row for the
-// slots in chosen order.  With a residual: out = residual + that sum
+// slots in chosen order.  Routed slot rows are found through the dispatch's
+// pos table, or, with pos == nullptr, at S*T + t*k + i (rows indexed by
+// (token, slot), as the self-dispatching decode kernels write them).  With a residual: out = residual + that sum
 // (transformer/block.go:77).  Writes fp32 and/or float64 output.  Grid
 // (T, ceil(d / 1024)); each thread owns four consecutive columns.
 template <typename SlotT>
@@ -158,7 +160,7 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
     float g[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        p[i] = i < k ? S * T + pos[(size_t)t * k + i] : 0;
+        p[i] = i < k ? S * T + (pos ? pos[(size_t)t * k + i] : t * k + i) : 0;
         g[i] = i < k ? gates32[(size_t)t * k + i] : 0.f;
     }
     const int n = min(4, d - j0);

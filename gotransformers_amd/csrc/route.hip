@@ -724,9 +724,9 @@ hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, in
 }
 
 // ---------------------------------------------------------------------------
-// Routing for few tokens (decode) in two launches: route_token_kernel (one
-// workgroup per token: input preparation, router logits, top-k or hash
-// routing) and dispatch_kernel.  With RMSNorm in front
+// Routing for few tokens (decode): route_token_kernel (one workgroup per
+// token: input preparation, router logits, top-k or hash routing), then
+// dispatch_kernel unless the expert kernels find their own tokens.  With RMSNorm in front
 // (normalization/rmsnorm.go:33-53) the norm weights are folded into the
 // router rows (wn = w * norm) and the inverse RMS comes from a pass over the
 // raw row, logit = inv_rms * dot(x, wn) + bias.
@@ -877,13 +877,13 @@ static hipError_t launch_token_typed(const FusedArgs &a, bool hash, hipStream_t 
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, hipStream_t s)
+hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, bool dispatch, hipStream_t s)
 {
     if (!fused_route_fits(a.T, a.k, a.kp)) return hipErrorInvalidValue;
     hipError_t e;
     if (input_f64) e = a.norm ? launch_token_typed<double, true>(a, hash, s) : launch_token_typed<double, false>(a, hash, s);
     else e = a.norm ? launch_token_typed<float, true>(a, hash, s) : launch_token_typed<float, false>(a, hash, s);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || !dispatch) return e;
     hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a.chosen, a.T, a.k, a.E, a.S, a.bm, a.load,
                        a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off, a.tile_desc);
     return hipGetLastError();

@@ -206,6 +206,43 @@ def test_device_forward_folds_two_term_combine(ctx, name, cfg, prec, T):
     assert rel_err(a, host) <= 1e-6
 
 
+@pytest.mark.parametrize("T", [1, 17, 64, 65])
+@pytest.mark.parametrize("use_hash", [False, True])
+def test_decode_kernels_find_their_own_tokens(ctx, T, use_hash):
+    """Up to 64 tokens the fp32 path launches no dispatch: the expert kernels
+    read the routing choices directly (a hot expert takes many passes of 8
+    tokens), and the dispatch tables a caller reads afterwards (load,
+    rowsForExpert, offsets) are built on request and equal the oracle's
+    dispatch of the same choices.  65 tokens takes the dispatch path; both
+    agree with the oracle."""
+    say(f"decode without dispatch T={T} hash={use_hash}")
+    cfg = dict(d=96, h=80, E=6, k=3, S=2)
+    spec = make_moe(gt.encode_rows, precision=FP4, seed=12, std=0.2, bias_std=0.02, use_hash=use_hash, **cfg)
+    if not use_hash:
+        spec.router.biases = zipf_router_bias(cfg["E"], 2.0, seed=3, scale=4.0)  # one expert takes most tokens
+    rng = np.random.default_rng(20 + T)
+    x = rng.uniform(-1, 1, (T, cfg["d"]))
+    ids = rng.integers(0, 5000, T) if use_hash else None
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        y = m.forward(x, ids, path=gt.PATH_FP32)
+        load = m.last_expert_load()
+        r = m.last_routing()
+        y2 = m.forward(x, ids, path=gt.PATH_FP32)
+    finally:
+        m.destroy()
+    assert np.array_equal(y, y2)
+    d = oracle.dispatch(r.chosen, cfg["E"])
+    assert np.array_equal(load, d.load)
+    assert np.array_equal(r.load, d.load)
+    assert np.array_equal(r.offsets, d.offsets)
+    assert np.array_equal(r.rows, d.rows)
+    if not use_hash:
+        assert d.load.max() >= min(T, 17), d.load  # the skew gives many passes to one expert
+    ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates)
+    assert rel_err(y, ref.outputs) <= FP32_TOL
+
+
 # --------------------------------------------------------------------------- reference invariants on the device
 
 @pytest.mark.parametrize("path", [gt.PATH_FP32])
