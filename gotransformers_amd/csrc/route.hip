@@ -271,12 +271,21 @@ __device__ __forceinline__ bool better(double s1, int e1, double s2, int e2)
     return s1 > s2 || (s1 == s2 && e1 < e2);
 }
 
-// Top-k of one token by one wave (EPL experts per lane).  Writes chosen,
-// gates (float64 and fp32) for token t, and the chosen list to `chosen_copy`
-// when given.
+// The balance biases of experts lane + 64 j (0 past E).
+template <int EPL>
+__device__ __forceinline__ void load_balance(const double *__restrict__ balance, int E, int lane, double (&bal)[EPL])
+{
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) bal[j] = lane + 64 * j < E ? balance[lane + 64 * j] : 0.0;
+}
+
+// Top-k of one token by one wave (EPL experts per lane; bal[j] is the
+// balance bias of expert lane + 64 j, loaded ahead by the caller).  Writes
+// chosen, gates (float64 and fp32) for token t, and the chosen list to
+// `chosen_copy` when given.
 template <int EPL>
 __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row, int t, int E, int k,
-                                           const double *__restrict__ balance, int lane, int32_t *__restrict__ chosen,
+                                           const double (&bal)[EPL], int lane, int32_t *__restrict__ chosen,
                                            double *__restrict__ gates, float *__restrict__ gates32,
                                            int32_t *chosen_copy)
 {
@@ -288,7 +297,7 @@ __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row,
         taken[j] = false;
         if (e < E) {
             a[j] = affinity(logit_row[e]);
-            sc[j] = a[j] + balance[e];
+            sc[j] = a[j] + bal[j];
         } else {
             a[j] = 0.0;
             sc[j] = -INFINITY;
@@ -373,7 +382,9 @@ __global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ lo
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;  // wave-uniform
-    topk_token<EPL>(logits + (size_t)t * E, t, E, k, balance, lane, chosen, gates, gates32, nullptr);
+    double bal[EPL];
+    load_balance<EPL>(balance, E, lane, bal);
+    topk_token<EPL>(logits + (size_t)t * E, t, E, k, bal, lane, chosen, gates, gates32, nullptr);
 }
 
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
@@ -757,19 +768,33 @@ __device__ __forceinline__ float4 in4(const double *row, int i)
     return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
 }
 
-// One 1024-thread workgroup per token.  Each lane keeps its share of the
-// token's row in registers (NX float4 runs, d <= 256*NX); the 16 waves share
-// the experts, two router rows in flight at a time; logits go to LDS, then
-// wave 0 runs top-k (or hash routing) and all threads write the token's
-// prepared row (converted or normalised, zero-padded).
+// One 1024-thread workgroup per token.  Every wave keeps the token's row in
+// registers (NX float4 runs per lane, d <= 256*NX); the 16 waves share the
+// experts, two router rows in flight at a time; logits go to LDS, then wave
+// 0 runs top-k (or hash routing).  The token's prepared row (converted or
+// normalised, zero-padded) is written from those registers, run j by wave j
+// (rows whose width is not a multiple of 4 re-read the input).  The small
+// operands (router and balance biases, norm weights) are loaded at the start
+// so that their latency overlaps the row's.
 template <typename InT, bool NORM, bool HASH, int EPL, int NX>
 __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
     __shared__ double lg[kMaxExperts];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = blockIdx.x;
     const InT *xr = reinterpret_cast<const InT *>(a.x) + (size_t)t * a.d;
     const bool vec = (a.d & 3) == 0;
+
+    // router bias of expert wave + 16 j in lane j; balance biases (wave 0)
+    double bias_l = 0.0;
+    double bal[EPL];
+    if (!HASH) {
+        if (wave + 16 * lane < a.E) bias_l = a.bias[wave + 16 * lane];
+        if (wave == 0) load_balance<EPL>(a.balance, a.E, lane, bal);
+    }
+    float4 nv = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (NORM && vec && wave < NX && 4 * lane + 256 * wave < a.d)
+        nv = *reinterpret_cast<const float4 *>(a.norm + 4 * lane + 256 * wave);
 
     float4 xv[NX];
     float ss = 0.f;
@@ -826,21 +851,47 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
                 d0 += __shfl_xor(d0, off);
                 d1 += __shfl_xor(d1, off);
             }
+            // e0 = wave + 16 (2 it), e1 = e0 + 16: lanes 2 it and 2 it + 1
+            const int j0 = (e0 - wave) / 16;
+            const double b0 = __shfl(bias_l, j0), b1 = __shfl(bias_l, j0 + 1);
             if (lane == 0) {
-                lg[e0] = (double)(d0 * inv) + a.bias[e0];
-                if (two) lg[e1] = (double)(d1 * inv) + a.bias[e1];
+                lg[e0] = (double)(d0 * inv) + b0;
+                if (two) lg[e1] = (double)(d1 * inv) + b1;
             }
         }
     }
     // prepared row
-    for (int i = threadIdx.x; i < a.kp; i += 1024) {
-        float v = 0.f;
-        if (i < a.d) {
-            v = in_at(xr, i);
-            if (NORM) v = v * inv * a.norm[i];
+    if (vec) {
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            const int i = 4 * lane + 256 * j;
+            if (j == wave && i < a.kp) {  // i < d, or padding (xv holds zeros there)
+                float4 v = xv[j];
+                if (NORM) {
+                    v.x = v.x * inv * nv.x;
+                    v.y = v.y * inv * nv.y;
+                    v.z = v.z * inv * nv.z;
+                    v.w = v.w * inv * nv.w;
+                    if (i >= a.d) v = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+                if (a.xf) *reinterpret_cast<float4 *>(a.xf + (size_t)t * a.kp + i) = v;
+                if (a.xb) {
+                    const uint2 b = make_uint2((uint32_t)bf16_bits(v.x) | ((uint32_t)bf16_bits(v.y) << 16),
+                                               (uint32_t)bf16_bits(v.z) | ((uint32_t)bf16_bits(v.w) << 16));
+                    *reinterpret_cast<uint2 *>(a.xb + (size_t)t * a.kp + i) = b;
+                }
+            }
         }
-        if (a.xf) a.xf[(size_t)t * a.kp + i] = v;
-        if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
+    } else {
+        for (int i = threadIdx.x; i < a.kp; i += 1024) {
+            float v = 0.f;
+            if (i < a.d) {
+                v = in_at(xr, i);
+                if (NORM) v = v * inv * a.norm[i];
+            }
+            if (a.xf) a.xf[(size_t)t * a.kp + i] = v;
+            if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
+        }
     }
     if (a.zero_out)
         for (int i = threadIdx.x; i < a.d; i += 1024) a.zero_out[(size_t)t * a.d + i] = 0.f;
@@ -849,7 +900,7 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
         if (HASH) {
             if (lane == 0) hash_token(a.ids, t, a.E, a.k, a.chosen, a.gates, a.gates32, nullptr);
         } else {
-            topk_token<EPL>(lg, t, a.E, a.k, a.balance, lane, a.chosen, a.gates, a.gates32, nullptr);
+            topk_token<EPL>(lg, t, a.E, a.k, bal, lane, a.chosen, a.gates, a.gates32, nullptr);
         }
     }
 }
