@@ -37,7 +37,9 @@ EXPORTED = [
     "gtmoe_graph_capture_forward", "gtmoe_graph_capture_stack", "gtmoe_graph_launch", "gtmoe_graph_destroy",
     "gtmoe_weights_file_open", "gtmoe_weights_file_close", "gtmoe_weights_file_error", "gtmoe_weights_file_count",
     "gtmoe_weights_file_entry", "gtmoe_weights_file_find", "gtmoe_weights_file_values", "gtmoe_weights_file_rows",
-    "gtmoe_layer_load_weights",
+    "gtmoe_layer_load_weights", "gtmoe_layer_add_adapters", "gtmoe_layer_remove_adapters", "gtmoe_layer_adapter_rank",
+    "gtmoe_layer_set_adapter", "gtmoe_layer_get_adapter", "gtmoe_layer_adapter_gradients",
+    "gtmoe_layer_zero_adapter_gradients", "gtmoe_backward",
 ]
 
 
@@ -114,6 +116,14 @@ def library():
         "gtmoe_weights_file_values": ([P, i32, P, C.c_int64], i32),
         "gtmoe_weights_file_rows": ([P, i32, P, C.c_int64, P, C.c_int64], i32),
         "gtmoe_layer_load_weights": ([P, P, C.c_char_p], i32),
+        "gtmoe_layer_add_adapters": ([P, i32, dbl, C.c_uint64], i32),
+        "gtmoe_layer_remove_adapters": ([P], i32),
+        "gtmoe_layer_adapter_rank": ([P, i32, i32, P], i32),
+        "gtmoe_layer_set_adapter": ([P, i32, i32, P, P], i32),
+        "gtmoe_layer_get_adapter": ([P, i32, i32, P, P], i32),
+        "gtmoe_layer_adapter_gradients": ([P, i32, i32, P, P], i32),
+        "gtmoe_layer_zero_adapter_gradients": ([P], i32),
+        "gtmoe_backward": ([P, i32, P, P], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -322,6 +332,74 @@ class MixtureOfExperts:
         out = np.empty_like(x)
         self.ctx.check(library().gtmoe_forward(self.handle, x.shape[0], x.ctypes.data, _ptr(ids), out.ctypes.data,
                                                 path))
+        return out
+
+    # ----------------------------------------------------------------- adapters
+
+    @staticmethod
+    def _role(kind, which):
+        """(kind, which) as in upload(), or ("router", None)."""
+        return ROLE_ROUTER if kind == "router" else ROLES[(kind, which)]
+
+    def _adapter_shape(self, kind, which):
+        if kind == "router":
+            return self.vector_size, self.routed_experts
+        if which == "down":
+            return self.expert_hidden_size, self.vector_size
+        return self.vector_size, self.expert_hidden_size
+
+    def add_adapters(self, rank, alpha, seed=0):
+        """Model.AddLowRankAdapters over this mixture's layers
+        (transformer/adapters.go:24-38): rank min(rank, inputs, outputs) per
+        layer, Down uniform in +-1/sqrt(inputs) (seeded here), Up zero."""
+        self.ctx.check(library().gtmoe_layer_add_adapters(self.handle, int(rank), float(alpha), int(seed)))
+
+    def remove_adapters(self):
+        self.ctx.check(library().gtmoe_layer_remove_adapters(self.handle))
+
+    def adapter_rank(self, kind, index=0, which=None):
+        r = C.c_int32(0)
+        self.ctx.check(library().gtmoe_layer_adapter_rank(self.handle, self._role(kind, which), index, C.byref(r)))
+        return r.value
+
+    def set_adapter(self, kind, index, which, down=None, up=None):
+        """Adapter.Down [rank][inputs] and Adapter.Up [outputs][rank] of one
+        layer (kind "shared"/"routed" with which "gate"/"up"/"down", or
+        "router")."""
+        inputs, outputs = self._adapter_shape(kind, which)
+        r = self.adapter_rank(kind, index, which)
+        dn = None if down is None else np.ascontiguousarray(down, np.float64).reshape(r, inputs)
+        u = None if up is None else np.ascontiguousarray(up, np.float64).reshape(outputs, r)
+        self.ctx.check(library().gtmoe_layer_set_adapter(self.handle, self._role(kind, which), index, _ptr(dn),
+                                                          _ptr(u)))
+
+    def adapter(self, kind, index=0, which=None):
+        """(Down, Up) of one layer's adapter."""
+        inputs, outputs = self._adapter_shape(kind, which)
+        r = self.adapter_rank(kind, index, which)
+        dn, u = np.empty((r, inputs)), np.empty((outputs, r))
+        self.ctx.check(library().gtmoe_layer_get_adapter(self.handle, self._role(kind, which), index, dn.ctypes.data,
+                                                          u.ctypes.data))
+        return dn, u
+
+    def adapter_gradients(self, kind, index=0, which=None):
+        """(DownGradients, UpGradients) of one layer's adapter."""
+        inputs, outputs = self._adapter_shape(kind, which)
+        r = self.adapter_rank(kind, index, which)
+        dn, u = np.empty((r, inputs)), np.empty((outputs, r))
+        self.ctx.check(library().gtmoe_layer_adapter_gradients(self.handle, self._role(kind, which), index,
+                                                                dn.ctypes.data, u.ctypes.data))
+        return dn, u
+
+    def zero_adapter_gradients(self):
+        self.ctx.check(library().gtmoe_layer_zero_adapter_gradients(self.handle))
+
+    def backward(self, output_gradients):
+        """MixtureOfExperts.Backward after forward() of the same rows: adds
+        to every adapter's gradients and returns the input gradients."""
+        g = np.ascontiguousarray(np.atleast_2d(output_gradients), np.float64)
+        out = np.empty_like(g)
+        self.ctx.check(library().gtmoe_backward(self.handle, g.shape[0], g.ctypes.data, out.ctypes.data))
         return out
 
     def forward_device(self, tokens, inputs_ptr, outputs_ptr, token_ids_ptr=None, path=PATH_AUTO, stream=None):

@@ -24,6 +24,7 @@ SOURCES = [
     ("experts_gemv.hip", []),
     ("experts_mfma.hip", []),
     ("misc.hip", []),
+    ("lora.hip", []),
     ("api.cpp", []),
     ("encode.cpp", ["-ffp-contract=off"]),
     ("weightfile.cpp", []),

@@ -9,9 +9,13 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
+#include <functional>
+#include <initializer_list>
 #include <map>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -145,6 +149,39 @@ struct Workspace {
     int32_t *chunk_cnt = nullptr;  // [chunks][E] scratch of the many-token dispatch
 };
 
+// Low-rank adapters of one weight role over all groups (G = S + E), or of
+// the router (G = 1): A [G][R][kin], B [G][rows][R] fp32, zero beyond each
+// layer's rank and widths; dA, dB their float64 gradient sums.
+struct AdapterSet {
+    int R = 0, kin = 0, width = 0, rows = 0, G = 0;
+    float *A = nullptr, *B = nullptr, *scale = nullptr;
+    double *dA = nullptr, *dB = nullptr;
+};
+
+// What the adapter path's forward keeps for the backward, sized for `cap`
+// tokens (P = cap * (S + k) positions).
+struct TrainWorkspace {
+    int cap = -1;
+    std::vector<void *> blocks;
+    float *gpre = nullptr, *upre = nullptr;  // [P][hp] pre-activations of gate and up
+    float *u_gate = nullptr, *u_up = nullptr, *u_down = nullptr, *u_router = nullptr;  // x A^T per position / token
+    double *og = nullptr;    // [T][d] output gradients
+    float *eg = nullptr;     // [P][d] expert output gradients
+    float *hgrad = nullptr;  // [P][hp]
+    float *ggrad = nullptr, *ugrad = nullptr;  // [P][hp]
+    float *dxg = nullptr, *dxu = nullptr;      // [P][dp]
+    float *t = nullptr;      // [max(P, T)][R]
+    double *dx = nullptr;    // [T][d]
+    double *lg = nullptr;    // [T][E]
+    float *lgf = nullptr;    // [T][E]
+    float *dxr = nullptr;    // [T][dp]
+    int32_t *pgroup = nullptr;  // [P]
+    int4 *tiles_dot = nullptr, *tiles_tr = nullptr;  // [P + G]
+    int32_t *goff_router = nullptr;  // {0, T}
+    double *zero_bias = nullptr;     // [E]
+    int P = 0, ntiles_dot = 0, ntiles_tr = 0;
+};
+
 struct gtmoe_layer {
     gtmoe_context *ctx = nullptr;
     gtmoe_layer_desc desc{};
@@ -176,6 +213,12 @@ struct gtmoe_layer {
     // tables (load, rows_for_expert, offsets) are built only when read
     bool skipped_dispatch = false;  // by the forward being enqueued
     bool dispatch_pending = false;  // by the last forward
+    // low-rank adapters on every layer (Model.AddLowRankAdapters over
+    // MixtureOfExperts.Layers); the last forward's kept state for Backward
+    bool has_adapters = false;
+    AdapterSet ad_gate, ad_up, ad_down, ad_router;
+    TrainWorkspace tw;
+    int adapter_T = -1;  // tokens of the last forward through the adapter path, -1: none
 };
 
 namespace {
@@ -574,6 +617,7 @@ void mark_forward(gtmoe_layer *L, int T, int path, hipStream_t s)
     L->last_stream = s;
     L->load_on_host = false;
     L->dispatch_pending = T > 0 && L->skipped_dispatch;
+    L->adapter_T = -1;  // set again by the adapter path's forward
 }
 
 // Build the dispatch tables of the last forward if its kernels skipped them
@@ -687,6 +731,335 @@ int32_t capture(gtmoe_context *ctx, F &&record, gtmoe_graph *g)
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Low-rank adapters (perceptron/adapter.go) and the adapter path: a forward
+// that keeps what the backward needs, and MixtureOfExperts.Backward
+// (mixtureofexperts.go:227-285) over frozen base weights.
+// ---------------------------------------------------------------------------
+namespace {
+
+void free_adapter(AdapterSet &a)
+{
+    for (void *p : {(void *)a.A, (void *)a.B, (void *)a.scale, (void *)a.dA, (void *)a.dB})
+        if (p) (void)hipFree(p);
+    a = AdapterSet{};
+}
+
+void free_train_workspace(TrainWorkspace &tw)
+{
+    for (void *p : tw.blocks) (void)hipFree(p);
+    tw = TrainWorkspace{};
+}
+
+void free_adapters(gtmoe_layer *L)
+{
+    free_adapter(L->ad_gate);
+    free_adapter(L->ad_up);
+    free_adapter(L->ad_down);
+    free_adapter(L->ad_router);
+    free_train_workspace(L->tw);
+    L->has_adapters = false;
+    L->adapter_T = -1;
+}
+
+// Uniform in [-limit, limit) from a seeded splitmix64 stream (the device
+// cannot follow the reference's random source; callers that need its exact
+// values set them with gtmoe_layer_set_adapter).
+double seeded_uniform(uint64_t &state, double limit)
+{
+    uint64_t z = (state += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    const double u = (double)(z >> 11) * (1.0 / 9007199254740992.0);
+    return -limit + 2.0 * limit * u;
+}
+
+// AddLowRankAdapter (adapter.go:28-44) on every group of one role: rank
+// min(rank, inputs, outputs) as Model.AddLowRankAdapters picks it
+// (transformer/adapters.go:24-38), Down uniform in +-1/sqrt(inputs), Up zero.
+int32_t alloc_adapter(gtmoe_context *ctx, AdapterSet &a, int G, int width, int kin, int rows, int rank, double alpha,
+                      uint64_t &seed)
+{
+    a.G = G;
+    a.width = width;
+    a.kin = kin;
+    a.rows = rows;
+    a.R = std::min(rank, std::min(width, rows));
+    const size_t na = (size_t)G * a.R * kin, nb = (size_t)G * rows * a.R;
+    HIP_TRY(ctx, hipMalloc(&a.A, na * sizeof(float)));
+    HIP_TRY(ctx, hipMalloc(&a.B, nb * sizeof(float)));
+    HIP_TRY(ctx, hipMalloc(&a.scale, G * sizeof(float)));
+    HIP_TRY(ctx, hipMalloc(&a.dA, na * sizeof(double)));
+    HIP_TRY(ctx, hipMalloc(&a.dB, nb * sizeof(double)));
+    std::vector<float> A(na, 0.f);
+    const double limit = 1.0 / std::sqrt((double)width);
+    for (int g = 0; g < G; ++g)
+        for (int j = 0; j < a.R; ++j)
+            for (int i = 0; i < width; ++i)
+                A[((size_t)g * a.R + j) * kin + i] = (float)seeded_uniform(seed, limit);
+    const std::vector<float> sc(G, (float)(alpha / a.R));
+    HIP_TRY(ctx, hipMemcpy(a.A, A.data(), na * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(ctx, hipMemset(a.B, 0, nb * sizeof(float)));
+    HIP_TRY(ctx, hipMemcpy(a.scale, sc.data(), G * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(ctx, hipMemset(a.dA, 0, na * sizeof(double)));
+    HIP_TRY(ctx, hipMemset(a.dB, 0, nb * sizeof(double)));
+    return GTMOE_OK;
+}
+
+// The adapter of (role, index) and its group, or null with an error.
+AdapterSet *adapter_of(gtmoe_layer *L, int role, int index, int *group)
+{
+    gtmoe_context *ctx = L->ctx;
+    if (!L->has_adapters) {
+        fail(ctx, GTMOE_ERR_NOT_READY, "the layer has no low-rank adapters");
+        return nullptr;
+    }
+    if (role == GTMOE_ROLE_ROUTER) {
+        if (index != 0) {
+            fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "the router is index 0, got %d", index);
+            return nullptr;
+        }
+        *group = 0;
+        return &L->ad_router;
+    }
+    const bool shared = role >= GTMOE_ROLE_SHARED_GATE && role <= GTMOE_ROLE_SHARED_DOWN;
+    const bool routed = role >= GTMOE_ROLE_ROUTED_GATE && role <= GTMOE_ROLE_ROUTED_DOWN;
+    if (!shared && !routed) {
+        fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown role %d", role);
+        return nullptr;
+    }
+    const int n = shared ? L->S : L->E;
+    if (index < 0 || index >= n) {
+        fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "%s expert %d of %d", shared ? "shared" : "routed", index, n);
+        return nullptr;
+    }
+    *group = shared ? index : L->S + index;
+    const int which = shared ? role - GTMOE_ROLE_SHARED_GATE : role - GTMOE_ROLE_ROUTED_GATE;
+    return which == 0 ? &L->ad_gate : which == 1 ? &L->ad_up : &L->ad_down;
+}
+
+int32_t ensure_train_workspace(gtmoe_layer *L, int T)
+{
+    TrainWorkspace &tw = L->tw;
+    if (tw.cap >= T && tw.cap > 0) return GTMOE_OK;
+    gtmoe_context *ctx = L->ctx;
+    free_train_workspace(tw);
+    const int cap = std::max(T, 1);
+    const size_t P = (size_t)cap * (L->S + L->k);
+    const size_t R = std::max({L->ad_gate.R, L->ad_up.R, L->ad_down.R, L->ad_router.R, 1});
+    auto get = [&](auto *&ptr, size_t count) -> int32_t {
+        void *p = nullptr;
+        HIP_TRY(ctx, hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(*ptr)));
+        tw.blocks.push_back(p);
+        ptr = static_cast<std::remove_reference_t<decltype(ptr)>>(p);
+        return GTMOE_OK;
+    };
+    int32_t rc = GTMOE_OK;
+    const size_t hp = L->hp, dp = L->dp, d = L->d, E = L->E;
+    for (auto step : std::initializer_list<std::function<int32_t()>>{
+             [&] { return get(tw.gpre, P * hp); }, [&] { return get(tw.upre, P * hp); },
+             [&] { return get(tw.u_gate, P * R); }, [&] { return get(tw.u_up, P * R); },
+             [&] { return get(tw.u_down, P * R); }, [&] { return get(tw.u_router, (size_t)cap * R); },
+             [&] { return get(tw.og, (size_t)cap * d); }, [&] { return get(tw.eg, P * d); },
+             [&] { return get(tw.hgrad, P * hp); }, [&] { return get(tw.ggrad, P * hp); },
+             [&] { return get(tw.ugrad, P * hp); }, [&] { return get(tw.dxg, P * dp); },
+             [&] { return get(tw.dxu, P * dp); }, [&] { return get(tw.t, std::max(P, (size_t)cap) * R); },
+             [&] { return get(tw.dx, (size_t)cap * d); }, [&] { return get(tw.lg, (size_t)cap * E); },
+             [&] { return get(tw.lgf, (size_t)cap * E); }, [&] { return get(tw.dxr, (size_t)cap * dp); },
+             [&] { return get(tw.pgroup, P); }, [&] { return get(tw.tiles_dot, P + L->G); },
+             [&] { return get(tw.tiles_tr, P + L->G); }, [&] { return get(tw.goff_router, (size_t)2); },
+             [&] { return get(tw.zero_bias, E); }}) {
+        rc = step();
+        if (rc != GTMOE_OK) {
+            free_train_workspace(tw);
+            return rc;
+        }
+    }
+    HIP_TRY(ctx, hipMemset(tw.zero_bias, 0, E * sizeof(double)));
+    HIP_TRY(ctx, hipDeviceSynchronize());  // the memset runs on the null stream
+    tw.cap = cap;
+    return GTMOE_OK;
+}
+
+LoraArgs lora_args(const AdapterSet &a, int P, const int32_t *pgroup, const int32_t *goff)
+{
+    LoraArgs l{};
+    l.A = a.A;
+    l.B = a.B;
+    l.scale = a.scale;
+    l.R = a.R;
+    l.kin = a.kin;
+    l.width = a.width;
+    l.rows = a.rows;
+    l.G = a.G;
+    l.P = P;
+    l.pgroup = pgroup;
+    l.goff = goff;
+    return l;
+}
+
+RowsArgs rows_args(const DeviceMatrix &m, const float *in, int ld_in, const int32_t *in_tok, float *out, int ld_out,
+                   const int4 *tiles)
+{
+    RowsArgs r{};
+    r.values = m.values;
+    r.scales = m.scales;
+    r.w_group_stride = (long long)m.group_value_bytes();
+    r.s_group_stride = (long long)m.group_scales();
+    r.rows = m.rows;
+    r.rows_p = m.rows_p;
+    r.kp = m.kp;
+    r.row_bytes = m.row_bytes;
+    r.nblocks = m.nblocks;
+    r.in = in;
+    r.ld_in = ld_in;
+    r.in_tok = in_tok;
+    r.out = out;
+    r.ld_out = ld_out;
+    r.tiles = tiles;
+    return r;
+}
+
+// Forward through the adapter path (host float64 in and out).  Each layer:
+// pre = (x W^T + s (x A^T) B^T) + b in fp32, kept with x A^T for Backward.
+int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64_t *token_ids, double *outputs)
+{
+    gtmoe_context *ctx = L->ctx;
+    Workspace &w = L->ws;
+    hipStream_t s = ctx->stream;
+    int32_t rc = ensure_train_workspace(L, T);
+    if (rc != GTMOE_OK) return rc;
+    TrainWorkspace &tw = L->tw;
+    const int d = L->d, dp = L->dp, hp = L->hp, E = L->E, S = L->S, k = L->k, G = L->G;
+    const bool hash = L->desc.use_hash_routing != 0;
+    HIP_TRY(ctx, hipMemcpyAsync(w.x64, inputs, sizeof(double) * T * d, hipMemcpyHostToDevice, s));
+    if (hash) HIP_TRY(ctx, hipMemcpyAsync(w.ids, token_ids, sizeof(int64_t) * T, hipMemcpyHostToDevice, s));
+    RUN(ctx, s, "convert_inputs", launch_convert_inputs_f64(w.x64, T, d, w.xf, dp, nullptr, dp, s));
+    if (hash) {
+        RUN(ctx, s, "hash_route", launch_hash_route(w.ids, T, E, k, w.chosen, w.gates, w.gates32, s));
+    } else {
+        const int32_t goff_r[2] = {0, T};
+        HIP_TRY(ctx, hipMemcpyAsync(tw.goff_router, goff_r, sizeof goff_r, hipMemcpyHostToDevice, s));
+        RUN(ctx, s, "router", launch_router(w.xf, dp, T, d, L->router_w, dp, tw.zero_bias, E, w.logits, s));
+        const LoraArgs ar = lora_args(L->ad_router, T, nullptr, tw.goff_router);
+        RUN(ctx, s, "lora_down", launch_lora_down(ar, w.xf, dp, nullptr, tw.u_router, s));
+        RUN(ctx, s, "lora_up_bias", launch_lora_up_bias_f64(ar, tw.u_router, w.logits, E, L->router_b, s));
+        RUN(ctx, s, "topk", launch_topk(w.logits, T, E, k, L->balance, w.chosen, w.gates, w.gates32, s));
+    }
+    L->skipped_dispatch = false;
+    RUN(ctx, s, "dispatch",
+        launch_dispatch(w.chosen, T, k, E, S, kGemvSlice, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
+                        w.tile_off, w.tile_desc, w.chunk_cnt, s));
+    // positions of every group, and work tiles over them
+    std::vector<int32_t> goff(G + 1);
+    HIP_TRY(ctx, hipMemcpyAsync(goff.data(), w.goff, sizeof(int32_t) * (G + 1), hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    const int P = goff[G];
+    if (P != T * (S + k)) return fail(ctx, GTMOE_ERR_DEVICE, "dispatch placed %d positions, expected %d", P, T * (S + k));
+    std::vector<int32_t> pgroup(P);
+    std::vector<int4> tdot, ttr;
+    const int bd = rows_dot_tile(), bt = rows_transposed_tile();
+    for (int g = 0; g < G; ++g) {
+        for (int p = goff[g]; p < goff[g + 1]; ++p) pgroup[p] = g;
+        for (int p = goff[g]; p < goff[g + 1]; p += bd) tdot.push_back(make_int4(g, p, std::min(bd, goff[g + 1] - p), 0));
+        for (int p = goff[g]; p < goff[g + 1]; p += bt) ttr.push_back(make_int4(g, p, std::min(bt, goff[g + 1] - p), 0));
+    }
+    HIP_TRY(ctx, hipMemcpyAsync(tw.pgroup, pgroup.data(), sizeof(int32_t) * P, hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_dot, tdot.data(), sizeof(int4) * tdot.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_tr, ttr.data(), sizeof(int4) * ttr.size(), hipMemcpyHostToDevice, s));
+    tw.P = P;
+    tw.ntiles_dot = (int)tdot.size();
+    tw.ntiles_tr = (int)ttr.size();
+
+    const float limit = (float)L->desc.clamp_limit;
+    struct Role {
+        const DeviceMatrix &m;
+        const AdapterSet &a;
+        float *pre, *u;
+    };
+    for (const Role &r : {Role{L->gate, L->ad_gate, tw.gpre, tw.u_gate}, Role{L->up, L->ad_up, tw.upre, tw.u_up}}) {
+        RUN(ctx, s, "rows_dot",
+            launch_rows_dot(rows_args(r.m, w.xf, dp, w.tok, r.pre, hp, tw.tiles_dot), r.m.precision, tw.ntiles_dot, s));
+        const LoraArgs la = lora_args(r.a, P, tw.pgroup, w.goff);
+        RUN(ctx, s, "lora_down", launch_lora_down(la, w.xf, dp, w.tok, r.u, s));
+        RUN(ctx, s, "lora_up_bias", launch_lora_up_bias(la, r.u, r.pre, hp, r.m.biases, s));
+    }
+    RUN(ctx, s, "swiglu", launch_swiglu_forward(tw.gpre, tw.upre, P, L->h, hp, limit, w.hidden32, s));
+    RUN(ctx, s, "rows_dot",
+        launch_rows_dot(rows_args(L->down, w.hidden32, hp, nullptr, w.slot_out, d, tw.tiles_dot), L->down.precision,
+                        tw.ntiles_dot, s));
+    const LoraArgs ld = lora_args(L->ad_down, P, tw.pgroup, w.goff);
+    RUN(ctx, s, "lora_down", launch_lora_down(ld, w.hidden32, hp, nullptr, tw.u_down, s));
+    RUN(ctx, s, "lora_up_bias", launch_lora_up_bias(ld, tw.u_down, w.slot_out, d, L->down.biases, s));
+    RUN(ctx, s, "combine",
+        launch_combine(T, d, S, k, w.slot_out, false, w.pos, w.gates32, nullptr, nullptr, w.y64, s));
+    HIP_TRY(ctx, hipMemcpyAsync(outputs, w.y64, sizeof(double) * T * d, hipMemcpyDeviceToHost, s));
+    L->last_load.assign(E, 0);
+    HIP_TRY(ctx, hipMemcpyAsync(L->last_load.data(), w.load, sizeof(int32_t) * E, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    mark_forward(L, T, GTMOE_PATH_FP32, s);
+    L->load_on_host = true;
+    L->relaunch_ready = false;
+    L->adapter_T = T;
+    return GTMOE_OK;
+}
+
+// MixtureOfExperts.Backward (mixtureofexperts.go:227-285) after an adapter
+// path forward of T tokens: adapter gradients are added to dA / dB, the
+// input gradients returned (host float64).
+int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, double *input_grads)
+{
+    gtmoe_context *ctx = L->ctx;
+    Workspace &w = L->ws;
+    TrainWorkspace &tw = L->tw;
+    hipStream_t s = ctx->stream;
+    const int d = L->d, dp = L->dp, hp = L->hp, E = L->E, S = L->S, k = L->k, P = tw.P;
+    const float limit = (float)L->desc.clamp_limit;
+    HIP_TRY(ctx, hipMemcpyAsync(tw.og, output_grads, sizeof(double) * T * d, hipMemcpyHostToDevice, s));
+    // down layer: its pre-activation gradient is the expert output gradient
+    RUN(ctx, s, "expert_output_grad",
+        launch_expert_output_grad(tw.og, d, d, w.tok, tw.pgroup, S, T, k, w.chosen, w.gates, P, tw.eg, s));
+    RUN(ctx, s, "rows_transposed",
+        launch_rows_transposed(rows_args(L->down, tw.eg, d, nullptr, tw.hgrad, hp, tw.tiles_tr), L->down.precision,
+                               tw.ntiles_tr, s));
+    RUN(ctx, s, "lora_backward",
+        launch_lora_backward(lora_args(L->ad_down, P, tw.pgroup, w.goff), tw.eg, d, tw.u_down, w.hidden32, hp,
+                             nullptr, tw.t, tw.hgrad, hp, L->ad_down.dA, L->ad_down.dB, s));
+    RUN(ctx, s, "swiglu_backward",
+        launch_swiglu_backward(tw.hgrad, tw.gpre, tw.upre, P, L->h, hp, limit, tw.ggrad, tw.ugrad, s));
+    struct Role {
+        const DeviceMatrix &m;
+        AdapterSet &a;
+        float *grad, *u, *dx;
+    };
+    for (const Role &r : {Role{L->gate, L->ad_gate, tw.ggrad, tw.u_gate, tw.dxg},
+                          Role{L->up, L->ad_up, tw.ugrad, tw.u_up, tw.dxu}}) {
+        RUN(ctx, s, "rows_transposed",
+            launch_rows_transposed(rows_args(r.m, r.grad, hp, nullptr, r.dx, dp, tw.tiles_tr), r.m.precision,
+                                   tw.ntiles_tr, s));
+        RUN(ctx, s, "lora_backward",
+            launch_lora_backward(lora_args(r.a, P, tw.pgroup, w.goff), r.grad, hp, r.u, w.xf, dp, w.tok, tw.t, r.dx,
+                                 dp, r.a.dA, r.a.dB, s));
+    }
+    RUN(ctx, s, "gather_input_grad", launch_gather_input_grad(tw.dxg, tw.dxu, dp, d, T, S, k, w.pos, tw.dx, s));
+    if (!L->desc.use_hash_routing) {
+        RUN(ctx, s, "router_backward",
+            launch_router_backward(tw.og, d, w.slot_out, d, w.chosen, w.gates, w.logits, w.pos, S, T, E, k, tw.lg,
+                                   tw.lgf, s));
+        RUN(ctx, s, "router_input_grad", launch_router_input_grad(tw.lgf, T, E, L->router_w, dp, d, tw.dxr, dp, s));
+        RUN(ctx, s, "lora_backward",
+            launch_lora_backward(lora_args(L->ad_router, T, nullptr, tw.goff_router), tw.lgf, E, tw.u_router, w.xf,
+                                 dp, nullptr, tw.t, tw.dxr, dp, L->ad_router.dA, L->ad_router.dB, s));
+        RUN(ctx, s, "add_rows", launch_add_rows_f64(tw.dxr, dp, d, T, tw.dx, s));
+    }
+    HIP_TRY(ctx, hipMemcpyAsync(input_grads, tw.dx, sizeof(double) * T * d, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return GTMOE_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int32_t gtmoe_abi_version(void) { return GTMOE_ABI_VERSION; }
@@ -824,6 +1197,7 @@ int32_t gtmoe_layer_destroy(gtmoe_layer *L)
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
+    free_adapters(L);
     free_matrix(L->gate);
     free_matrix(L->up);
     free_matrix(L->down);
@@ -961,8 +1335,10 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
         mark_forward(L, 0, path, s);
         L->last_load.assign(L->E, 0);
         L->load_on_host = true;
+        if (L->has_adapters) L->adapter_T = 0;
         return GTMOE_OK;
     }
+    if (L->has_adapters) return adapter_forward(L, T, inputs, token_ids, outputs);
     Workspace &w = L->ws;
     HIP_TRY(ctx, hipMemcpyAsync(w.x64, inputs, sizeof(double) * T * L->d, hipMemcpyHostToDevice, s));
     if (L->desc.use_hash_routing)
@@ -997,6 +1373,8 @@ static int32_t check_forward_device(gtmoe_layer *L, int32_t T, const float *inpu
     if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
     if (L->desc.use_hash_routing && T > 0 && !token_ids)
         return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: hash routing needs one token ID per row");
+    if (L->has_adapters)
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED, "a layer with low-rank adapters runs through gtmoe_forward");
     *path = choose_path(L, T, flags);
     if (*path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
         return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
@@ -1141,6 +1519,9 @@ static int32_t stack_common(gtmoe_layer *const *layers, int32_t n_layers, int32_
         int32_t rc = check_layer_call(layers[l]);
         if (rc != GTMOE_OK) return rc;
         if (!layers[l]->has_norm) return fail(ctx, GTMOE_ERR_NOT_READY, "stack layer %d has no norm weights", l);
+        if (layers[l]->has_adapters)
+            return fail(ctx, GTMOE_ERR_UNSUPPORTED, "stack layer %d has low-rank adapters; it runs through gtmoe_forward",
+                        l);
     }
     *ctx_out = ctx;
     return GTMOE_OK;
@@ -1550,6 +1931,171 @@ int32_t gtmoe_layer_load_weights(gtmoe_layer *L, gtmoe_weights_file *f, const ch
         if (rc != GTMOE_OK) return rc;
     }
     return GTMOE_OK;
+}
+
+
+int32_t gtmoe_layer_add_adapters(gtmoe_layer *L, int32_t rank, double alpha, uint64_t seed)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (rank < 1)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "Model.AddLowRankAdapters: rank must be at least 1, got %d", rank);
+    if (L->has_adapters)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                    "Model.AddLowRankAdapters: the model already has adapters, merge or remove them first");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    uint64_t state = seed;
+    int32_t rc = alloc_adapter(ctx, L->ad_gate, L->G, L->d, L->dp, L->h, rank, alpha, state);
+    if (rc == GTMOE_OK) rc = alloc_adapter(ctx, L->ad_up, L->G, L->d, L->dp, L->h, rank, alpha, state);
+    if (rc == GTMOE_OK) rc = alloc_adapter(ctx, L->ad_down, L->G, L->h, L->hp, L->d, rank, alpha, state);
+    if (rc == GTMOE_OK) rc = alloc_adapter(ctx, L->ad_router, 1, L->d, L->dp, L->E, rank, alpha, state);
+    if (rc != GTMOE_OK) {
+        free_adapters(L);
+        return rc;
+    }
+    HIP_TRY(ctx, hipDeviceSynchronize());  // the memsets run on the null stream
+    free_train_workspace(L->tw);
+    L->has_adapters = true;
+    L->adapter_T = -1;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_remove_adapters(gtmoe_layer *L)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    free_adapters(L);
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_adapter_rank(gtmoe_layer *L, int32_t role, int32_t index, int32_t *rank)
+{
+    if (!L || !rank) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(L->ctx->mu);
+    int g = 0;
+    const AdapterSet *a = adapter_of(L, role, index, &g);
+    if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
+    *rank = a->R;
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_set_adapter(gtmoe_layer *L, int32_t role, int32_t index, const double *down, const double *up)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int g = 0;
+    AdapterSet *a = adapter_of(L, role, index, &g);
+    if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (down) {
+        std::vector<float> A((size_t)a->R * a->kin, 0.f);
+        for (int j = 0; j < a->R; ++j)
+            for (int i = 0; i < a->width; ++i) A[(size_t)j * a->kin + i] = (float)down[(size_t)j * a->width + i];
+        HIP_TRY(ctx, hipMemcpy(a->A + (size_t)g * a->R * a->kin, A.data(), A.size() * sizeof(float),
+                               hipMemcpyHostToDevice));
+    }
+    if (up) {
+        std::vector<float> B((size_t)a->rows * a->R);
+        for (size_t i = 0; i < B.size(); ++i) B[i] = (float)up[i];
+        HIP_TRY(ctx, hipMemcpy(a->B + (size_t)g * a->rows * a->R, B.data(), B.size() * sizeof(float),
+                               hipMemcpyHostToDevice));
+    }
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_get_adapter(gtmoe_layer *L, int32_t role, int32_t index, double *down, double *up)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int g = 0;
+    AdapterSet *a = adapter_of(L, role, index, &g);
+    if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (down) {
+        std::vector<float> A((size_t)a->R * a->kin);
+        HIP_TRY(ctx, hipMemcpy(A.data(), a->A + (size_t)g * a->R * a->kin, A.size() * sizeof(float),
+                               hipMemcpyDeviceToHost));
+        for (int j = 0; j < a->R; ++j)
+            for (int i = 0; i < a->width; ++i) down[(size_t)j * a->width + i] = A[(size_t)j * a->kin + i];
+    }
+    if (up) {
+        std::vector<float> B((size_t)a->rows * a->R);
+        HIP_TRY(ctx, hipMemcpy(B.data(), a->B + (size_t)g * a->rows * a->R, B.size() * sizeof(float),
+                               hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < B.size(); ++i) up[i] = B[i];
+    }
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_adapter_gradients(gtmoe_layer *L, int32_t role, int32_t index, double *down_grad,
+                                      double *up_grad)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int g = 0;
+    AdapterSet *a = adapter_of(L, role, index, &g);
+    if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (down_grad) {
+        std::vector<double> A((size_t)a->R * a->kin);
+        HIP_TRY(ctx, hipMemcpy(A.data(), a->dA + (size_t)g * a->R * a->kin, A.size() * sizeof(double),
+                               hipMemcpyDeviceToHost));
+        for (int j = 0; j < a->R; ++j)
+            for (int i = 0; i < a->width; ++i) down_grad[(size_t)j * a->width + i] = A[(size_t)j * a->kin + i];
+    }
+    if (up_grad)
+        HIP_TRY(ctx, hipMemcpy(up_grad, a->dB + (size_t)g * a->rows * a->R, (size_t)a->rows * a->R * sizeof(double),
+                               hipMemcpyDeviceToHost));
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_layer_zero_adapter_gradients(gtmoe_layer *L)
+{
+    if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (!L->has_adapters) return fail(ctx, GTMOE_ERR_NOT_READY, "the layer has no low-rank adapters");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    for (AdapterSet *a : {&L->ad_gate, &L->ad_up, &L->ad_down, &L->ad_router}) {
+        HIP_TRY(ctx, hipMemset(a->dA, 0, (size_t)a->G * a->R * a->kin * sizeof(double)));
+        HIP_TRY(ctx, hipMemset(a->dB, 0, (size_t)a->G * a->rows * a->R * sizeof(double)));
+    }
+    HIP_TRY(ctx, hipDeviceSynchronize());  // the memsets run on the null stream
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_backward(gtmoe_layer *L, int32_t tokens, const double *output_gradients, double *input_gradients)
+{
+    int32_t rc = check_layer_call(L);
+    if (rc != GTMOE_OK) return rc;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    if (!L->has_adapters)
+        return fail(ctx, GTMOE_ERR_UNSUPPORTED,
+                    "mixture of experts: weights are compressed for running the model, call DecompressWeights before "
+                    "training, or add a low-rank adapter to train around them");
+    if (L->adapter_T < 0) return fail(ctx, GTMOE_ERR_NOT_READY, "mixture of experts: call Forward before Backward");
+    if (tokens != L->adapter_T)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                    "mixture of experts: output gradients are %dx%d but the last Forward produced %dx%d", tokens, L->d,
+                    L->adapter_T, L->d);
+    if (tokens == 0) return GTMOE_OK;
+    if (!output_gradients || !input_gradients)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "output or input gradients are null");
+    return adapter_backward(L, tokens, output_gradients, input_gradients);
 }
 
 }  // extern "C"

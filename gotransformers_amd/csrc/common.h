@@ -108,6 +108,32 @@ struct GemvArgs {
     int self_dispatch, shared_slices, list_off, E;
 };
 
+// One weight role of a group set for the adapter path's generic kernels
+// (rows_dot: out[p][r] = in[row(p)] . W[r]; rows_transposed: out[p] =
+// sum_r in[p][r] W[r]).  tiles: (group, first position, positions).
+struct RowsArgs {
+    const void *values;
+    const float *scales;
+    long long w_group_stride;  // bytes
+    long long s_group_stride;  // floats
+    int rows, rows_p, kp, row_bytes, nblocks;
+    const float *in;
+    int ld_in;
+    const int32_t *in_tok;  // input row of a position (rows_dot), or null: the position
+    float *out;
+    int ld_out;
+    const int4 *tiles;
+};
+
+// Low-rank adapters of one weight role over G groups (A [G][R][kin], B
+// [G][rows][R], scale [G]) applied to P positions (pgroup[p]: group of p, or
+// null: group 0; goff[G+1]: first position of every group).
+struct LoraArgs {
+    const float *A, *B, *scale;
+    int R, kin, width, rows, G, P;
+    const int32_t *pgroup, *goff;
+};
+
 // Tokens per work slice of the GEMV path (the dispatch's tile size there).
 constexpr int kGemvSlice = 8;
 // Up to this many tokens the fp32 path's expert kernels find their own
@@ -192,5 +218,38 @@ hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool
                           const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s);
 hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s);
 hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);
+
+// Adapter path (lora.hip, route.hip).
+hipError_t launch_rows_dot(const RowsArgs &a, int precision, int ntiles, hipStream_t s);
+hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, hipStream_t s);
+int rows_dot_tile();
+int rows_transposed_tile();
+hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
+                            hipStream_t s);
+hipError_t launch_lora_up_bias(const LoraArgs &a, const float *u, float *out, int ld_out, const float *bias,
+                               hipStream_t s);
+hipError_t launch_lora_up_bias_f64(const LoraArgs &a, const float *u, double *out, int ld_out, const double *bias,
+                                   hipStream_t s);
+hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, const float *u, const float *in,
+                                int ld_in, const int32_t *in_tok, float *t, float *dx, int ld_dx, double *dA,
+                                double *dB, hipStream_t s);
+hipError_t launch_swiglu_forward(const float *gpre, const float *upre, int P, int h, int hp, float limit,
+                                 float *hidden, hipStream_t s);
+hipError_t launch_swiglu_backward(const float *hgrad, const float *gpre, const float *upre, int P, int h, int hp,
+                                  float limit, float *ggrad, float *ugrad, hipStream_t s);
+hipError_t launch_expert_output_grad(const double *og, int d, int ld, const int32_t *tok, const int32_t *pgroup,
+                                     int S, int T, int k, const int32_t *chosen, const double *gates, int P,
+                                     float *eg, hipStream_t s);
+hipError_t launch_gather_input_grad(const float *dxg, const float *dxu, int ld, int d, int T, int S, int k,
+                                    const int32_t *pos, double *dx, hipStream_t s);
+hipError_t launch_router_input_grad(const float *lg, int T, int E, const float *w, int ldw, int d, float *dx,
+                                    int ld_dx, hipStream_t s);
+hipError_t launch_add_rows_f64(const float *src, int ld, int d, int T, double *dst, hipStream_t s);
+// Router logit gradients (mixtureofexperts.go:262-282): lg [T][E] float64
+// and fp32 copy, zero for the experts a token did not choose.
+hipError_t launch_router_backward(const double *og, int d, const float *expert_out, int ld_out,
+                                  const int32_t *chosen, const double *gates, const double *logits,
+                                  const int32_t *pos, int S, int T, int E, int k, double *lg, float *lgf,
+                                  hipStream_t s);
 
 }  // namespace gtmoe

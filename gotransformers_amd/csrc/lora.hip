@@ -1,0 +1,534 @@
+// Kernels of the adapter path: a forward that keeps what the backward needs,
+// and the backward of a mixture whose layers carry low-rank adapters over
+// frozen (compressed) weights.
+//
+//   Layer.Forward with an adapter (perceptron/layer.go:133-162,
+//   adapter.go:66-76):  pre = (x W^T + s (x A^T) B^T) + b,  s = alpha / rank
+//   Layer.Backward, base frozen (layer.go:164-210, adapter.go:78-99):
+//     dB += s g^T u      (u = x A^T, kept by the forward)
+//     t   = s g B
+//     dA += t^T x
+//     dx  = g W + t A    (g W row by row is Rows.AddScaledRowTo,
+//                         lowprecision/rows.go:285-324)
+//
+// Work is numbered by positions as in the expert kernels: P = T*(S+k), shared
+// expert s on positions [s*T, (s+1)*T), the routed (token, slot) pairs after
+// them in dispatch order; pgroup[p] is the group of position p, goff[G+1]
+// the first position of every group.  A position's input row is in_tok[p]
+// (gate/up: the token) or p itself (down: the hidden row) when in_tok is null.
+//
+// Adapter storage per weight role, all groups in one allocation, zero beyond
+// a layer's rank and beyond its widths (so the padding adds nothing):
+//   A [G][R][kin] fp32 (Down of the reference, rank x inputs)
+//   B [G][rows][R] fp32 (Up, outputs x rank)
+//   dA, dB as float64 accumulators of the same shapes (the reference's
+//   DownGradients / UpGradients), scale[G] fp32.
+// Everything runs in fp32 with the reference's operation order where it has
+// one (block sums of a row times the block scale, bias after the adapter).
+#include "common.h"
+
+namespace gtmoe {
+
+namespace {
+
+constexpr int kDotTile = 8;   // positions per workgroup of rows_dot_kernel
+constexpr int kDotK = 256;    // K values staged per step
+constexpr int kTrTile = 4;    // positions per workgroup of rows_transposed_kernel
+constexpr int kTrRows = 256;  // gradient rows staged per step
+
+__device__ __forceinline__ float fp4_value(uint32_t code)
+{
+    const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+    const float v = mag[code & 7];
+    return (code & 8) ? -v : v;
+}
+
+// The 16 values of block b (columns 16b .. 16b+15) of row r, without the
+// block scale (Int8, FP4) or as stored (Float32).
+template <int PREC>
+__device__ __forceinline__ void block_values(const char *codes, int r, int b, int row_bytes, float (&w)[16])
+{
+    if constexpr (PREC == kInt8) {
+        const uint4 q = *reinterpret_cast<const uint4 *>(codes + panel_unit_offset(r, b, row_bytes));
+        const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int v = 0; v < 16; ++v) w[v] = (float)(int8_t)(d[v >> 2] >> (8 * (v & 3)));
+    } else if constexpr (PREC == kFP4) {
+        const uint2 q = *reinterpret_cast<const uint2 *>(codes + panel_unit_offset(r, b >> 1, row_bytes) + 8 * (b & 1));
+        const uint32_t d[2] = {q.x, q.y};
+#pragma unroll
+        for (int v = 0; v < 16; ++v) w[v] = fp4_value(d[v >> 3] >> (4 * (v & 7)));
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float4 f = *reinterpret_cast<const float4 *>(codes + panel_unit_offset(r, 4 * b + u, row_bytes));
+            w[4 * u] = f.x;
+            w[4 * u + 1] = f.y;
+            w[4 * u + 2] = f.z;
+            w[4 * u + 3] = f.w;
+        }
+    }
+}
+
+// pre[p][r] = sum over blocks b of (sum_{i in b} x_i q_{r,i}) * scale_{r,b}
+// (Rows.DotRow, rows.go:207-257), no bias.  Workgroup: one wave, lane = row
+// r of panel blockIdx.x, the kDotTile positions of tile blockIdx.y.
+template <int PREC>
+__global__ __launch_bounds__(64) void rows_dot_kernel(RowsArgs a)
+{
+    __shared__ float xs[kDotTile][kDotK];
+    const int4 td = a.tiles[blockIdx.y];
+    const int g = td.x, p0 = td.y, m = td.z;
+    const int lane = threadIdx.x;
+    const int r = blockIdx.x * 64 + lane;
+    const char *codes = reinterpret_cast<const char *>(a.values) + (size_t)g * a.w_group_stride;
+    const float *sc = a.scales + (size_t)g * a.s_group_stride;
+    float acc[kDotTile];
+#pragma unroll
+    for (int q = 0; q < kDotTile; ++q) acc[q] = 0.f;
+    for (int k0 = 0; k0 < a.kp; k0 += kDotK) {
+        __syncthreads();
+        for (int idx = lane; idx < kDotTile * kDotK; idx += 64) {
+            const int q = idx / kDotK, c = idx - q * kDotK;
+            float v = 0.f;
+            if (q < m && k0 + c < a.kp) {
+                const int p = p0 + q;
+                const int row = a.in_tok ? a.in_tok[p] : p;
+                v = a.in[(size_t)row * a.ld_in + k0 + c];
+            }
+            xs[q][c] = v;
+        }
+        __syncthreads();
+        const int kn = min(kDotK, a.kp - k0);
+        for (int c = 0; c < kn; c += 16) {
+            const int b = (k0 + c) >> 4;
+            float w[16];
+            block_values<PREC>(codes, r, b, a.row_bytes, w);
+            const float s = PREC == kFloat32 ? 1.f : sc[panel_scale_index(r, b, a.nblocks)];
+#pragma unroll
+            for (int q = 0; q < kDotTile; ++q) {
+                float bs = 0.f;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) bs = fmaf(xs[q][c + v], w[v], bs);
+                acc[q] = PREC == kFloat32 ? acc[q] + bs : fmaf(bs, s, acc[q]);
+            }
+        }
+    }
+    if (r < a.rows)
+        for (int q = 0; q < m; ++q) a.out[(size_t)(p0 + q) * a.ld_out + r] = acc[q];
+}
+
+// out[p][i] = sum_r grad[p][r] * W[r][i] for the group's rows r: the
+// reference's Rows.AddScaledRowTo over every row with scale grad[p][r]
+// (target_i += (grad * blockScale) * value).  Lane = one block of 16 columns
+// (blockIdx.x * 64 + lane), the kTrTile positions of tile blockIdx.y; every
+// column of the padded width is written (zero past the matrix).
+template <int PREC>
+__global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a)
+{
+    __shared__ float gs[kTrTile][kTrRows];
+    const int4 td = a.tiles[blockIdx.y];
+    const int g = td.x, p0 = td.y, m = td.z;
+    const int lane = threadIdx.x;
+    const int b = blockIdx.x * 64 + lane;  // block of 16 columns
+    const bool live = b < a.nblocks;
+    const char *codes = reinterpret_cast<const char *>(a.values) + (size_t)g * a.w_group_stride;
+    const float *sc = a.scales + (size_t)g * a.s_group_stride;
+    float acc[kTrTile][16];
+#pragma unroll
+    for (int q = 0; q < kTrTile; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[q][v] = 0.f;
+    for (int n0 = 0; n0 < a.rows; n0 += kTrRows) {
+        __syncthreads();
+        for (int idx = lane; idx < kTrTile * kTrRows; idx += 64) {
+            const int q = idx / kTrRows, c = idx - q * kTrRows;
+            gs[q][c] = q < m && n0 + c < a.rows ? a.in[(size_t)(p0 + q) * a.ld_in + n0 + c] : 0.f;
+        }
+        __syncthreads();
+        if (!live) continue;
+        const int nn = min(kTrRows, a.rows - n0);
+        for (int c = 0; c < nn; ++c) {
+            const int r = n0 + c;
+            float w[16];
+            block_values<PREC>(codes, r, b, a.row_bytes, w);
+            const float s = PREC == kFloat32 ? 1.f : sc[panel_scale_index(r, b, a.nblocks)];
+#pragma unroll
+            for (int q = 0; q < kTrTile; ++q) {
+                const float cs = PREC == kFloat32 ? gs[q][c] : gs[q][c] * s;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[q][v] = fmaf(cs, w[v], acc[q][v]);
+            }
+        }
+    }
+    if (!live) return;
+    for (int q = 0; q < m; ++q) {
+        float4 *o = reinterpret_cast<float4 *>(a.out + (size_t)(p0 + q) * a.ld_out + 16 * b);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o[u] = make_float4(acc[q][4 * u], acc[q][4 * u + 1], acc[q][4 * u + 2], acc[q][4 * u + 3]);
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// u[p][j] = sum_i in[row(p)][i] * A[g(p)][j][i]; one wave per position.
+__global__ __launch_bounds__(256) void lora_down_kernel(LoraArgs a, const float *__restrict__ in, int ld_in,
+                                                        const int32_t *__restrict__ in_tok, float *__restrict__ u)
+{
+    const int lane = threadIdx.x & 63;
+    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (p >= a.P) return;  // wave-uniform
+    const int g = a.pgroup ? a.pgroup[p] : 0;
+    const int row = in_tok ? in_tok[p] : p;
+    const float *x = in + (size_t)row * ld_in;
+    const float *A = a.A + (size_t)g * a.R * a.kin;
+    for (int j = 0; j < a.R; ++j) {
+        float s = 0.f;
+        for (int i = lane; i < a.width; i += 64) s = fmaf(x[i], A[(size_t)j * a.kin + i], s);
+        s = wave_sum(s);
+        if (lane == 0) u[(size_t)p * a.R + j] = s;
+    }
+}
+
+// out[p][n] = (out[p][n] + scale[g] * sum_j B[g][n][j] u[p][j]) + bias[n]
+// for n < rows (the reference adds the adapter, then the bias).
+template <typename OutT>
+__global__ __launch_bounds__(256) void lora_up_bias_kernel(LoraArgs a, const float *__restrict__ u,
+                                                           OutT *__restrict__ out, int ld_out,
+                                                           const float *__restrict__ bias32,
+                                                           const double *__restrict__ bias64)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int p = blockIdx.y;
+    if (n >= a.rows) return;
+    const int g = a.pgroup ? a.pgroup[p] : 0;
+    const float *B = a.B + ((size_t)g * a.rows + n) * a.R;
+    const float *up = u + (size_t)p * a.R;
+    float s = 0.f;
+    for (int j = 0; j < a.R; ++j) s = fmaf(B[j], up[j], s);
+    OutT &o = out[(size_t)p * ld_out + n];
+    if constexpr (sizeof(OutT) == 8) {
+        o = (o + (double)(a.scale[g] * s)) + bias64[n];
+    } else {
+        o = (o + a.scale[g] * s) + bias32[(size_t)g * a.rows + n];
+    }
+}
+
+// dB[g][n][j] += scale[g] * sum_{p in g} grad[p][n] * u[p][j]
+__global__ __launch_bounds__(256) void lora_grad_up_kernel(LoraArgs a, const float *__restrict__ grad, int ld_g,
+                                                           const float *__restrict__ u, double *__restrict__ dB)
+{
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int g = blockIdx.y;
+    if (idx >= a.rows * a.R) return;
+    const int n = idx / a.R, j = idx - n * a.R;
+    float s = 0.f;
+    for (int p = a.goff[g]; p < a.goff[g + 1]; ++p) s = fmaf(grad[(size_t)p * ld_g + n], u[(size_t)p * a.R + j], s);
+    dB[(size_t)g * a.rows * a.R + idx] += (double)(a.scale[g] * s);
+}
+
+// t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one wave per position.
+__global__ __launch_bounds__(256) void lora_t_kernel(LoraArgs a, const float *__restrict__ grad, int ld_g,
+                                                     float *__restrict__ t)
+{
+    const int lane = threadIdx.x & 63;
+    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (p >= a.P) return;  // wave-uniform
+    const int g = a.pgroup ? a.pgroup[p] : 0;
+    const float *gr = grad + (size_t)p * ld_g;
+    const float *B = a.B + (size_t)g * a.rows * a.R;
+    for (int j = 0; j < a.R; ++j) {
+        float s = 0.f;
+        for (int n = lane; n < a.rows; n += 64) s = fmaf(gr[n], B[(size_t)n * a.R + j], s);
+        s = wave_sum(s);
+        if (lane == 0) t[(size_t)p * a.R + j] = a.scale[g] * s;
+    }
+}
+
+// dA[g][j][i] += sum_{p in g} t[p][j] * in[row(p)][i], i < width
+__global__ __launch_bounds__(256) void lora_grad_down_kernel(LoraArgs a, const float *__restrict__ t,
+                                                             const float *__restrict__ in, int ld_in,
+                                                             const int32_t *__restrict__ in_tok,
+                                                             double *__restrict__ dA)
+{
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int g = blockIdx.y;
+    if (idx >= a.R * a.width) return;
+    const int j = idx / a.width, i = idx - j * a.width;
+    float s = 0.f;
+    for (int p = a.goff[g]; p < a.goff[g + 1]; ++p) {
+        const int row = in_tok ? in_tok[p] : p;
+        s = fmaf(t[(size_t)p * a.R + j], in[(size_t)row * ld_in + i], s);
+    }
+    dA[((size_t)g * a.R + j) * a.kin + i] += (double)s;
+}
+
+// dx[p][i] += sum_j t[p][j] * A[g][j][i], i < width
+__global__ __launch_bounds__(256) void lora_dx_kernel(LoraArgs a, const float *__restrict__ t,
+                                                      float *__restrict__ dx, int ld_dx)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int p = blockIdx.y;
+    if (i >= a.width) return;
+    const int g = a.pgroup ? a.pgroup[p] : 0;
+    const float *A = a.A + (size_t)g * a.R * a.kin + i;
+    const float *tp = t + (size_t)p * a.R;
+    float s = 0.f;
+    for (int j = 0; j < a.R; ++j) s = fmaf(tp[j], A[(size_t)j * a.kin], s);
+    dx[(size_t)p * ld_dx + i] += s;
+}
+
+__device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// gate and up activations and their derivatives (activationfunction.go:
+// 102-115, moreactivationfunctions.go:207-244); limit > 0 selects the
+// clamped pair
+__device__ __forceinline__ float gate_act(float x, float limit)
+{
+    if (limit > 0.f && x > limit) x = limit;
+    return x * sigm(x);
+}
+__device__ __forceinline__ float gate_deriv(float x, float limit)
+{
+    if (limit > 0.f && x > limit) return 0.f;
+    const float s = sigm(x);
+    return s + x * s * (1.f - s);
+}
+__device__ __forceinline__ float up_act(float x, float limit)
+{
+    if (limit > 0.f) return x > limit ? limit : (x < -limit ? -limit : x);
+    return x;
+}
+__device__ __forceinline__ float up_deriv(float x, float limit)
+{
+    if (limit > 0.f && (x > limit || x < -limit)) return 0.f;
+    return 1.f;
+}
+
+// hidden = act_g(gate_pre) * act_u(up_pre) (gatedfeedforward.go:49-57); the
+// padding columns [h, hp) are zero
+__global__ __launch_bounds__(256) void swiglu_forward_kernel(const float *__restrict__ gpre,
+                                                             const float *__restrict__ upre, int h, int hp,
+                                                             float limit, float *__restrict__ hidden)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const size_t o = (size_t)blockIdx.y * hp + n;
+    if (n >= hp) return;
+    hidden[o] = n < h ? gate_act(gpre[o], limit) * up_act(upre[o], limit) : 0.f;
+}
+
+// gatedfeedforward.go:59-67 with Layer.Backward's activation step
+// (layer.go:175-182): gate_grad = hidden_grad * up_out * act_g'(gate_pre),
+// up_grad = hidden_grad * gate_out * act_u'(up_pre)
+__global__ __launch_bounds__(256) void swiglu_backward_kernel(const float *__restrict__ hgrad,
+                                                              const float *__restrict__ gpre,
+                                                              const float *__restrict__ upre, int h, int hp,
+                                                              float limit, float *__restrict__ ggrad,
+                                                              float *__restrict__ ugrad)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const size_t o = (size_t)blockIdx.y * hp + n;
+    if (n >= hp) return;
+    float gg = 0.f, ug = 0.f;
+    if (n < h) {
+        const float gp = gpre[o], upv = upre[o], hg = hgrad[o];
+        gg = hg * up_act(upv, limit) * gate_deriv(gp, limit);
+        ug = hg * gate_act(gp, limit) * up_deriv(upv, limit);
+    }
+    ggrad[o] = gg;
+    ugrad[o] = ug;
+}
+
+// Gradient of every position's expert output: the token's output gradient,
+// times the slot's gate for a routed position (mixtureofexperts.go:243-247).
+__global__ __launch_bounds__(256) void expert_output_grad_kernel(const double *__restrict__ og, int d, int ld,
+                                                                 const int32_t *__restrict__ tok,
+                                                                 const int32_t *__restrict__ pgroup, int S, int T,
+                                                                 int k, const int32_t *__restrict__ chosen,
+                                                                 const double *__restrict__ gates,
+                                                                 float *__restrict__ eg)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int p = blockIdx.y;
+    if (i >= ld) return;
+    const int t = tok[p], g = pgroup[p];
+    double w = 1.0;
+    if (g >= S)
+        for (int j = 0; j < k; ++j)
+            if (chosen[(size_t)t * k + j] == g - S) w = gates[(size_t)t * k + j];
+    eg[(size_t)p * ld + i] = i < d ? (float)(og[(size_t)t * d + i] * w) : 0.f;
+}
+
+// Input gradient of each token: the shared experts' rows, then its routed
+// slots in chosen order (mixtureofexperts.go:237-256), each row being the
+// gate layer's plus the up layer's input gradient.
+__global__ __launch_bounds__(256) void gather_input_grad_kernel(const float *__restrict__ dxg,
+                                                                const float *__restrict__ dxu, int ld, int d, int T,
+                                                                int S, int k, const int32_t *__restrict__ pos,
+                                                                double *__restrict__ dx)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y;
+    if (i >= d) return;
+    double acc = 0.0;
+    for (int s = 0; s < S; ++s) {
+        const size_t o = (size_t)(s * T + t) * ld + i;
+        acc += (double)(dxg[o] + dxu[o]);
+    }
+    for (int j = 0; j < k; ++j) {
+        const size_t o = (size_t)(S * T + pos[(size_t)t * k + j]) * ld + i;
+        acc += (double)(dxg[o] + dxu[o]);
+    }
+    dx[(size_t)t * d + i] = acc;
+}
+
+// dx[t][i] += sum_e lg[t][e] * W[e][i] (the router's base rows, fp32, row
+// stride ldw), i < d
+__global__ __launch_bounds__(256) void router_input_grad_kernel(const float *__restrict__ lg, int E,
+                                                                const float *__restrict__ w, int ldw, int d,
+                                                                float *__restrict__ dx, int ld_dx)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y;
+    if (i >= d) return;
+    float s = 0.f;
+    for (int e = 0; e < E; ++e) s = fmaf(lg[(size_t)t * E + e], w[(size_t)e * ldw + i], s);
+    dx[(size_t)t * ld_dx + i] = s;
+}
+
+__global__ __launch_bounds__(256) void add_rows_f64_kernel(const float *__restrict__ src, int ld, int d, int T,
+                                                           double *__restrict__ dst)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y;
+    if (i >= d || t >= T) return;
+    dst[(size_t)t * d + i] += (double)src[(size_t)t * ld + i];
+}
+
+inline dim3 cols_grid(int cols, int rows) { return dim3((cols + 255) / 256, rows); }
+
+}  // namespace
+
+hipError_t launch_rows_dot(const RowsArgs &a, int precision, int ntiles, hipStream_t s)
+{
+    if (ntiles <= 0) return hipSuccess;
+    const dim3 grid(a.rows_p / 64, ntiles);
+    switch (precision) {
+    case kInt8: hipLaunchKernelGGL(rows_dot_kernel<kInt8>, grid, dim3(64), 0, s, a); break;
+    case kFP4: hipLaunchKernelGGL(rows_dot_kernel<kFP4>, grid, dim3(64), 0, s, a); break;
+    case kFloat32: hipLaunchKernelGGL(rows_dot_kernel<kFloat32>, grid, dim3(64), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, hipStream_t s)
+{
+    if (ntiles <= 0) return hipSuccess;
+    const dim3 grid((a.nblocks + 63) / 64, ntiles);
+    switch (precision) {
+    case kInt8: hipLaunchKernelGGL(rows_transposed_kernel<kInt8>, grid, dim3(64), 0, s, a); break;
+    case kFP4: hipLaunchKernelGGL(rows_transposed_kernel<kFP4>, grid, dim3(64), 0, s, a); break;
+    case kFloat32: hipLaunchKernelGGL(rows_transposed_kernel<kFloat32>, grid, dim3(64), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+int rows_dot_tile() { return kDotTile; }
+int rows_transposed_tile() { return kTrTile; }
+
+hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
+                            hipStream_t s)
+{
+    if (a.P <= 0 || a.R <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lora_down_kernel, dim3((a.P + 3) / 4), dim3(256), 0, s, a, in, ld_in, in_tok, u);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_up_bias(const LoraArgs &a, const float *u, float *out, int ld_out, const float *bias,
+                               hipStream_t s)
+{
+    if (a.P <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lora_up_bias_kernel<float>, cols_grid(a.rows, a.P), dim3(256), 0, s, a, u, out, ld_out, bias,
+                       nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_up_bias_f64(const LoraArgs &a, const float *u, double *out, int ld_out, const double *bias,
+                                   hipStream_t s)
+{
+    if (a.P <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lora_up_bias_kernel<double>, cols_grid(a.rows, a.P), dim3(256), 0, s, a, u, out, ld_out,
+                       nullptr, bias);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, const float *u, const float *in,
+                                int ld_in, const int32_t *in_tok, float *t, float *dx, int ld_dx, double *dA,
+                                double *dB, hipStream_t s)
+{
+    if (a.P <= 0 || a.R <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lora_grad_up_kernel, cols_grid(a.rows * a.R, a.G), dim3(256), 0, s, a, grad, ld_g, u, dB);
+    hipLaunchKernelGGL(lora_t_kernel, dim3((a.P + 3) / 4), dim3(256), 0, s, a, grad, ld_g, t);
+    hipLaunchKernelGGL(lora_grad_down_kernel, cols_grid(a.R * a.width, a.G), dim3(256), 0, s, a, t, in, ld_in,
+                       in_tok, dA);
+    hipLaunchKernelGGL(lora_dx_kernel, cols_grid(a.width, a.P), dim3(256), 0, s, a, t, dx, ld_dx);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_forward(const float *gpre, const float *upre, int P, int h, int hp, float limit,
+                                 float *hidden, hipStream_t s)
+{
+    if (P <= 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_forward_kernel, cols_grid(hp, P), dim3(256), 0, s, gpre, upre, h, hp, limit, hidden);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_backward(const float *hgrad, const float *gpre, const float *upre, int P, int h, int hp,
+                                  float limit, float *ggrad, float *ugrad, hipStream_t s)
+{
+    if (P <= 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_backward_kernel, cols_grid(hp, P), dim3(256), 0, s, hgrad, gpre, upre, h, hp, limit,
+                       ggrad, ugrad);
+    return hipGetLastError();
+}
+
+hipError_t launch_expert_output_grad(const double *og, int d, int ld, const int32_t *tok, const int32_t *pgroup,
+                                     int S, int T, int k, const int32_t *chosen, const double *gates, int P,
+                                     float *eg, hipStream_t s)
+{
+    if (P <= 0) return hipSuccess;
+    hipLaunchKernelGGL(expert_output_grad_kernel, cols_grid(ld, P), dim3(256), 0, s, og, d, ld, tok, pgroup, S, T, k,
+                       chosen, gates, eg);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_input_grad(const float *dxg, const float *dxu, int ld, int d, int T, int S, int k,
+                                    const int32_t *pos, double *dx, hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_input_grad_kernel, cols_grid(d, T), dim3(256), 0, s, dxg, dxu, ld, d, T, S, k, pos, dx);
+    return hipGetLastError();
+}
+
+hipError_t launch_router_input_grad(const float *lg, int T, int E, const float *w, int ldw, int d, float *dx,
+                                    int ld_dx, hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(router_input_grad_kernel, cols_grid(d, T), dim3(256), 0, s, lg, E, w, ldw, d, dx, ld_dx);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rows_f64(const float *src, int ld, int d, int T, double *dst, hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(add_rows_f64_kernel, cols_grid(d, T), dim3(256), 0, s, src, ld, d, T, dst);
+    return hipGetLastError();
+}
+
+}  // namespace gtmoe

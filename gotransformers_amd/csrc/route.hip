@@ -940,4 +940,63 @@ hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, boo
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Router backward (mixtureofexperts.go:262-282): per token, the gradient of
+// each chosen gate is the output gradient dotted with that slot's expert
+// output; through the gate normalisation and the affinity, the router logit
+// of chosen expert e gets (gg_i - sum_j gg_j g_j) / sum_j a_j * sigmoid(l) /
+// (2 a).  One wave per token; the sums over slots run in slot order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void router_backward_kernel(const double *__restrict__ og, int d,
+                                                             const float *__restrict__ expert_out, int ld_out,
+                                                             const int32_t *__restrict__ chosen,
+                                                             const double *__restrict__ gates,
+                                                             const double *__restrict__ logits,
+                                                             const int32_t *__restrict__ pos, int S, int T, int E,
+                                                             int k, double *__restrict__ lg, float *__restrict__ lgf)
+{
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x;
+    for (int e = lane; e < E; e += 64) {
+        lg[(size_t)t * E + e] = 0.0;
+        lgf[(size_t)t * E + e] = 0.f;
+    }
+    double gg[kMaxK];
+    for (int i = 0; i < k && i < kMaxK; ++i) {
+        const float *row = expert_out + (size_t)(S * T + pos[(size_t)t * k + i]) * ld_out;
+        double s = 0.0;
+        for (int m = lane; m < d; m += 64) s += og[(size_t)t * d + m] * (double)row[m];
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        gg[i] = s;
+    }
+    __syncthreads();  // the zero fill above precedes lane 0's writes
+    if (lane != 0) return;
+    double wsum = 0.0, atot = 0.0;
+    for (int i = 0; i < k && i < kMaxK; ++i) {
+        wsum += gg[i] * gates[(size_t)t * k + i];
+        atot += affinity(logits[(size_t)t * E + chosen[(size_t)t * k + i]]);
+    }
+    for (int i = 0; i < k && i < kMaxK; ++i) {
+        const int e = chosen[(size_t)t * k + i];
+        const double l = logits[(size_t)t * E + e];
+        const double a = affinity(l);
+        const double sig = 1.0 / (1.0 + go_exp(-l));
+        const double v = (gg[i] - wsum) / atot * (sig / (2.0 * a));
+        lg[(size_t)t * E + e] = v;
+        lgf[(size_t)t * E + e] = (float)v;
+    }
+}
+
+hipError_t launch_router_backward(const double *og, int d, const float *expert_out, int ld_out,
+                                  const int32_t *chosen, const double *gates, const double *logits,
+                                  const int32_t *pos, int S, int T, int E, int k, double *lg, float *lgf,
+                                  hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    if (k > kMaxK) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(router_backward_kernel, dim3(T), dim3(64), 0, s, og, d, expert_out, ld_out, chosen, gates,
+                       logits, pos, S, T, E, k, lg, lgf);
+    return hipGetLastError();
+}
+
 }  // namespace gtmoe

@@ -307,6 +307,53 @@ int32_t gtmoe_weights_file_rows(gtmoe_weights_file *file, int32_t index, void *v
  * reference would switch the layer's precision). */
 int32_t gtmoe_layer_load_weights(gtmoe_layer *layer, gtmoe_weights_file *file, const char *name);
 
+/* ---------------------------------------------------------------------------
+ * Low-rank adapters and the backward (training around frozen compressed
+ * experts).
+ *
+ * A layer with adapters runs gtmoe_forward through the adapter path: every
+ * layer of the mixture (shared and routed experts' gate, up and down, and
+ * the router) computes pre = (x W^T + s (x Down^T) Up^T) + b with s =
+ * alpha / rank (perceptron/layer.go:133-162, perceptron/adapter.go:66-76),
+ * in fp32, and keeps what gtmoe_backward needs.  gtmoe_forward_device, the
+ * stack and graph entry points refuse such a layer.  Adapter dropout is not
+ * supported (rate 0).
+ * ------------------------------------------------------------------------- */
+
+/* Model.AddLowRankAdapters over MixtureOfExperts.Layers
+ * (transformer/adapters.go:24-38, mixtureofexperts.go:326-335): each layer
+ * gets Layer.AddLowRankAdapter (adapter.go:28-44) with rank min(rank, inputs,
+ * outputs): Down uniform in +-1/sqrt(inputs) from `seed` (not the
+ * reference's random source; set the values with gtmoe_layer_set_adapter to
+ * match a Go-side adapter), Up zero, gradients zero.  The router's adapter
+ * exists with hash routing too and then stays unused. */
+int32_t gtmoe_layer_add_adapters(gtmoe_layer *layer, int32_t rank, double alpha, uint64_t seed);
+/* Model.RemoveAdapters (adapters.go:40-46). */
+int32_t gtmoe_layer_remove_adapters(gtmoe_layer *layer);
+/* Rank of one layer's adapter (LowRankAdapter.Rank); role/index as in
+ * gtmoe_upload_rows. */
+int32_t gtmoe_layer_adapter_rank(gtmoe_layer *layer, int32_t role, int32_t index, int32_t *rank);
+/* Adapter.Down [rank][inputs] and Adapter.Up [outputs][rank], float64
+ * row-major; either may be null to leave it. */
+int32_t gtmoe_layer_set_adapter(gtmoe_layer *layer, int32_t role, int32_t index, const double *down,
+                                const double *up);
+int32_t gtmoe_layer_get_adapter(gtmoe_layer *layer, int32_t role, int32_t index, double *down, double *up);
+/* Adapter.DownGradients and Adapter.UpGradients (the sums every Backward
+ * adds to), same shapes as Down and Up. */
+int32_t gtmoe_layer_adapter_gradients(gtmoe_layer *layer, int32_t role, int32_t index, double *down_grad,
+                                      double *up_grad);
+/* parameter.ZeroGradients over the adapters. */
+int32_t gtmoe_layer_zero_adapter_gradients(gtmoe_layer *layer);
+/* MixtureOfExperts.Backward (mixtureofexperts.go:227-285) after a
+ * gtmoe_forward of the same `tokens` rows: output_gradients [tokens][d] in,
+ * input_gradients [tokens][d] out (float64); every adapter's gradients are
+ * added to.  Base weights are frozen (Layer.Backward with FreezeBase,
+ * layer.go:164-210): input gradients go through them with
+ * Rows.AddScaledRowTo (lowprecision/rows.go:285-324).  Without adapters it
+ * fails as the reference panics for compressed weights. */
+int32_t gtmoe_backward(gtmoe_layer *layer, int32_t tokens, const double *output_gradients,
+                       double *input_gradients);
+
 #ifdef __cplusplus
 }
 #endif
