@@ -47,6 +47,7 @@ struct TimingRecord {
 
 struct gtmoe_context {
     int device = 0;
+    int compute_units = 256;
     hipStream_t stream = nullptr;
     std::recursive_mutex mu;
     std::string error;
@@ -176,10 +177,12 @@ struct TrainWorkspace {
     float *lgf = nullptr;    // [T][E]
     float *dxr = nullptr;    // [T][dp]
     int32_t *pgroup = nullptr;  // [P]
-    int4 *tiles_dot = nullptr, *tiles_tr = nullptr;  // [P + G]
+    int4 *tiles_tr = nullptr;  // [P + G]
     int32_t *goff_router = nullptr;  // {0, T}
     double *zero_bias = nullptr;     // [E]
-    int P = 0, ntiles_dot = 0, ntiles_tr = 0;
+    float *partial = nullptr;        // [chunks][P][max(dp, hp)] row-chunk sums of the transposed product
+    int chunks = 1;                  // row chunks the partial buffer holds
+    int P = 0, ntiles_tr = 0;
 };
 
 struct gtmoe_layer {
@@ -857,6 +860,10 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
     };
     int32_t rc = GTMOE_OK;
     const size_t hp = L->hp, dp = L->dp, d = L->d, E = L->E;
+    // row chunks of the transposed product: enough workgroups at decode
+    // sizes, scratch bounded by 256 MB
+    const size_t per_chunk = P * std::max(hp, dp) * sizeof(float);
+    tw.chunks = (int)std::max<size_t>(1, std::min<size_t>(64, (256u << 20) / per_chunk));
     for (auto step : std::initializer_list<std::function<int32_t()>>{
              [&] { return get(tw.gpre, P * hp); }, [&] { return get(tw.upre, P * hp); },
              [&] { return get(tw.u_gate, P * R); }, [&] { return get(tw.u_up, P * R); },
@@ -867,9 +874,9 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
              [&] { return get(tw.dxu, P * dp); }, [&] { return get(tw.t, std::max(P, (size_t)cap) * R); },
              [&] { return get(tw.dx, (size_t)cap * d); }, [&] { return get(tw.lg, (size_t)cap * E); },
              [&] { return get(tw.lgf, (size_t)cap * E); }, [&] { return get(tw.dxr, (size_t)cap * dp); },
-             [&] { return get(tw.pgroup, P); }, [&] { return get(tw.tiles_dot, P + L->G); },
-             [&] { return get(tw.tiles_tr, P + L->G); }, [&] { return get(tw.goff_router, (size_t)2); },
-             [&] { return get(tw.zero_bias, E); }}) {
+             [&] { return get(tw.pgroup, P); }, [&] { return get(tw.tiles_tr, P + L->G); },
+             [&] { return get(tw.goff_router, (size_t)2); }, [&] { return get(tw.zero_bias, E); },
+             [&] { return get(tw.partial, (size_t)tw.chunks * P * std::max(hp, dp)); }}) {
         rc = step();
         if (rc != GTMOE_OK) {
             free_train_workspace(tw);
@@ -921,6 +928,17 @@ RowsArgs rows_args(const DeviceMatrix &m, const float *in, int ld_in, const int3
     return r;
 }
 
+// Row chunks for the transposed product over `rows` rows: enough one-wave
+// workgroups for about four waves per SIMD (one chunk when the tiles alone
+// do that).
+int transposed_chunks(const gtmoe_layer *L, int rows, int ntiles, int colblocks)
+{
+    const int busy = ntiles * colblocks;
+    int want = (16 * L->ctx->compute_units + busy - 1) / std::max(busy, 1);
+    want = std::min(want, (rows + rows_transposed_chunk_rows() - 1) / rows_transposed_chunk_rows());
+    return std::max(1, std::min(want, L->tw.chunks));
+}
+
 // Forward through the adapter path (host float64 in and out).  Each layer:
 // pre = (x W^T + s (x A^T) B^T) + b in fp32, kept with x A^T for Backward.
 int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64_t *token_ids, double *outputs)
@@ -958,20 +976,43 @@ int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64
     const int P = goff[G];
     if (P != T * (S + k)) return fail(ctx, GTMOE_ERR_DEVICE, "dispatch placed %d positions, expected %d", P, T * (S + k));
     std::vector<int32_t> pgroup(P);
-    std::vector<int4> tdot, ttr;
-    const int bd = rows_dot_tile(), bt = rows_transposed_tile();
+    std::vector<int4> ttr;
+    const int bt = rows_transposed_tile();
     for (int g = 0; g < G; ++g) {
         for (int p = goff[g]; p < goff[g + 1]; ++p) pgroup[p] = g;
-        for (int p = goff[g]; p < goff[g + 1]; p += bd) tdot.push_back(make_int4(g, p, std::min(bd, goff[g + 1] - p), 0));
         for (int p = goff[g]; p < goff[g + 1]; p += bt) ttr.push_back(make_int4(g, p, std::min(bt, goff[g + 1] - p), 0));
     }
     HIP_TRY(ctx, hipMemcpyAsync(tw.pgroup, pgroup.data(), sizeof(int32_t) * P, hipMemcpyHostToDevice, s));
-    HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_dot, tdot.data(), sizeof(int4) * tdot.size(), hipMemcpyHostToDevice, s));
     HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_tr, ttr.data(), sizeof(int4) * ttr.size(), hipMemcpyHostToDevice, s));
     tw.P = P;
-    tw.ntiles_dot = (int)tdot.size();
     tw.ntiles_tr = (int)ttr.size();
 
+    // the bare products x W^T by the decode GEMV kernels (raw mode, over the
+    // dispatch's slices), then the adapter terms and the biases
+    const int slices = S * ((T + kGemvSlice - 1) / kGemvSlice) + (T * k + kGemvSlice - 1) / kGemvSlice + E;
+    GemvArgs a{};
+    a.w0 = L->gate.values;
+    a.s0 = L->gate.scales;
+    a.b0 = L->gate.biases;
+    a.w1 = L->up.values;
+    a.s1 = L->up.scales;
+    a.b1 = L->up.biases;
+    a.w_group_stride = (long long)L->gate.group_value_bytes();
+    a.s_group_stride = (long long)L->gate.group_scales();
+    a.rows = L->h;
+    a.nblocks = L->gate.nblocks;
+    a.row_bytes = L->gate.row_bytes;
+    a.in = w.xf;
+    a.ld_in = dp;
+    a.in_rows = w.cap;
+    a.tok = w.tok;
+    a.count = w.tile_off + G;
+    a.desc = w.tile_desc;
+    a.out = tw.gpre;
+    a.ld_out = hp;
+    a.raw = 1;
+    a.raw_up = tw.upre;
+    RUN(ctx, s, "gemv_gateup", launch_gemv_gateup(a, L->gate.precision, slices, s));
     const float limit = (float)L->desc.clamp_limit;
     struct Role {
         const DeviceMatrix &m;
@@ -979,16 +1020,29 @@ int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64
         float *pre, *u;
     };
     for (const Role &r : {Role{L->gate, L->ad_gate, tw.gpre, tw.u_gate}, Role{L->up, L->ad_up, tw.upre, tw.u_up}}) {
-        RUN(ctx, s, "rows_dot",
-            launch_rows_dot(rows_args(r.m, w.xf, dp, w.tok, r.pre, hp, tw.tiles_dot), r.m.precision, tw.ntiles_dot, s));
         const LoraArgs la = lora_args(r.a, P, tw.pgroup, w.goff);
         RUN(ctx, s, "lora_down", launch_lora_down(la, w.xf, dp, w.tok, r.u, s));
         RUN(ctx, s, "lora_up_bias", launch_lora_up_bias(la, r.u, r.pre, hp, r.m.biases, s));
     }
     RUN(ctx, s, "swiglu", launch_swiglu_forward(tw.gpre, tw.upre, P, L->h, hp, limit, w.hidden32, s));
-    RUN(ctx, s, "rows_dot",
-        launch_rows_dot(rows_args(L->down, w.hidden32, hp, nullptr, w.slot_out, d, tw.tiles_dot), L->down.precision,
-                        tw.ntiles_dot, s));
+    GemvArgs b{};
+    b.w0 = L->down.values;
+    b.s0 = L->down.scales;
+    b.b0 = L->down.biases;
+    b.w_group_stride = (long long)L->down.group_value_bytes();
+    b.s_group_stride = (long long)L->down.group_scales();
+    b.rows = d;
+    b.nblocks = L->down.nblocks;
+    b.row_bytes = L->down.row_bytes;
+    b.in = w.hidden32;
+    b.ld_in = hp;
+    b.in_rows = (long long)w.cap * (S + k);
+    b.count = w.tile_off + G;
+    b.desc = w.tile_desc;
+    b.out = w.slot_out;
+    b.ld_out = d;
+    b.raw = 1;
+    RUN(ctx, s, "gemv_down", launch_gemv_down(b, L->down.precision, slices, s));
     const LoraArgs ld = lora_args(L->ad_down, P, tw.pgroup, w.goff);
     RUN(ctx, s, "lora_down", launch_lora_down(ld, w.hidden32, hp, nullptr, tw.u_down, s));
     RUN(ctx, s, "lora_up_bias", launch_lora_up_bias(ld, tw.u_down, w.slot_out, d, L->down.biases, s));
@@ -1020,9 +1074,13 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
     // down layer: its pre-activation gradient is the expert output gradient
     RUN(ctx, s, "expert_output_grad",
         launch_expert_output_grad(tw.og, d, d, w.tok, tw.pgroup, S, T, k, w.chosen, w.gates, P, tw.eg, s));
-    RUN(ctx, s, "rows_transposed",
-        launch_rows_transposed(rows_args(L->down, tw.eg, d, nullptr, tw.hgrad, hp, tw.tiles_tr), L->down.precision,
-                               tw.ntiles_tr, s));
+    auto transposed = [&](const DeviceMatrix &m, const float *in, int ld_in, float *out, int ld_out) {
+        RowsArgs r = rows_args(m, in, ld_in, nullptr, out, ld_out, tw.tiles_tr);
+        r.tiles_positions = P;
+        const int chunks = transposed_chunks(L, m.rows, tw.ntiles_tr, (m.nblocks + 63) / 64);
+        return launch_rows_transposed(r, m.precision, tw.ntiles_tr, chunks, tw.partial, s);
+    };
+    RUN(ctx, s, "rows_transposed", transposed(L->down, tw.eg, d, tw.hgrad, hp));
     RUN(ctx, s, "lora_backward",
         launch_lora_backward(lora_args(L->ad_down, P, tw.pgroup, w.goff), tw.eg, d, tw.u_down, w.hidden32, hp,
                              nullptr, tw.t, tw.hgrad, hp, L->ad_down.dA, L->ad_down.dB, s));
@@ -1035,9 +1093,7 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
     };
     for (const Role &r : {Role{L->gate, L->ad_gate, tw.ggrad, tw.u_gate, tw.dxg},
                           Role{L->up, L->ad_up, tw.ugrad, tw.u_up, tw.dxu}}) {
-        RUN(ctx, s, "rows_transposed",
-            launch_rows_transposed(rows_args(r.m, r.grad, hp, nullptr, r.dx, dp, tw.tiles_tr), r.m.precision,
-                                   tw.ntiles_tr, s));
+        RUN(ctx, s, "rows_transposed", transposed(r.m, r.grad, hp, r.dx, dp));
         RUN(ctx, s, "lora_backward",
             launch_lora_backward(lora_args(r.a, P, tw.pgroup, w.goff), r.grad, hp, r.u, w.xf, dp, w.tok, tw.t, r.dx,
                                  dp, r.a.dA, r.a.dB, s));
@@ -1090,6 +1146,7 @@ int32_t gtmoe_open(int32_t device, gtmoe_context **out)
     if (hipSetDevice(device) != hipSuccess) return fail(nullptr, GTMOE_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     gtmoe_context *ctx = new gtmoe_context;
     ctx->device = device;
+    if (prop.multiProcessorCount > 0) ctx->compute_units = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return fail(nullptr, GTMOE_ERR_DEVICE, "cannot create a stream");

@@ -106,11 +106,14 @@ struct GemvArgs {
     // routed entry t*k + j at S*T + t*k + j.  list_off: LDS offset of the
     // entry list (set by the launcher; room for T*k entries).
     int self_dispatch, shared_slices, list_off, E;
+    // raw: write the bare products, no bias or activation (gate to out, up to
+    // raw_up with the same layout); the adapter path's forward
+    int raw;
+    float *raw_up;
 };
 
-// One weight role of a group set for the adapter path's generic kernels
-// (rows_dot: out[p][r] = in[row(p)] . W[r]; rows_transposed: out[p] =
-// sum_r in[p][r] W[r]).  tiles: (group, first position, positions).
+// One weight role of a group set for the adapter path's transposed product
+// (out[p] = sum_r in[p][r] W[r]).  tiles: (group, first position, positions).
 struct RowsArgs {
     const void *values;
     const float *scales;
@@ -119,10 +122,11 @@ struct RowsArgs {
     int rows, rows_p, kp, row_bytes, nblocks;
     const float *in;
     int ld_in;
-    const int32_t *in_tok;  // input row of a position (rows_dot), or null: the position
+    const int32_t *in_tok;  // unused by the transposed product (its input row is the position)
     float *out;
     int ld_out;
     const int4 *tiles;
+    int tiles_positions;  // positions the tiles cover (rows of out)
 };
 
 // Low-rank adapters of one weight role over G groups (A [G][R][kin], B
@@ -220,10 +224,13 @@ hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s);
 hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);
 
 // Adapter path (lora.hip, route.hip).
-hipError_t launch_rows_dot(const RowsArgs &a, int precision, int ntiles, hipStream_t s);
-hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, hipStream_t s);
-int rows_dot_tile();
+// out = in W over `chunks` row chunks; partial: chunks * positions * ld_out
+// floats of scratch when chunks > 1
+hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int chunks, float *partial,
+                                  hipStream_t s);
 int rows_transposed_tile();
+// smallest row chunk worth a workgroup of its own
+int rows_transposed_chunk_rows();
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
                             hipStream_t s);
 hipError_t launch_lora_up_bias(const LoraArgs &a, const float *u, float *out, int ld_out, const float *bias,

@@ -469,8 +469,12 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
             for (int wv = 0; wv < NW; ++wv) s += red[slot(wv, m, q, wave)];
             v[m] = s;
         }
-        float *out = a.out + (size_t)slice_out_row<MODE>(a, sl, t) * a.ld_out + row;
-        if constexpr (GATEUP) {
+        const size_t orow = (size_t)slice_out_row<MODE>(a, sl, t) * a.ld_out;
+        float *out = a.out + orow + row;
+        if (a.raw) {  // the bare products (the adapter path adds its terms and the bias)
+            *out = v[0];
+            if constexpr (GATEUP) a.raw_up[orow + row] = v[MATS - 1];
+        } else if constexpr (GATEUP) {
             float gv = v[0] + bias[0];
             float uv = v[1] + bias[MATS - 1];
             if (a.clamp > 0.f) {

@@ -4,6 +4,7 @@
 //
 //   Layer.Forward with an adapter (perceptron/layer.go:133-162,
 //   adapter.go:66-76):  pre = (x W^T + s (x A^T) B^T) + b,  s = alpha / rank
+//   (x W^T comes from the decode GEMV kernels in their raw mode)
 //   Layer.Backward, base frozen (layer.go:164-210, adapter.go:78-99):
 //     dB += s g^T u      (u = x A^T, kept by the forward)
 //     t   = s g B
@@ -31,10 +32,8 @@ namespace gtmoe {
 
 namespace {
 
-constexpr int kDotTile = 8;   // positions per workgroup of rows_dot_kernel
-constexpr int kDotK = 256;    // K values staged per step
 constexpr int kTrTile = 4;    // positions per workgroup of rows_transposed_kernel
-constexpr int kTrRows = 256;  // gradient rows staged per step
+constexpr int kTrRows = 128;  // gradient rows staged per step
 
 __device__ __forceinline__ float fp4_value(uint32_t code)
 {
@@ -70,61 +69,17 @@ __device__ __forceinline__ void block_values(const char *codes, int r, int b, in
     }
 }
 
-// pre[p][r] = sum over blocks b of (sum_{i in b} x_i q_{r,i}) * scale_{r,b}
-// (Rows.DotRow, rows.go:207-257), no bias.  Workgroup: one wave, lane = row
-// r of panel blockIdx.x, the kDotTile positions of tile blockIdx.y.
-template <int PREC>
-__global__ __launch_bounds__(64) void rows_dot_kernel(RowsArgs a)
-{
-    __shared__ float xs[kDotTile][kDotK];
-    const int4 td = a.tiles[blockIdx.y];
-    const int g = td.x, p0 = td.y, m = td.z;
-    const int lane = threadIdx.x;
-    const int r = blockIdx.x * 64 + lane;
-    const char *codes = reinterpret_cast<const char *>(a.values) + (size_t)g * a.w_group_stride;
-    const float *sc = a.scales + (size_t)g * a.s_group_stride;
-    float acc[kDotTile];
-#pragma unroll
-    for (int q = 0; q < kDotTile; ++q) acc[q] = 0.f;
-    for (int k0 = 0; k0 < a.kp; k0 += kDotK) {
-        __syncthreads();
-        for (int idx = lane; idx < kDotTile * kDotK; idx += 64) {
-            const int q = idx / kDotK, c = idx - q * kDotK;
-            float v = 0.f;
-            if (q < m && k0 + c < a.kp) {
-                const int p = p0 + q;
-                const int row = a.in_tok ? a.in_tok[p] : p;
-                v = a.in[(size_t)row * a.ld_in + k0 + c];
-            }
-            xs[q][c] = v;
-        }
-        __syncthreads();
-        const int kn = min(kDotK, a.kp - k0);
-        for (int c = 0; c < kn; c += 16) {
-            const int b = (k0 + c) >> 4;
-            float w[16];
-            block_values<PREC>(codes, r, b, a.row_bytes, w);
-            const float s = PREC == kFloat32 ? 1.f : sc[panel_scale_index(r, b, a.nblocks)];
-#pragma unroll
-            for (int q = 0; q < kDotTile; ++q) {
-                float bs = 0.f;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) bs = fmaf(xs[q][c + v], w[v], bs);
-                acc[q] = PREC == kFloat32 ? acc[q] + bs : fmaf(bs, s, acc[q]);
-            }
-        }
-    }
-    if (r < a.rows)
-        for (int q = 0; q < m; ++q) a.out[(size_t)(p0 + q) * a.ld_out + r] = acc[q];
-}
-
 // out[p][i] = sum_r grad[p][r] * W[r][i] for the group's rows r: the
 // reference's Rows.AddScaledRowTo over every row with scale grad[p][r]
 // (target_i += (grad * blockScale) * value).  Lane = one block of 16 columns
-// (blockIdx.x * 64 + lane), the kTrTile positions of tile blockIdx.y; every
-// column of the padded width is written (zero past the matrix).
+// (blockIdx.x * 64 + lane), the kTrTile positions of tile blockIdx.y, rows
+// [blockIdx.z * chunk_rows, +chunk_rows); with more than one row chunk each
+// writes its partial sums to partial[blockIdx.z] (same layout as out) and
+// sum_chunks_kernel adds them in chunk order.  Every column of the padded
+// width is written (zero past the matrix).
 template <int PREC>
-__global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a)
+__global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a, int chunk_rows, float *__restrict__ partial,
+                                                             long long partial_stride)
 {
     __shared__ float gs[kTrTile][kTrRows];
     const int4 td = a.tiles[blockIdx.y];
@@ -139,15 +94,17 @@ __global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a)
     for (int q = 0; q < kTrTile; ++q)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[q][v] = 0.f;
-    for (int n0 = 0; n0 < a.rows; n0 += kTrRows) {
+    const int nbeg = blockIdx.z * chunk_rows, nend = min(a.rows, nbeg + chunk_rows);
+    for (int n0 = nbeg; n0 < nend; n0 += kTrRows) {
         __syncthreads();
         for (int idx = lane; idx < kTrTile * kTrRows; idx += 64) {
             const int q = idx / kTrRows, c = idx - q * kTrRows;
-            gs[q][c] = q < m && n0 + c < a.rows ? a.in[(size_t)(p0 + q) * a.ld_in + n0 + c] : 0.f;
+            gs[q][c] = q < m && n0 + c < nend ? a.in[(size_t)(p0 + q) * a.ld_in + n0 + c] : 0.f;
         }
         __syncthreads();
         if (!live) continue;
-        const int nn = min(kTrRows, a.rows - n0);
+        const int nn = min(kTrRows, nend - n0);
+#pragma unroll 4
         for (int c = 0; c < nn; ++c) {
             const int r = n0 + c;
             float w[16];
@@ -162,11 +119,24 @@ __global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a)
         }
     }
     if (!live) return;
+    float *dst = gridDim.z == 1 ? a.out : partial + (size_t)blockIdx.z * partial_stride;
     for (int q = 0; q < m; ++q) {
-        float4 *o = reinterpret_cast<float4 *>(a.out + (size_t)(p0 + q) * a.ld_out + 16 * b);
+        float4 *o = reinterpret_cast<float4 *>(dst + (size_t)(p0 + q) * a.ld_out + 16 * b);
 #pragma unroll
         for (int u = 0; u < 4; ++u) o[u] = make_float4(acc[q][4 * u], acc[q][4 * u + 1], acc[q][4 * u + 2], acc[q][4 * u + 3]);
     }
+}
+
+// out[p][i] = sum over chunks c (in order) of partial[c][p][i], i < cols
+__global__ __launch_bounds__(256) void sum_chunks_kernel(const float *__restrict__ partial, long long stride,
+                                                         int chunks, int cols, int ld, float *__restrict__ out)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const size_t o = (size_t)blockIdx.y * ld + i;
+    if (i >= cols) return;
+    float s = partial[o];
+    for (int c = 1; c < chunks; ++c) s += partial[(size_t)c * stride + o];
+    out[o] = s;
 }
 
 __device__ __forceinline__ float wave_sum(float v)
@@ -175,23 +145,32 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
-// u[p][j] = sum_i in[row(p)][i] * A[g(p)][j][i]; one wave per position.
+// u[p][j] = sum_i in[row(p)][i] * A[g(p)][j][i]; one wave per (position,
+// rank j).  Rows are read as float4 runs over the padded width kin (zeros
+// past the width in both operands); the loads are unconditional (clamped
+// index, masked sum) so the compiler keeps them all in flight.
 __global__ __launch_bounds__(256) void lora_down_kernel(LoraArgs a, const float *__restrict__ in, int ld_in,
                                                         const int32_t *__restrict__ in_tok, float *__restrict__ u)
 {
     const int lane = threadIdx.x & 63;
-    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (p >= a.P) return;  // wave-uniform
+    const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wv >= a.P * a.R) return;  // wave-uniform
+    const int p = wv / a.R, j = wv - p * a.R;
     const int g = a.pgroup ? a.pgroup[p] : 0;
     const int row = in_tok ? in_tok[p] : p;
-    const float *x = in + (size_t)row * ld_in;
-    const float *A = a.A + (size_t)g * a.R * a.kin;
-    for (int j = 0; j < a.R; ++j) {
-        float s = 0.f;
-        for (int i = lane; i < a.width; i += 64) s = fmaf(x[i], A[(size_t)j * a.kin + i], s);
-        s = wave_sum(s);
-        if (lane == 0) u[(size_t)p * a.R + j] = s;
+    const float4 *x = reinterpret_cast<const float4 *>(in + (size_t)row * ld_in);
+    const float4 *A = reinterpret_cast<const float4 *>(a.A + ((size_t)g * a.R + j) * a.kin);
+    const int n4 = a.kin / 4;
+    float s = 0.f;
+#pragma unroll 4
+    for (int i = lane; i < n4 + 63; i += 64) {
+        const int c = min(i, n4 - 1);
+        const float4 xv = x[c], av = A[c];
+        const float d = xv.x * av.x + xv.y * av.y + xv.z * av.z + xv.w * av.w;
+        s += i < n4 ? d : 0.f;
     }
+    s = wave_sum(s);
+    if (lane == 0) u[(size_t)p * a.R + j] = s;
 }
 
 // out[p][n] = (out[p][n] + scale[g] * sum_j B[g][n][j] u[p][j]) + bias[n]
@@ -227,26 +206,32 @@ __global__ __launch_bounds__(256) void lora_grad_up_kernel(LoraArgs a, const flo
     if (idx >= a.rows * a.R) return;
     const int n = idx / a.R, j = idx - n * a.R;
     float s = 0.f;
+#pragma unroll 8
     for (int p = a.goff[g]; p < a.goff[g + 1]; ++p) s = fmaf(grad[(size_t)p * ld_g + n], u[(size_t)p * a.R + j], s);
     dB[(size_t)g * a.rows * a.R + idx] += (double)(a.scale[g] * s);
 }
 
-// t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one wave per position.
+// t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one wave per
+// (position, rank j), unconditional loads as in lora_down_kernel.
 __global__ __launch_bounds__(256) void lora_t_kernel(LoraArgs a, const float *__restrict__ grad, int ld_g,
                                                      float *__restrict__ t)
 {
     const int lane = threadIdx.x & 63;
-    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (p >= a.P) return;  // wave-uniform
+    const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wv >= a.P * a.R) return;  // wave-uniform
+    const int p = wv / a.R, j = wv - p * a.R;
     const int g = a.pgroup ? a.pgroup[p] : 0;
     const float *gr = grad + (size_t)p * ld_g;
-    const float *B = a.B + (size_t)g * a.rows * a.R;
-    for (int j = 0; j < a.R; ++j) {
-        float s = 0.f;
-        for (int n = lane; n < a.rows; n += 64) s = fmaf(gr[n], B[(size_t)n * a.R + j], s);
-        s = wave_sum(s);
-        if (lane == 0) t[(size_t)p * a.R + j] = a.scale[g] * s;
+    const float *B = a.B + (size_t)g * a.rows * a.R + j;
+    float s = 0.f;
+#pragma unroll 8
+    for (int n = lane; n < a.rows + 63; n += 64) {
+        const int c = min(n, a.rows - 1);
+        const float d = gr[c] * B[(size_t)c * a.R];
+        s += n < a.rows ? d : 0.f;
     }
+    s = wave_sum(s);
+    if (lane == 0) t[(size_t)p * a.R + j] = a.scale[g] * s;
 }
 
 // dA[g][j][i] += sum_{p in g} t[p][j] * in[row(p)][i], i < width
@@ -260,6 +245,7 @@ __global__ __launch_bounds__(256) void lora_grad_down_kernel(LoraArgs a, const f
     if (idx >= a.R * a.width) return;
     const int j = idx / a.width, i = idx - j * a.width;
     float s = 0.f;
+#pragma unroll 8
     for (int p = a.goff[g]; p < a.goff[g + 1]; ++p) {
         const int row = in_tok ? in_tok[p] : p;
         s = fmaf(t[(size_t)p * a.R + j], in[(size_t)row * ld_in + i], s);
@@ -413,40 +399,37 @@ inline dim3 cols_grid(int cols, int rows) { return dim3((cols + 255) / 256, rows
 
 }  // namespace
 
-hipError_t launch_rows_dot(const RowsArgs &a, int precision, int ntiles, hipStream_t s)
+hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int chunks, float *partial,
+                                  hipStream_t s)
 {
     if (ntiles <= 0) return hipSuccess;
-    const dim3 grid(a.rows_p / 64, ntiles);
+    if (chunks < 1 || (chunks > 1 && !partial)) return hipErrorInvalidValue;
+    const int chunk_rows = (a.rows + chunks - 1) / chunks;
+    const long long stride = (long long)a.tiles_positions * a.ld_out;
+    const dim3 grid((a.nblocks + 63) / 64, ntiles, chunks);
     switch (precision) {
-    case kInt8: hipLaunchKernelGGL(rows_dot_kernel<kInt8>, grid, dim3(64), 0, s, a); break;
-    case kFP4: hipLaunchKernelGGL(rows_dot_kernel<kFP4>, grid, dim3(64), 0, s, a); break;
-    case kFloat32: hipLaunchKernelGGL(rows_dot_kernel<kFloat32>, grid, dim3(64), 0, s, a); break;
+    case kInt8: hipLaunchKernelGGL(rows_transposed_kernel<kInt8>, grid, dim3(64), 0, s, a, chunk_rows, partial, stride); break;
+    case kFP4: hipLaunchKernelGGL(rows_transposed_kernel<kFP4>, grid, dim3(64), 0, s, a, chunk_rows, partial, stride); break;
+    case kFloat32:
+        hipLaunchKernelGGL(rows_transposed_kernel<kFloat32>, grid, dim3(64), 0, s, a, chunk_rows, partial, stride);
+        break;
     default: return hipErrorInvalidValue;
     }
+    if (chunks > 1)
+        hipLaunchKernelGGL(sum_chunks_kernel, dim3((a.kp + 255) / 256, a.tiles_positions), dim3(256), 0, s, partial,
+                           stride, chunks, a.kp, a.ld_out, a.out);
     return hipGetLastError();
 }
 
-hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, hipStream_t s)
-{
-    if (ntiles <= 0) return hipSuccess;
-    const dim3 grid((a.nblocks + 63) / 64, ntiles);
-    switch (precision) {
-    case kInt8: hipLaunchKernelGGL(rows_transposed_kernel<kInt8>, grid, dim3(64), 0, s, a); break;
-    case kFP4: hipLaunchKernelGGL(rows_transposed_kernel<kFP4>, grid, dim3(64), 0, s, a); break;
-    case kFloat32: hipLaunchKernelGGL(rows_transposed_kernel<kFloat32>, grid, dim3(64), 0, s, a); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-int rows_dot_tile() { return kDotTile; }
 int rows_transposed_tile() { return kTrTile; }
+int rows_transposed_chunk_rows() { return 32; }
 
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
                             hipStream_t s)
 {
     if (a.P <= 0 || a.R <= 0) return hipSuccess;
-    hipLaunchKernelGGL(lora_down_kernel, dim3((a.P + 3) / 4), dim3(256), 0, s, a, in, ld_in, in_tok, u);
+    const int waves = a.P * a.R;
+    hipLaunchKernelGGL(lora_down_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, a, in, ld_in, in_tok, u);
     return hipGetLastError();
 }
 
@@ -474,7 +457,8 @@ hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, 
 {
     if (a.P <= 0 || a.R <= 0) return hipSuccess;
     hipLaunchKernelGGL(lora_grad_up_kernel, cols_grid(a.rows * a.R, a.G), dim3(256), 0, s, a, grad, ld_g, u, dB);
-    hipLaunchKernelGGL(lora_t_kernel, dim3((a.P + 3) / 4), dim3(256), 0, s, a, grad, ld_g, t);
+    const int waves = a.P * a.R;
+    hipLaunchKernelGGL(lora_t_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, a, grad, ld_g, t);
     hipLaunchKernelGGL(lora_grad_down_kernel, cols_grid(a.R * a.width, a.G), dim3(256), 0, s, a, t, in, ld_in,
                        in_tok, dA);
     hipLaunchKernelGGL(lora_dx_kernel, cols_grid(a.width, a.P), dim3(256), 0, s, a, t, dx, ld_dx);
