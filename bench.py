@@ -15,6 +15,9 @@ blocks RMSNorm + MoE + residual, d=2048, 64+1 experts, top-4, h=1024, FP4,
 T=64 / T=8192; four distinct seeded weight sets cycled over the 24 layers,
 every layer with its own resident copy).
 
+--adapters R times a training step instead: forward and backward through
+the host API with rank-R adapters on every layer of the mixture.
+
 Prints one JSON line.  `value` comes from the timed steps (synchronised on
 both sides, no per-kernel events).  `roofline` is for the dominant kernel:
 HBM-bound gemv_gateup (decode) or MFMA-bound mfma_gateup (prefill); achieved
@@ -43,6 +46,7 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer tokens/s @1 GPU; achieved HBM GB/s & MFMA util vs peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
 
 WORKLOADS = {
     "c2": dict(d=1024, E=16, k=2, h=2048, S=0, prec="int8", T=32, layers=1, copies=4, seed=0),
@@ -138,6 +142,99 @@ def traffic_from_profiles(key):
     return None if entry is None else entry.get("bytes_per_launch")
 
 
+def transposed_bytes(c, load, T):
+    """Algorithmic HBM bytes of the backward's three transposed products over
+    the compressed rows (down, gate, up): every active expert's three
+    matrices once, the gradients read and the input-side gradients written
+    (fp32)."""
+    active = int(np.count_nonzero(load)) + c["S"]
+    P = int(load.sum()) + c["S"] * T
+    per_expert = 2 * expert_bytes(c, c["h"], c["d"]) + expert_bytes(c, c["d"], c["h"])
+    return active * per_expert + P * (c["d"] + c["h"] + 2 * c["h"] + c["h"] + 2 * c["d"]) * 4
+
+
+def adapter_bench(args, c):
+    """--adapters R: one training step of a layer whose every layer carries a
+    rank-R adapter (alpha 2R): forward and backward through the host API
+    (float64 rows in and out over PCIe, as the reference's Forward and
+    Backward take them).  The roofline is for the transposed product over
+    the compressed rows, timed by the library's per-kernel events."""
+    import gotransformers_amd as gt
+    from oracle import lora
+    T, d = c["T"], c["d"]
+    spec = make_specs(gt, c)[0]
+    ctx = gt.Context(0)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    m.add_adapters(args.adapters, 2.0 * args.adapters, seed=1)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((T, d))
+    G = rng.uniform(-1, 1, (T, d))
+    steps = args.steps or 50
+    warmup = args.warmup if args.warmup is not None else 5
+    for _ in range(warmup):
+        m.forward(x)
+        m.backward(G)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.forward(x)
+        m.backward(G)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    load = m.last_expert_load()
+    ctx.timing(True)
+    ctx.timing_reset()
+    n_detail = min(steps, 20)
+    for _ in range(n_detail):
+        m.forward(x)
+        m.backward(G)
+    times = ctx.timing_read()
+    ctx.timing(False)
+    m.destroy()
+    ctx.close()
+    tr_ms, tr_calls = times["rows_transposed"]
+    per_step_s = tr_ms / n_detail / 1e3
+    P = int(load.sum()) + c["S"] * T
+    if T * c["k"] > 8 * c["E"]:  # many positions per expert: bound by arithmetic (fp32-exact products)
+        work = 2.0 * P * 3 * c["d"] * c["h"]
+        achieved = work / per_step_s / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / MFMA_FP32_PEAK_TFLOPS}
+    else:
+        work = transposed_bytes(c, load, T)
+        achieved = work / per_step_s / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+    roof.update({"traffic": None, "kernel": "rows_transposed", "algorithmic_per_step": work,
+                 "mean_launch_us": tr_ms / tr_calls * 1e3, "launches_per_step": tr_calls / n_detail})
+    cpu = None
+    if not args.no_cpu:
+        ads = lora.make_adapters(spec, args.adapters, 2.0 * args.adapters, np.random.default_rng(1))
+        tokens = min(T, 8)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            _, st = lora.forward(spec, ads, x[:tokens])
+            lora.backward(spec, ads, st, G[:tokens], lora.zero_grads(spec, ads))
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds:
+                break
+        cpu = {"value": tokens * reps / el, "unit": "tokens/s", "cores": host_cores(), "kind": "port",
+               "sample": f"{reps} forward+backward steps of the float64 adapter restatement (numpy) over "
+                         f"{tokens} tokens, {el:.1f} s"}
+    line = {
+        "metric": "MoE-layer adapter training tokens/s (forward + backward, host API) @1 GPU",
+        "value": T / (ms / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload} layer with rank-{args.adapters} adapters on every layer, T={T}",
+                   "tokens": T, "d_model": d, "routed_experts": c["E"], "shared_experts": c["S"],
+                   "top_k": c["k"], "expert_hidden": c["h"], "expert_weights": f"{c['prec']} per-16 fp32 scales"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "detail": {"kernel_ms_per_step_events": {k: v[0] / n_detail for k, v in sorted(times.items())}},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -150,6 +247,8 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay each step as a recorded HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (for PMC byte-counter calibration)")
+    ap.add_argument("--adapters", type=int, default=0,
+                    help="time a training step (forward + backward) with rank-R adapters on every layer")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
@@ -163,6 +262,12 @@ def main():
     c = dict(WORKLOADS[args.workload])
     if args.tokens:
         c["T"] = args.tokens
+    if args.adapters:
+        if c["layers"] != 1:
+            print("--adapters measures a single layer (c2, c3 or c4)", file=sys.stderr)
+            sys.exit(2)
+        adapter_bench(args, c)
+        return
     T, d = c["T"], c["d"]
     prefill_like = T * c["k"] > 8 * c["E"]
     steps = args.steps or (400 if not prefill_like and c["layers"] == 1 else 30 if c["layers"] == 1 else 10)
