@@ -24,10 +24,12 @@
 // Tiles: the m-tiles of all groups (the dispatch kernel wrote their count
 // and a (group, first position, positions) descriptor per tile; blocks past
 // the last tile exit) times the column tiles, in a 1-D grid ordered for the
-// XCDs: the hardware hands block b to XCD b % 8, so block b takes m-tile
-// 8*(j / NT) + b % 8 and column tile j % NT with j = b / 8 -- the column
-// tiles of one m-tile run back to back on one XCD and find its activation
-// rows in that XCD's L2.
+// XCDs: the hardware hands block b to XCD x = b % 8, and XCD x takes the
+// x-th eighth of the m-tiles, in order, each with its NT column tiles back
+// to back (block b: m-tile x * ceil(tiles / 8) + j / NT, column tile j % NT,
+// j = b / 8).  An m-tile's activation rows and an expert's weights (its
+// m-tiles are consecutive) are then read from HBM once per XCD that needs
+// them and found in that XCD's L2 by the other tiles.
 #include <type_traits>
 
 #include "common.h"
@@ -156,11 +158,12 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDA];
 
     const int j8 = blockIdx.x >> 3;
-    const int tile = (j8 / a.ntiles_n) * 8 + (blockIdx.x & 7);
-    const int ntile = j8 % a.ntiles_n;
     const int ntiles = *a.count;
-    const int4 dsc = a.desc[tile];  // in bounds: the table has 8 entries of slack past the largest tile count
-    if (tile >= ntiles) return;
+    const int per_xcd = (ntiles + 7) >> 3;
+    const int tile = (blockIdx.x & 7) * per_xcd + j8 / a.ntiles_n;
+    const int ntile = j8 % a.ntiles_n;
+    if (j8 / a.ntiles_n >= per_xcd || tile >= ntiles) return;
+    const int4 dsc = a.desc[tile];
     const int g = dsc.x;
     const int p0 = dsc.y;  // first position of the tile
     const int M = dsc.z;   // positions in the tile
