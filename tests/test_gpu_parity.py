@@ -206,6 +206,41 @@ def test_device_forward_folds_two_term_combine(ctx, name, cfg, prec, T):
     assert rel_err(a, host) <= 1e-6
 
 
+@pytest.mark.parametrize("E,k", [(16, 3), (64, 4), (96, 2)])
+def test_decode_routing_ties_and_nan_match_the_oracle(ctx, E, k):
+    """The decode routing kernel (ranked choice for E <= 64, rounds of
+    arg-max above) on logits with exact ties and NaN: a router of zero
+    weights makes every logit of a token equal to its bias, and a NaN input
+    makes a token's logits NaN.  Chosen experts and gates are bit-exact
+    against the oracle's routing of the same float64 logits."""
+    say(f"decode routing ties/NaN E={E} k={k}")
+    d, T = 64, 6
+    spec = make_moe(gt.encode_rows, d=d, h=64, E=E, k=k, S=0, precision=INT8, seed=13)
+    spec.router.weights = gt.encode_rows(FLOAT32, np.zeros((E, d)))
+    bias = np.zeros(E)
+    bias[E // 3] = bias[E // 2] = 0.25  # a tie above the rest
+    spec.router.biases = bias
+    balance = np.zeros(E)
+    balance[1] = balance[E - 1] = 0.125  # ties among the balance-lifted experts
+    x = np.random.default_rng(14).uniform(-1, 1, (T, d))
+    x[2, 5] = np.nan
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        m.balance_biases = balance
+        with np.errstate(invalid="ignore"):
+            m.forward(x, path=gt.PATH_FP32)
+        r = m.last_routing()
+    finally:
+        m.destroy()
+    logits = np.tile(bias, (T, 1))
+    logits[2] = np.nan
+    want = oracle.route_from_logits(logits, k, balance)
+    assert np.array_equal(r.chosen, want.chosen)
+    finite = np.arange(T) != 2
+    assert np.array_equal(r.gates[finite].view(np.int64), want.gates[finite].view(np.int64))
+    assert np.all(np.isnan(r.gates[2])) and np.all(np.isnan(want.gates[2]))
+
+
 @pytest.mark.parametrize("T", [1, 17, 64, 65])
 @pytest.mark.parametrize("use_hash", [False, True])
 def test_decode_kernels_find_their_own_tokens(ctx, T, use_hash):
