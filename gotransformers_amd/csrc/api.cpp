@@ -404,11 +404,19 @@ struct Inputs {
     bool norm;
 };
 
+// A stack layer's combine left for the next layer's routing kernel to do.
+struct PendingCombine {
+    const float *slot;
+    const int32_t *pos;
+    const float *gates;
+    int S, k, d;
+};
+
 // Input preparation, routing and dispatch.  Few tokens: one fused launch.
 // Otherwise: convert or RMSNorm into ws.xf / ws.xb, router and top-k (or hash
 // routing), then the dispatch.  token_ids: device pointer (hash routing).
 int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t *token_ids, int path, hipStream_t s,
-                          float *zero_out = nullptr)
+                          float *zero_out = nullptr, const PendingCombine *pend = nullptr)
 {
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
@@ -456,12 +464,23 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         f.tile_off = w.tile_off;
         f.tile_desc = w.tile_desc;
         f.zero_out = zero_out;
+        if (pend) {  // x is the fp32 residual stream, updated in place first
+            f.pend_slot = pend->slot;
+            f.pend_pos = pend->pos;
+            f.pend_gates = pend->gates;
+            f.pend_S = pend->S;
+            f.pend_k = pend->k;
+        }
         // the fp32 path's kernels find their own tokens from the choices
         L->skipped_dispatch = path == GTMOE_PATH_FP32 && T <= kSelfDispatchMaxTokens;
         RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, !L->skipped_dispatch, s));
         return GTMOE_OK;
     }
     L->skipped_dispatch = false;
+    if (pend)
+        RUN(ctx, s, "combine",
+            launch_combine(T, pend->d, pend->S, pend->k, pend->slot, false, pend->pos, pend->gates,
+                           (const float *)in.x, (float *)in.x, nullptr, s));
     if (zero_out) RUN(ctx, s, "zero_out", launch_fill_i32(reinterpret_cast<int32_t *>(zero_out), T * L->d, 0, s));
     if (in.norm) {
         RUN(ctx, s, "rmsnorm", launch_rmsnorm((const float *)in.x, T, L->d, L->norm_w, xf, L->dp, xb, L->dp, s));
@@ -1589,6 +1608,8 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
                          uint32_t flags, hipStream_t s)
 {
     gtmoe_context *ctx = layers[0]->ctx;
+    PendingCombine pending{};
+    bool have_pending = false;
     for (int l = 0; l < n_layers; ++l) {
         gtmoe_layer *L = layers[l];
         const int path = choose_path(L, T, flags);
@@ -1601,12 +1622,22 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
             continue;
         }
         Workspace &w = L->ws;
-        rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s);
+        rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s, nullptr, have_pending ? &pending : nullptr);
+        have_pending = false;
         if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
         if (rc != GTMOE_OK) return rc;
-        RUN(ctx, s, "combine",
-            launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos, w.gates32, x, x, nullptr,
-                           s));
+        const int32_t *pos = L->skipped_dispatch ? nullptr : w.pos;
+        // on the fp32 path the next layer's routing kernel, which reads x
+        // anyway, does this layer's combine (one launch fewer per layer)
+        if (l + 1 < n_layers && path == GTMOE_PATH_FP32 &&
+            fused_route_fits(T, layers[l + 1]->k, layers[l + 1]->dp)) {
+            pending = PendingCombine{w.slot_out, pos, w.gates32, L->S, L->k, L->d};
+            have_pending = true;
+        } else {
+            RUN(ctx, s, "combine",
+                launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, pos, w.gates32, x, x, nullptr,
+                               s));
+        }
         mark_forward(L, T, path, s);
     }
     return GTMOE_OK;

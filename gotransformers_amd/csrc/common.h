@@ -189,6 +189,13 @@ struct FusedArgs {
     int32_t *load, *offsets, *rows, *pos, *goff, *tok, *tile_off;
     int4 *tile_desc;
     float *zero_out;  // [T][d] rows zeroed by the token's workgroup, or nullptr
+    // The previous stack layer's combine, done here before anything else
+    // (x is then float and updated in place): x[t] += shared rows + gate *
+    // routed slot rows, in the combine kernel's order and arithmetic.
+    const float *pend_slot;    // that layer's fp32 slot outputs, or nullptr: nothing pending
+    const int32_t *pend_pos;   // its pos table, or nullptr: slot rows at S*T + t*k + i
+    const float *pend_gates;   // [T][k]
+    int pend_S, pend_k;
 };
 
 // Launchers (each returns the hipError_t of its launch).

@@ -780,10 +780,31 @@ template <typename InT, bool NORM, bool HASH, int EPL, int NX>
 __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
     __shared__ double lg[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) float comb[NX * 256];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = blockIdx.x;
     const InT *xr = reinterpret_cast<const InT *>(a.x) + (size_t)t * a.d;
     const bool vec = (a.d & 3) == 0;
+
+    if constexpr (sizeof(InT) == 4) {
+        if (a.pend_slot) {  // the previous layer's combine (combine_kernel's arithmetic)
+            float *x = const_cast<float *>(reinterpret_cast<const float *>(xr));
+            for (int c = threadIdx.x; c < a.d; c += 1024) {
+                float acc = 0.f;
+                for (int s = 0; s < a.pend_S; ++s) acc += a.pend_slot[((size_t)s * a.T + t) * a.d + c];
+                for (int i = 0; i < a.pend_k; ++i) {
+                    const int q = a.pend_pos ? a.pend_pos[(size_t)t * a.pend_k + i] : t * a.pend_k + i;
+                    acc = fmaf(a.pend_gates[(size_t)t * a.pend_k + i],
+                               a.pend_slot[(size_t)(a.pend_S * a.T + q) * a.d + c], acc);
+                }
+                const float v = x[c] + acc;
+                x[c] = v;
+                comb[c] = v;
+            }
+            __syncthreads();
+            xr = reinterpret_cast<const InT *>(comb);  // this token's row, from LDS from here on
+        }
+    }
 
     // router bias of expert wave + 16 j in lane j; balance biases (wave 0)
     double bias_l = 0.0;
