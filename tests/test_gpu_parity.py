@@ -206,6 +206,22 @@ def test_device_forward_folds_two_term_combine(ctx, name, cfg, prec, T):
     assert rel_err(a, host) <= 1e-6
 
 
+@pytest.mark.parametrize("d,h,T", [(4096, 192, 16), (192, 4096, 64)])
+def test_widest_decode_gemv(ctx, d, h, T):
+    """The fp32 path at its widest K (4096): the gate/up (d) or down (h)
+    kernel stages 8 tokens x 4096 values as bf16 hi/lo (128 KiB of LDS) plus
+    the self-dispatch entry list."""
+    say(f"widest GEMV d={d} h={h} T={T}")
+    spec = make_moe(gt.encode_rows, d=d, h=h, E=6, k=3, S=1, precision=FP4, seed=15, std=0.02, bias_std=0.01)
+    x = np.random.default_rng(16).uniform(-1, 1, (T, d))
+    y, r, used = run_layer(ctx, spec, x, gt.PATH_FP32)
+    assert used == gt.PATH_FP32
+    ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates, threads=8)
+    e = rel_err(y, ref.outputs)
+    say(f"widest GEMV max rel err {e:.2e}")
+    assert e <= FP32_TOL
+
+
 @pytest.mark.parametrize("E,k", [(16, 3), (64, 4), (96, 2)])
 def test_decode_routing_ties_and_nan_match_the_oracle(ctx, E, k):
     """The decode routing kernel (ranked choice for E <= 64, rounds of
