@@ -629,6 +629,11 @@ hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
 {
     static_assert(kGemvSlice <= 8, "at most two token quads per slice");
     if (a.nblocks % Chunk<PREC>::CB) return hipErrorInvalidValue;
+    // a self-dispatching gate/up launch whose experts nearly all have tokens,
+    // over K <= 32 chunks: four waves per workgroup (eight chunks each) fit
+    // every busy workgroup at once; eight would leave some for a second round
+    if (GATEUP && a.self_dispatch && a.nblocks / Chunk<PREC>::CB <= 32 && a.T * a.k >= a.E)
+        return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
     if (waves_for<PREC>(a) == 8) return launch_nw<PREC, GATEUP, 8>(a, max_slices, s);
     return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
 }
