@@ -150,6 +150,41 @@ __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h
     return __builtin_bit_cast(bf16x8, o);
 }
 
+// The output tile in LDS: 128 rows of 128 bf16 columns, row stride OLD
+// (68 words: the rows m and m + 4 that one ds_write covers fall on disjoint
+// banks).
+constexpr int OLD = 136;
+static_assert(BM * OLD <= 2 * BM * LDA, "the output tile fits in the activation buffers");
+
+// Rows [0, M) of the LDS output tile to out rows p0 + m; tile column c goes
+// to output column col_of(c) (groups of 8 tile columns map to 8 consecutive
+// output columns).  Thread t stores the 16-byte pieces t + 256 i (row
+// piece / 16, columns 8 (piece % 16) ..).  Widths or strides that are not
+// multiples of 8 columns take 2-byte stores.
+template <typename ColOf>
+__device__ __forceinline__ void store_tile(const MfmaArgs &a, const uint16_t *os, int p0, int M, ColOf col_of)
+{
+    uint16_t *out = reinterpret_cast<uint16_t *>(a.out);
+    const int tid = threadIdx.x;
+    if (a.n % 8 == 0 && a.ldo % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < BM * 16 / 256; ++i) {
+            const int piece = tid + 256 * i;
+            const int m = piece >> 4, c = (piece & 15) * 8;
+            const int n = col_of(c);
+            if (m < M && n < a.n)
+                *reinterpret_cast<uint4 *>(out + (size_t)(p0 + m) * a.ldo + n) =
+                    *reinterpret_cast<const uint4 *>(os + m * OLD + c);
+        }
+    } else {
+        for (int e = tid; e < BM * 128; e += 256) {
+            const int m = e >> 7, c = e & 127;
+            const int n = col_of(c);
+            if (m < M && n < a.n) out[(size_t)(p0 + m) * a.ldo + n] = os[m * OLD + c];
+        }
+    }
+}
+
 }  // namespace
 
 template <int PREC, bool GATEUP>
@@ -316,64 +351,60 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     }
     if (k < nsteps) step(std::integral_constant<int, 0>{}, k);
 
-    // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows
-    // 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r.  Full tiles
-    // (the common case) take a path without per-row checks.
+    // epilogue: the tile's bf16 outputs are put in LDS (free now: every wave
+    // is past its last read of the activations) and leave in 16-byte stores
+    // of whole row pieces.  Lane holds column (lane & 31) of each 32x32 tile,
+    // rows 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r; rows past
+    // the tile's M are computed from zero activations and not stored.
+    uint16_t *os = &As[0][0][0];
     const int rq = h * 4;
-    const bool full = M >= BM;
+    auto put = [&](int i, int r, int c, uint32_t pair) {  // registers r, r + 1 (rows m, m + 1)
+        const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
+        os[m * OLD + c] = (uint16_t)pair;
+        os[(m + 1) * OLD + c] = (uint16_t)(pair >> 16);
+    };
     if constexpr (GATEUP) {
         const int n = ncol[0];
-        if (n < a.n) {
-            const float bg = a.b0[(size_t)g * a.n + n], bu = a.b1[(size_t)g * a.n + n];
-            uint16_t *out = reinterpret_cast<uint16_t *>(a.out) + (size_t)p0 * a.ldo + n;
-            auto emit = [&](int i, int r) {
-                const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
-                float gv = acc[i][0][r] + bg;
-                float uv = acc[i][1][r] + bu;
-                if (a.clamp > 0.f) {
+        const bool has = n < a.n;
+        const float bg = has ? a.b0[(size_t)g * a.n + n] : 0.f, bu = has ? a.b1[(size_t)g * a.n + n] : 0.f;
+        const int c = wave * 32 + col;
+        auto emit_all = [&](auto clamp_tag) {
+            constexpr bool CL = decltype(clamp_tag)::value;
+            auto swiglu = [&](float gv, float uv) {
+                if constexpr (CL) {
                     gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
                     uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
                 }
-                const __bf16 hv = (__bf16)(silu(gv) * uv);
-                out[(size_t)m * a.ldo] = __builtin_bit_cast(uint16_t, hv);
+                return silu(gv) * uv;
             };
-            if (full) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) emit(i, r);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (i * 32 + 8 * (r >> 2) + rq + (r & 3) < M) emit(i, r);
-            }
-        }
+                for (int r = 0; r < 16; r += 2)
+                    put(i, r, c,
+                        pack_bf16(swiglu(acc[i][0][r] + bg, acc[i][1][r] + bu),
+                                  swiglu(acc[i][0][r + 1] + bg, acc[i][1][r + 1] + bu)));
+        };
+        if (a.clamp > 0.f) emit_all(std::true_type{});
+        else emit_all(std::false_type{});
+        __syncthreads();
+        // tile column c is hidden column ntile * 128 + c
+        store_tile(a, os, p0, M, [&](int c) { return ntile * (BN / 2) + c; });
     } else {
-        uint16_t *out = reinterpret_cast<uint16_t *>(a.out) + (size_t)p0 * a.ldo;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+            // one column tile of every wave per pass: tile column c is output
+            // column ntile * 256 + (c / 32) * 64 + j * 32 + c % 32
             const int n = ncol[j];
-            if (n >= a.n) continue;
-            const float bd = a.b0[(size_t)g * a.n + n];
-            auto emit = [&](int i, int r) {
-                const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
-                const __bf16 v = (__bf16)(acc[i][j][r] + bd);
-                out[(size_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, v);
-            };
-            if (full) {
+            const float bd = n < a.n ? a.b0[(size_t)g * a.n + n] : 0.f;
+            const int c = wave * 32 + col;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) emit(i, r);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (i * 32 + 8 * (r >> 2) + rq + (r & 3) < M) emit(i, r);
-            }
+                for (int r = 0; r < 16; r += 2) put(i, r, c, pack_bf16(acc[i][j][r] + bd, acc[i][j][r + 1] + bd));
+            __syncthreads();
+            store_tile(a, os, p0, M, [&](int c) { return ntile * BN + (c >> 5) * 64 + j * 32 + (c & 31); });
+            if (j == 0) __syncthreads();  // the next pass rewrites the LDS tile
         }
     }
 }
