@@ -333,7 +333,9 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
         dequant_pair(bq[ST ^ 1], 0, bfa);  // pair 0 of step k + 1 (past the end: unused)
         interleave();
         __builtin_amdgcn_sched_barrier(0);
-        if (k + 1 < nsteps) store_a(ST ^ 1, av[ST ^ 1]);
+        // past the last step this stores a re-load nobody reads (the
+        // epilogue reuses the buffers only after the barrier below)
+        store_a(ST ^ 1, av[ST ^ 1]);
         __syncthreads();
     };
 

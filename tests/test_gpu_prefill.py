@@ -72,6 +72,75 @@ def test_small_layers_bf16_path(ctx, name, prec):
     assert e <= BF16_TOL, e
 
 
+def run_prefill(ctx, spec, x, ids=None):
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        y = m.forward(x, ids, path=gt.PATH_BF16)
+        r = m.last_routing()
+        assert m.last_path == gt.PATH_BF16
+    finally:
+        m.destroy()
+    check_dispatch(r, len(spec.routed))
+    ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates, threads=16)
+    return y, ref.outputs
+
+
+def row_rel_err(y, r):
+    """Worst row of max |y - r| / max |r| (rows of any magnitude)."""
+    return float(np.max(np.max(np.abs(y - r), axis=1) / np.max(np.abs(r), axis=1)))
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+@pytest.mark.parametrize("prec", [FLOAT32, INT8, FP4])
+def test_small_layers_past_the_fused_routing(ctx, name, prec):
+    """T*k above the fused routing's 2048: the rows are prepared by the
+    conversion kernel and routed by the separate router and top-k."""
+    cfg = SMALL[name]
+    T = 2048 // cfg["k"] + 37
+    say(f"prefill past the fused routing {name} precision {prec} T={T}")
+    spec = make_moe(gt.encode_rows, precision=prec, seed=17, std=0.3, bias_std=0.05, **cfg)
+    rng = np.random.default_rng(18)
+    x = rng.uniform(-1, 1, size=(T, cfg["d"]))
+    ids = rng.integers(0, 1000, size=T) if cfg.get("use_hash") else None
+    y, ref = run_prefill(ctx, spec, x, ids)
+    e = rel_err(y, ref)
+    say(f"[{name} / {prec}] max rel err {e:.3e}")
+    assert e <= BF16_TOL, e
+
+
+@pytest.mark.parametrize("prec", [INT8, FP4])
+def test_rows_of_any_magnitude(ctx, prec):
+    """Rows from 1e-8 to 1e8 in magnitude: every row to the bar on its own.
+    Hash routing: learned routing of a 1e8 row can drive every affinity to
+    zero and its gates to 0/0, in the reference as well."""
+    say(f"prefill rows of any magnitude, precision {prec}")
+    spec = make_moe(gt.encode_rows, d=96, h=64, E=8, k=2, S=1, precision=prec, seed=19, std=0.3, bias_std=0.05,
+                    use_hash=True)
+    rng = np.random.default_rng(20)
+    T = 1100
+    x = rng.uniform(-1, 1, size=(T, 96)) * (10.0 ** rng.integers(-8, 9, size=(T, 1)))
+    ids = rng.integers(0, 1000, size=T)
+    y, ref = run_prefill(ctx, spec, x, ids)
+    e = row_rel_err(y, ref)
+    say(f"[{prec}] worst row rel err {e:.3e}")
+    assert e <= BF16_TOL, e
+
+
+@pytest.mark.parametrize("prec", [INT8, FP4])
+@pytest.mark.parametrize("std", [1e-6, 1e5])
+def test_weights_of_extreme_scale(ctx, prec, std):
+    """Block scales far from 1 in either direction (weights of std 1e-6 and
+    1e5), to the same bar."""
+    say(f"weights std {std} precision {prec}")
+    spec = make_moe(gt.encode_rows, d=64, h=48, E=6, k=2, S=1, precision=prec, seed=21, std=std, router_std=0.3,
+                    bias_std=0.0)
+    x = np.random.default_rng(22).uniform(-1, 1, size=(1100, 64))
+    y, ref = run_prefill(ctx, spec, x)
+    e = rel_err(y, ref)
+    say(f"[std {std} / {prec}] max rel err {e:.3e}")
+    assert e <= BF16_TOL, e
+
+
 def test_bf16_one_row_matches_many_rows(ctx):
     say("bf16 one row vs many rows")
     spec = make_moe(gt.encode_rows, d=128, h=192, E=4, k=2, S=1, seed=9, precision=INT8)
