@@ -206,13 +206,19 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, h = lane >> 5;
 
-    // activations: thread -> one row, half of the K step (32 values); rows
+    // activations: thread t -> rows t/8 + 32i (i < 4), 8 values at 8 (t % 8)
+    // of the K step, so that eight lanes read a row's whole 128-byte piece
+    // per load (a wave touches 8 cache lines per load, not 32 partly); rows
     // past the tile read past the buffer and get zeros
-    const int ar = tid >> 1, ah = tid & 1;
+    const int ar = tid >> 3, ac = tid & 7;
     const __amdgpu_buffer_rsrc_t asrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(a.a), 0, (int)(a.a_rows * a.lda * 2), kRawBufferWord3);
-    uint32_t aoff = 0x80000000u;
-    if (ar < M) aoff = ((uint32_t)(GATEUP ? a.tok[p0 + ar] : p0 + ar) * (uint32_t)a.lda + ah * 32) * 2u;
+    uint32_t aoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = ar + 32 * i;
+        aoff[i] = r < M ? ((uint32_t)(GATEUP ? a.tok[p0 + r] : p0 + r) * (uint32_t)a.lda + ac * 8) * 2u : 0x80000000u;
+    }
 
     // weights: the wave's two column tiles (gate/up: the same 32 neurons of
     // gate and up; down: 64 consecutive rows), a group's matrices as buffer
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
         const int k0 = min(step, nsteps - 1) * BK;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(asrc, aoff, k0 * 2 + 16 * i, 0));
+            v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(asrc, aoff[i], k0 * 2, 0));
     };
     auto load_b = [&](BRaw<PREC> (&q)[2], int step) {
         const int m = min(step, nsteps - 1);
@@ -277,9 +283,8 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             for (int p = 0; p < 2; ++p) load_block<PREC>(q[j], p, bsrc[j], bvo[j], bvs[j], m, p);
     };
     auto store_a = [&](int buf, const uint4 (&v)[4]) {
-        uint4 *pa = reinterpret_cast<uint4 *>(&As[buf][ar][ah * 32]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pa[i] = v[i];
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4 *>(&As[buf][ar + 32 * i][ac * 8]) = v[i];
     };
     // The K step is done in two halves (pair p = 0, 1: 16 MFMAs each, K
     // values of scale blocks 2p and 2p + 1).  While the MFMAs of one half run,
@@ -323,11 +328,14 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     // step k of the pipeline (ST = k % 2); bfa holds pair 0 of step k
     auto step = [&](auto st_tag, int k) {
         constexpr int ST = decltype(st_tag)::value;
+        // av[ST] went to LDS at the end of the previous step: its refill
+        // goes first, two whole steps ahead of its own store
+        load_a(av[ST], k + 2);
+        __builtin_amdgcn_sched_barrier(0);
         mfma_pair(ST, 0, bfa);
         dequant_pair(bq[ST], 1, bfb);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
-        load_a(av[ST], k + 2);
         load_b(bq[ST], k + 2);
         mfma_pair(ST, 1, bfb);
         dequant_pair(bq[ST ^ 1], 0, bfa);  // pair 0 of step k + 1 (past the end: unused)
