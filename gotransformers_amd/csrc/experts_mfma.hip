@@ -61,18 +61,19 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // Codes of the two scale blocks a lane dequantizes per K step, per column
-// tile, and their scales.
+// tile, and the scales of the row's four blocks of the step (the lane uses
+// blocks 2p + h: one 16-byte load serves both halves of the wave).
 template <int PREC>
 struct BRaw;
 template <>
 struct BRaw<kInt8> {
     uint4 q[2];
-    float s[2];
+    float s[4];
 };
 template <>
 struct BRaw<kFP4> {
     uint2 q[2];
-    float s[2];
+    float s[4];
 };
 template <>
 struct BRaw<kFloat32> {
@@ -90,21 +91,18 @@ struct GroupSrc {
     __amdgpu_buffer_rsrc_t scales;
 };
 
-// Block b = 4m + 2p + h of the K step's lane row, where m = k0 / 64 and h =
-// lane / 32 (the lane's half).  vo / vs: the lane's byte offsets of its row
-// (plus its half's share) in the codes / scales; the rest is scalar.
+// Codes of block b = 4m + 2p + h of the K step's lane row, where m = k0 / 64
+// and h = lane / 32 (the lane's half).  vo: the lane's byte offset of its row
+// (plus its half's share) in the codes; the rest is scalar.
 template <int PREC>
-__device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc &src, uint32_t vo, uint32_t vs,
-                                           int m, int p)
+__device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc &src, uint32_t vo, int m, int p)
 {
     if constexpr (PREC == kInt8) {
-        // unit b, scale (b >> 2, b & 3); vo carries h * 1024, vs h * 4
+        // unit b; vo carries h * 1024
         r.q[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, (4 * m + 2 * p) * 1024, 0));
-        r.s[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.scales, vs, (m * 256 + 2 * p) * 4, 0));
     } else if constexpr (PREC == kFP4) {
         // unit b >> 1 = 2m + p, byte (b & 1) * 8; vo carries h * 8
         r.q[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.codes, vo, (2 * m + p) * 1024, 0));
-        r.s[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.scales, vs, (m * 256 + 2 * p) * 4, 0));
     } else {
         // units 4b .. 4b + 3; vo carries 4h * 1024
 #pragma unroll
@@ -114,6 +112,23 @@ __device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc 
     }
 }
 
+// The four block scales (4m .. 4m + 3) of the lane's row for K step m; vs:
+// the row's byte offset in the scales.
+template <int PREC>
+__device__ __forceinline__ void load_scales(BRaw<PREC> &r, const GroupSrc &src, uint32_t vs, int m)
+{
+    if constexpr (PREC != kFloat32) {
+        const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(src.scales, vs, m * 1024, 0));
+        r.s[0] = v.x;
+        r.s[1] = v.y;
+        r.s[2] = v.z;
+        r.s[3] = v.w;
+    }
+}
+
+// The lane's half of the wave (its block of a pair is 2p + half).
+__device__ __forceinline__ bool lane_half() { return (threadIdx.x & 32) != 0; }
+
 // Values 8h..8h+7 of block i as bf16 (times the block scale).
 template <int PREC>
 __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h)
@@ -121,7 +136,7 @@ __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h
     u32x4 o;
     if constexpr (PREC == kInt8) {
         const uint32_t d0 = h ? r.q[i].z : r.q[i].x, d1 = h ? r.q[i].w : r.q[i].y;
-        const float s = r.s[i];
+        const float s = lane_half() ? r.s[2 * i + 1] : r.s[2 * i];  // constant indices: no scratch
         o[0] = pack_bf16((float)(int)(int8_t)d0 * s, (float)(int)(int8_t)(d0 >> 8) * s);
         o[1] = pack_bf16((float)(int)(int8_t)(d0 >> 16) * s, (float)(int)(int8_t)(d0 >> 24) * s);
         o[2] = pack_bf16((float)(int)(int8_t)d1 * s, (float)(int)(int8_t)(d1 >> 8) * s);
@@ -131,7 +146,7 @@ __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h
         // scale operand only takes a power of two, so it stays 1.0 and the
         // block scale is applied in fp32)
         const uint32_t d = h ? r.q[i].y : r.q[i].x;
-        const float s = r.s[i];
+        const float s = lane_half() ? r.s[2 * i + 1] : r.s[2 * i];  // constant indices: no scratch
         const f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
         const f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
         const f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
@@ -242,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
         if constexpr (PREC != kFloat32) {
             bsrc[j].scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(sc) + (size_t)g * a.s_group_stride, 0,
                                                              (int)(a.s_group_stride * 4), kRawBufferWord3);
-            bvs[j] = ((uint32_t)(n / 64) * 64u * (uint32_t)a.nblocks + (uint32_t)(n % 64) * 4u + h) * 4u;
+            bvs[j] = ((uint32_t)(n / 64) * 64u * (uint32_t)a.nblocks + (uint32_t)(n % 64) * 4u) * 4u;
         } else {
             bsrc[j].scales = bsrc[j].codes;
             bvs[j] = 0;
@@ -278,9 +293,11 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
         const int m = min(step, nsteps - 1);
         // pair p of the step: this lane's block is 2p + h
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
-            for (int p = 0; p < 2; ++p) load_block<PREC>(q[j], p, bsrc[j], bvo[j], bvs[j], m, p);
+            for (int p = 0; p < 2; ++p) load_block<PREC>(q[j], p, bsrc[j], bvo[j], m, p);
+            load_scales<PREC>(q[j], bsrc[j], bvs[j], m);
+        }
     };
     auto store_a = [&](int buf, const uint4 (&v)[4]) {
 #pragma unroll
