@@ -128,13 +128,33 @@ hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *x
     return hipGetLastError();
 }
 
-// Slot rows are fp32 (fp32 path) or bf16 (MFMA path).
-__device__ __forceinline__ float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
-__device__ __forceinline__ float4 load4(const uint16_t *p)
+// Slot rows are fp32 (fp32 path) or bf16 (MFMA path); C consecutive values
+// of a row as floats (C = 4: one 16-byte load of fp32, C = 8: one of bf16).
+template <int C>
+__device__ __forceinline__ void loadC(const float *p, float (&v)[C])
 {
-    const uint2 v = *reinterpret_cast<const uint2 *>(p);
-    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
-                       __uint_as_float(v.y & 0xffff0000u));
+#pragma unroll
+    for (int q = 0; q < C; q += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(p + q);
+        v[q] = f.x;
+        v[q + 1] = f.y;
+        v[q + 2] = f.z;
+        v[q + 3] = f.w;
+    }
+}
+template <int C>
+__device__ __forceinline__ void loadC(const uint16_t *p, float (&v)[C])
+{
+#pragma unroll
+    for (int q = 0; q < C; q += 8) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p + q);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[q + 2 * i] = __uint_as_float(w[i] << 16);
+            v[q + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
 }
 __device__ __forceinline__ float load1(const float *p) { return *p; }
 __device__ __forceinline__ float load1(const uint16_t *p) { return __uint_as_float((uint32_t)*p << 16); }
@@ -146,49 +166,70 @@ __device__ __forceinline__ float load1(const uint16_t *p) { return __uint_as_flo
 // (token, slot), as the self-dispatching decode kernels write them).  With a residual: out = residual + that sum
 // (transformer/block.go:77).  Writes fp32 and/or float64 output.  Grid
 // (T, ceil(d / 1024)); each thread owns four consecutive columns.
-template <typename SlotT>
+// Each thread owns C consecutive columns (C = 4 for fp32 slot rows, 8 for
+// bf16: 16-byte loads); the routed rows (KB >= k of them, rows past k re-read
+// row 0 and are not added) are requested before the adds, which keep the
+// reference's order.  vec_io: residual and outputs are 16-byte aligned.
+template <typename SlotT, int KB>
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k, const SlotT *__restrict__ slot_out,
                                                       const int32_t *__restrict__ pos,
                                                       const float *__restrict__ gates32,
                                                       const float *__restrict__ residual, float *__restrict__ out32,
-                                                      double *__restrict__ out64)
+                                                      double *__restrict__ out64, bool vec_io)
 {
+    constexpr int C = sizeof(SlotT) == 2 ? 8 : 4;
     const int t = blockIdx.x;
-    const int j0 = (blockIdx.y * 256 + threadIdx.x) * 4;
+    const int j0 = (blockIdx.y * 256 + threadIdx.x) * C;
     if (j0 >= d) return;
-    int p[8];
-    float g[8];
+    int p[KB];
+    float g[KB];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        p[i] = i < k ? S * T + (pos ? pos[(size_t)t * k + i] : t * k + i) : 0;
-        g[i] = i < k ? gates32[(size_t)t * k + i] : 0.f;
+    for (int i = 0; i < KB; ++i) {
+        const int ii = i < k ? i : 0;
+        p[i] = S * T + (pos ? pos[(size_t)t * k + ii] : t * k + ii);
+        g[i] = gates32[(size_t)t * k + ii];
     }
-    const int n = min(4, d - j0);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    if (n == 4 && (d & 3) == 0) {
+    const int n = min(C, d - j0);
+    float acc[C];
+#pragma unroll
+    for (int q = 0; q < C; ++q) acc[q] = 0.f;
+    if (n == C && d % C == 0 && vec_io) {
+        float v[KB][C];
+#pragma unroll
+        for (int i = 0; i < KB; ++i) loadC<C>(slot_out + (size_t)p[i] * d + j0, v[i]);
         for (int s = 0; s < S; ++s) {
-            const float4 v = load4(slot_out + ((size_t)s * T + t) * d + j0);
-            acc[0] += v.x;
-            acc[1] += v.y;
-            acc[2] += v.z;
-            acc[3] += v.w;
+            float u[C];
+            loadC<C>(slot_out + ((size_t)s * T + t) * d + j0, u);
+#pragma unroll
+            for (int q = 0; q < C; ++q) acc[q] += u[q];
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (i < k) {
-                const float4 v = load4(slot_out + (size_t)p[i] * d + j0);
-                acc[0] = fmaf(g[i], v.x, acc[0]);
-                acc[1] = fmaf(g[i], v.y, acc[1]);
-                acc[2] = fmaf(g[i], v.z, acc[2]);
-                acc[3] = fmaf(g[i], v.w, acc[3]);
-            }
-    } else {
-        for (int q = 0; q < n; ++q) {
-            for (int s = 0; s < S; ++s) acc[q] += load1(slot_out + ((size_t)s * T + t) * d + j0 + q);
+        for (int i = 0; i < KB; ++i)
+            if (i < k)
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (i < k) acc[q] = fmaf(g[i], load1(slot_out + (size_t)p[i] * d + j0 + q), acc[q]);
+                for (int q = 0; q < C; ++q) acc[q] = fmaf(g[i], v[i][q], acc[q]);
+        const size_t o = (size_t)t * d + j0;
+        if (residual) {
+            float r[C];
+            loadC<C>(residual + o, r);
+#pragma unroll
+            for (int q = 0; q < C; ++q) acc[q] = r[q] + acc[q];
         }
+        if (out32)
+#pragma unroll
+            for (int q = 0; q < C; q += 4)
+                *reinterpret_cast<float4 *>(out32 + o + q) = make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
+        if (out64)
+#pragma unroll
+            for (int q = 0; q < C; q += 2)
+                *reinterpret_cast<double2 *>(out64 + o + q) = make_double2((double)acc[q], (double)acc[q + 1]);
+        return;
+    }
+    for (int q = 0; q < n; ++q) {
+        for (int s = 0; s < S; ++s) acc[q] += load1(slot_out + ((size_t)s * T + t) * d + j0 + q);
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+            if (i < k) acc[q] = fmaf(g[i], load1(slot_out + (size_t)p[i] * d + j0 + q), acc[q]);
     }
     for (int q = 0; q < n; ++q) {
         const size_t o = (size_t)t * d + j0 + q;
@@ -203,13 +244,22 @@ hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool
                           const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s)
 {
     if (T <= 0) return hipSuccess;
-    const dim3 grid(T, (d + 1023) / 1024);
-    if (slot_bf16)
-        hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, dim3(256), 0, s, T, d, S, k,
-                           static_cast<const uint16_t *>(slot_out), pos, gates32, residual, out32, out64);
-    else
-        hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, s, T, d, S, k,
-                           static_cast<const float *>(slot_out), pos, gates32, residual, out32, out64);
+    if (k < 1 || k > 8) return hipErrorInvalidValue;
+    auto aligned = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const bool vec_io = aligned(residual) && aligned(out32) && aligned(out64);  // null counts as aligned
+    auto go = [&](auto kb_tag) {
+        constexpr int KB = decltype(kb_tag)::value;
+        if (slot_bf16)
+            hipLaunchKernelGGL((combine_kernel<uint16_t, KB>), dim3(T, (d + 2047) / 2048), dim3(256), 0, s, T, d, S,
+                               k, static_cast<const uint16_t *>(slot_out), pos, gates32, residual, out32, out64,
+                               vec_io);
+        else
+            hipLaunchKernelGGL((combine_kernel<float, KB>), dim3(T, (d + 1023) / 1024), dim3(256), 0, s, T, d, S, k,
+                               static_cast<const float *>(slot_out), pos, gates32, residual, out32, out64, vec_io);
+    };
+    if (k <= 2) go(std::integral_constant<int, 2>{});
+    else if (k <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
     return hipGetLastError();
 }
 
