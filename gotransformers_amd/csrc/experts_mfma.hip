@@ -19,7 +19,9 @@
 // column l%32 and, for each pair of 16-value MFMA steps, one whole scale
 // block (block 2p + l/32 of the K step), whose first and second halves feed
 // the two steps.  The activations are read from LDS in the same permuted K
-// order.  The next step's global loads are in flight during the MFMAs.
+// order.  Global loads run two K steps ahead of the MFMAs, and the epilogue
+// stages the tile's bf16 outputs in LDS so that they leave in 16-byte row
+// pieces.
 //
 // Tiles: the m-tiles of all groups (the dispatch kernel wrote their count
 // and a (group, first position, positions) descriptor per tile; blocks past
