@@ -219,3 +219,33 @@ def test_c5_shaped_stack(ctx, T, path, tol):
     e = rel_err(x[sample], ref)
     say(f"[C5 stack T={T}] path {used}, max rel err {e:.3e}")
     assert e <= tol
+
+
+@pytest.mark.parametrize("path,T", [(gt.PATH_BF16, 1100), (gt.PATH_FP32, 300)])
+def test_device_buffers_off_16_byte_alignment(ctx, path, T):
+    """forward_device on caller buffers that start 4 bytes past a 16-byte
+    boundary (the combine then takes its scalar stores) gives the same bits
+    as on aligned buffers."""
+    import torch
+    say(f"device buffers off alignment, path {path}, T={T}")
+    d = 64
+    spec = make_moe(gt.encode_rows, d=d, h=96, E=8, k=3, S=1, precision=INT8, seed=31, std=0.1, bias_std=0.02)
+    x = np.random.default_rng(32).uniform(-1, 1, (T, d)).astype(np.float32)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        xa = torch.from_numpy(x).cuda()
+        ya = torch.full((T, d), float("nan"), device="cuda")
+        xbuf = torch.zeros(T * d + 4, device="cuda")
+        ybuf = torch.full((T * d + 4,), float("nan"), device="cuda")
+        xo, yo = xbuf[1:1 + T * d], ybuf[1:1 + T * d]  # 4 bytes past the allocation's alignment
+        xo.copy_(xa.reshape(-1))
+        assert xo.data_ptr() % 16 == 4 and yo.data_ptr() % 16 == 4
+        m.forward_device(T, xa.data_ptr(), ya.data_ptr(), path=path)
+        m.forward_device(T, xo.data_ptr(), yo.data_ptr(), path=path)
+        torch.cuda.synchronize()
+        assert m.last_path == path
+        a, b = ya.cpu().numpy(), yo.cpu().numpy().reshape(T, d)
+    finally:
+        m.destroy()
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(a, b)
