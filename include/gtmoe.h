@@ -158,8 +158,9 @@ int32_t gtmoe_forward(gtmoe_layer *layer, int32_t tokens, const double *inputs, 
                       double *outputs, uint32_t flags);
 
 /* Forward over device-resident fp32 activations (inputs and outputs T x d in
- * HBM, token_ids T int64 in HBM or NULL), enqueued on `stream` (a
- * hipStream_t; NULL = the context's stream) without synchronising.  Hash
+ * HBM, row-major, any 4-byte-aligned addresses; token_ids T int64 in HBM or
+ * NULL), enqueued on `stream` (a hipStream_t; NULL = the context's stream)
+ * without synchronising.  Hash
  * routing ids must be non-negative: the device cannot panic.  For callers
  * that keep activations on the GPU between layers; no reference counterpart
  * beyond Forward itself. */
