@@ -789,15 +789,29 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     if constexpr (sizeof(InT) == 4) {
         if (a.pend_slot) {  // the previous layer's combine (combine_kernel's arithmetic)
             float *x = const_cast<float *>(reinterpret_cast<const float *>(xr));
+            // the routed rows and gates of this token (at most 8; slots past
+            // pend_k re-read slot 0 and are not added), all requested before
+            // the adds, which keep the reference's order
+            const float *row[8];
+            float g[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int ii = i < a.pend_k ? i : 0;
+                const int q = a.pend_pos ? a.pend_pos[(size_t)t * a.pend_k + ii] : t * a.pend_k + ii;
+                row[i] = a.pend_slot + (size_t)(a.pend_S * a.T + q) * a.d;
+                g[i] = a.pend_gates[(size_t)t * a.pend_k + ii];
+            }
             for (int c = threadIdx.x; c < a.d; c += 1024) {
+                float v8[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v8[i] = row[i][c];
+                const float xc = x[c];
                 float acc = 0.f;
                 for (int s = 0; s < a.pend_S; ++s) acc += a.pend_slot[((size_t)s * a.T + t) * a.d + c];
-                for (int i = 0; i < a.pend_k; ++i) {
-                    const int q = a.pend_pos ? a.pend_pos[(size_t)t * a.pend_k + i] : t * a.pend_k + i;
-                    acc = fmaf(a.pend_gates[(size_t)t * a.pend_k + i],
-                               a.pend_slot[(size_t)(a.pend_S * a.T + q) * a.d + c], acc);
-                }
-                const float v = x[c] + acc;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (i < a.pend_k) acc = fmaf(g[i], v8[i], acc);
+                const float v = xc + acc;
                 x[c] = v;
                 comb[c] = v;
             }
