@@ -17,7 +17,8 @@
 // dequantized exactly once per workgroup, by the wave that uses it,
 // straight from the panel layout into MFMA operand registers: lane l holds
 // column l%32 and, for each pair of 16-value MFMA steps, one whole scale
-// block (block 2p + l/32 of the K step), whose first and second halves feed
+// block (block 2p + l/32 of the K step; FP4: 2(l/32) + p, so that its two
+// blocks of a step are one 16-byte unit), whose first and second halves feed
 // the two steps.  The activations are read from LDS in the same permuted K
 // order.  Global loads run two K steps ahead of the MFMAs, and the epilogue
 // stages the tile's bf16 outputs in LDS so that they leave in 16-byte row
@@ -74,7 +75,7 @@ struct BRaw<kInt8> {
 };
 template <>
 struct BRaw<kFP4> {
-    uint2 q[2];
+    uint4 u;  // the lane's whole unit of the step: its blocks for pairs 0 and 1
     float s[4];
 };
 template <>
@@ -93,9 +94,11 @@ struct GroupSrc {
     __amdgpu_buffer_rsrc_t scales;
 };
 
-// Codes of block b = 4m + 2p + h of the K step's lane row, where m = k0 / 64
-// and h = lane / 32 (the lane's half).  vo: the lane's byte offset of its row
-// (plus its half's share) in the codes; the rest is scalar.
+// Codes of the lane's block of pair p of K step m (m = k0 / 64, h = lane / 32,
+// the lane's half): Int8 and Float32 take block 4m + 2p + h; FP4 takes block
+// 4m + 2h + p, so that a lane's two blocks of a step are one 16-byte unit,
+// loaded with pair 0.  vo: the lane's byte offset of its row (plus its
+// half's share) in the codes; the rest is scalar.
 template <int PREC>
 __device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc &src, uint32_t vo, int m, int p)
 {
@@ -103,8 +106,8 @@ __device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc 
         // unit b; vo carries h * 1024
         r.q[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, (4 * m + 2 * p) * 1024, 0));
     } else if constexpr (PREC == kFP4) {
-        // unit b >> 1 = 2m + p, byte (b & 1) * 8; vo carries h * 8
-        r.q[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.codes, vo, (2 * m + p) * 1024, 0));
+        // unit 2m + h (blocks 4m + 2h and 4m + 2h + 1); vo carries h * 1024
+        if (p == 0) r.u = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, 2 * m * 1024, 0));
     } else {
         // units 4b .. 4b + 3; vo carries 4h * 1024
 #pragma unroll
@@ -147,8 +150,8 @@ __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h
         // e2m1 pairs, even value in the low nibble (the conversion's own
         // scale operand only takes a power of two, so it stays 1.0 and the
         // block scale is applied in fp32)
-        const uint32_t d = h ? r.q[i].y : r.q[i].x;
-        const float s = lane_half() ? r.s[2 * i + 1] : r.s[2 * i];  // constant indices: no scratch
+        const uint32_t d = i == 0 ? (h ? r.u.y : r.u.x) : (h ? r.u.w : r.u.z);
+        const float s = lane_half() ? r.s[2 + i] : r.s[i];  // block 2 half + i of the step
         const f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
         const f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
         const f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             (int)a.w_group_stride, kRawBufferWord3);
         const uint32_t rowoff = (uint32_t)(n / 64) * 64u * (uint32_t)a.row_bytes + (uint32_t)(n % 64) * 16u;
         if constexpr (PREC == kInt8) bvo[j] = rowoff + h * 1024u;
-        else if constexpr (PREC == kFP4) bvo[j] = rowoff + h * 8u;
+        else if constexpr (PREC == kFP4) bvo[j] = rowoff + h * 1024u;
         else bvo[j] = rowoff + h * 4096u;
         if constexpr (PREC != kFloat32) {
             bsrc[j].scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(sc) + (size_t)g * a.s_group_stride, 0,
@@ -293,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     };
     auto load_b = [&](BRaw<PREC> (&q)[2], int step) {
         const int m = min(step, nsteps - 1);
-        // pair p of the step: this lane's block is 2p + h
+        // pair p of the step: this lane's block is 2p + h (FP4: 2h + p)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -320,8 +323,8 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             // k-values of this MFMA step: lanes of half h carry values
-            // 8s2..8s2+7 of block 2p + h of the K step
-            const int kk = 16 * (2 * p + h) + 8 * s2;
+            // 8s2..8s2+7 of block 2p + h (FP4: 2h + p) of the K step
+            const int kk = 16 * (PREC == kFP4 ? 2 * h + p : 2 * p + h) + 8 * s2;
             bf16x8 af[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][i * 32 + col][kk]);
