@@ -282,8 +282,12 @@ class MixtureOfExperts:
         return m
 
     def destroy(self):
+        """Free the layer's device memory.  Refused (InvalidArgument, the
+        layer kept) while a recorded Graph uses the layer."""
         if self.handle:
-            library().gtmoe_layer_destroy(self.handle)
+            code = library().gtmoe_layer_destroy(self.handle)
+            if code != OK:
+                self.ctx.check(code)
             self.handle = None
 
     def upload(self, kind, index, which, rows, biases):

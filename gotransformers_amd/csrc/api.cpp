@@ -222,6 +222,9 @@ struct gtmoe_layer {
     AdapterSet ad_gate, ad_up, ad_down, ad_router;
     TrainWorkspace tw;
     int adapter_T = -1;  // tokens of the last forward through the adapter path, -1: none
+    // recorded graphs that hold pointers into this layer's workspace: while
+    // any exists the workspace is never reallocated
+    int live_graphs = 0;
 };
 
 namespace {
@@ -321,29 +324,25 @@ double decoded_value(const gtmoe_rows *r, int row, int i)
     }
 }
 
-int32_t ensure_workspace(gtmoe_layer *L, int T)
+// The buffers of a forward for `cap` tokens laid out from `base` (256-byte
+// aligned parts); returns the bytes they take.  With base null only the size
+// is computed.  Without host staging the float64 rows of the host-API calls
+// and the residual of a host-API stack are left out (device forwards only).
+size_t layout_workspace(const gtmoe_layer *L, int cap, bool host_staging, char *base, Workspace &w)
 {
-    gtmoe_context *ctx = L->ctx;
-    if (T <= L->ws.cap) return GTMOE_OK;
-    int cap = T < 64 ? 64 : T;
-    if (L->ws.base) {
-        HIP_TRY(ctx, hipDeviceSynchronize());
-        (void)hipFree(L->ws.base);
-        L->ws = Workspace{};
-    }
     const size_t P = (size_t)cap * (L->S + L->k);
     const size_t TK = (size_t)cap * L->k;
+    const size_t hs = host_staging ? 1 : 0;
     struct Part {
         void **ptr;
         size_t bytes;
     };
-    Workspace &w = L->ws;
     Part parts[] = {
-        {(void **)&w.x64, (size_t)cap * L->d * 8},      {(void **)&w.y64, (size_t)cap * L->d * 8},
+        {(void **)&w.x64, hs * cap * L->d * 8},         {(void **)&w.y64, hs * cap * L->d * 8},
         {(void **)&w.xf, (size_t)cap * L->dp * 4},      {(void **)&w.xb, (size_t)cap * L->dp * 2},
-        {(void **)&w.xs, (size_t)cap * L->d * 4},       {(void **)&w.logits, (size_t)cap * L->E * 8},
+        {(void **)&w.xs, hs * cap * L->d * 4},          {(void **)&w.logits, (size_t)cap * L->E * 8},
         {(void **)&w.chosen, TK * 4},                   {(void **)&w.gates, TK * 8},
-        {(void **)&w.gates32, TK * 4},                  {(void **)&w.ids, (size_t)cap * 8},
+        {(void **)&w.gates32, TK * 4},                  {(void **)&w.ids, hs * cap * 8},
         {(void **)&w.load, (size_t)L->E * 4},           {(void **)&w.offsets, (size_t)(L->E + 1) * 4},
         {(void **)&w.rows, TK * 4},                     {(void **)&w.pos, TK * 4},
         {(void **)&w.goff, (size_t)(L->G + 1) * 4},     {(void **)&w.tile_off, (size_t)(L->G + 1) * 4},
@@ -352,8 +351,35 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
         {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
         {(void **)&w.chunk_cnt, (size_t)dispatch_chunks(cap) * L->E * 4},
     };
-    size_t total = 0;
-    for (const Part &p : parts) total += align_up(p.bytes, 256);
+    size_t off = 0;
+    for (const Part &p : parts) {
+        if (base) *p.ptr = p.bytes ? base + off : nullptr;
+        off += align_up(p.bytes, 256);
+    }
+    if (base) {
+        w.base = base;
+        w.cap = cap;
+    }
+    return off;
+}
+
+int32_t ensure_workspace(gtmoe_layer *L, int T)
+{
+    gtmoe_context *ctx = L->ctx;
+    if (T <= L->ws.cap) return GTMOE_OK;
+    if (L->live_graphs > 0)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                    "a forward of %d tokens needs a larger workspace than the %d tokens this layer's %d recorded "
+                    "graph(s) use; destroy the graphs first",
+                    T, L->ws.cap, L->live_graphs);
+    int cap = T < 64 ? 64 : T;
+    if (L->ws.base) {
+        HIP_TRY(ctx, hipDeviceSynchronize());
+        (void)hipFree(L->ws.base);
+        L->ws = Workspace{};
+    }
+    Workspace w{};
+    const size_t total = layout_workspace(L, cap, true, nullptr, w);
     void *base = nullptr;
     HIP_TRY(ctx, hipMalloc(&base, total));
     // zero once: padding columns of the activation buffers are never written.
@@ -361,13 +387,7 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
     // non-blocking streams the forward runs on: wait for it here.
     HIP_TRY(ctx, hipMemset(base, 0, total));
     HIP_TRY(ctx, hipDeviceSynchronize());
-    size_t off = 0;
-    for (const Part &p : parts) {
-        *p.ptr = (char *)base + off;
-        off += align_up(p.bytes, 256);
-    }
-    w.base = base;
-    w.cap = cap;
+    layout_workspace(L, cap, true, (char *)base, L->ws);
     return GTMOE_OK;
 }
 
@@ -714,6 +734,8 @@ namespace {
 void free_graph(gtmoe_graph *g)
 {
     if (!g) return;
+    if (g->exec)
+        for (gtmoe_layer *L : g->layers) --L->live_graphs;
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;
@@ -744,7 +766,11 @@ int32_t capture(gtmoe_context *ctx, F &&record, gtmoe_graph *g)
     }
     g->graph = graph;
     e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
-    if (e != hipSuccess) return fail(ctx, GTMOE_ERR_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    if (e != hipSuccess) {
+        g->exec = nullptr;
+        return fail(ctx, GTMOE_ERR_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    for (gtmoe_layer *L : g->layers) ++L->live_graphs;
     return GTMOE_OK;
 }
 
@@ -1271,6 +1297,9 @@ int32_t gtmoe_layer_destroy(gtmoe_layer *L)
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (L->live_graphs > 0)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "the layer is part of %d recorded graph(s); destroy them first",
+                    L->live_graphs);
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
     free_adapters(L);
@@ -1451,10 +1480,18 @@ static int32_t check_forward_device(gtmoe_layer *L, int32_t T, const float *inpu
         return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "mixture of experts: hash routing needs one token ID per row");
     if (L->has_adapters)
         return fail(ctx, GTMOE_ERR_UNSUPPORTED, "a layer with low-rank adapters runs through gtmoe_forward");
+    if (T > 0) {
+        // the routing may clear the outputs while rows of the inputs are
+        // still being read: the two buffers must not overlap
+        const uintptr_t a = (uintptr_t)inputs, b = (uintptr_t)outputs;
+        const uintptr_t n = (uintptr_t)T * (uintptr_t)L->d * sizeof(float);
+        if (a < b + n && b < a + n)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "inputs and outputs overlap; a forward cannot run in place");
+    }
     *path = choose_path(L, T, flags);
     if (*path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
         return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
-    return ensure_workspace(L, T);
+    return GTMOE_OK;
 }
 
 // The kernels of one device forward, enqueued on s.
@@ -1491,9 +1528,9 @@ int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     int path = 0;
     rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
+    if (rc == GTMOE_OK) rc = ensure_workspace(L, tokens);
     if (rc != GTMOE_OK) return rc;
-    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    return forward_device_run(L, tokens, inputs, token_ids, outputs, path, s);
+    return forward_device_run(L, tokens, inputs, token_ids, outputs, path, (hipStream_t)stream);
 }
 
 int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen, double *gates, int32_t *load,
@@ -1654,6 +1691,13 @@ int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_
     const int T = tokens;
     if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
     if (T > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
+    if (chosen || gates)  // [n_layers][T][k] needs one k
+        for (int l = 1; l < n_layers; ++l)
+            if (layers[l]->k != layers[0]->k)
+                return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                            "stack layer %d picks %d experts per token and layer 0 picks %d; the routing outputs "
+                            "are [n_layers][T][k] for one k",
+                            l, layers[l]->k, layers[0]->k);
     const bool hashed = [&] {
         for (int l = 0; l < n_layers; ++l)
             if (layers[l]->desc.use_hash_routing) return true;
@@ -1707,8 +1751,7 @@ int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers,
     for (int l = 0; l < n_layers; ++l)
         if (layers[l]->desc.use_hash_routing && tokens > 0 && !token_ids)
             return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "hash routing needs one token ID per row");
-    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    return stack_run(layers, n_layers, tokens, x, token_ids, flags, s);
+    return stack_run(layers, n_layers, tokens, x, token_ids, flags, (hipStream_t)stream);
 }
 
 int32_t gtmoe_graph_capture_forward(gtmoe_layer *L, int32_t tokens, const float *inputs, const int64_t *token_ids,
@@ -1723,6 +1766,7 @@ int32_t gtmoe_graph_capture_forward(gtmoe_layer *L, int32_t tokens, const float 
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     int path = 0;
     rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
+    if (rc == GTMOE_OK) rc = ensure_workspace(L, tokens);
     if (rc != GTMOE_OK) return rc;
     gtmoe_graph *g = new gtmoe_graph;
     g->ctx = ctx;
@@ -1785,7 +1829,7 @@ int32_t gtmoe_graph_launch(gtmoe_graph *g, void *stream)
     gtmoe_context *ctx = g->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    hipStream_t s = (hipStream_t)stream;
     HIP_TRY(ctx, hipGraphLaunch(g->exec, s));
     for (size_t i = 0; i < g->layers.size(); ++i) {
         g->layers[i]->skipped_dispatch = g->skipped[i] != 0;
@@ -1873,7 +1917,7 @@ int32_t gtmoe_relaunch(gtmoe_layer *L, int32_t kernel, void *stream)
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     if (L->last_T <= 0 || !L->relaunch_ready)
         return fail(ctx, GTMOE_ERR_NOT_READY, "no forward with tokens to launch again");
-    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    hipStream_t s = (hipStream_t)stream;
     const bool gateup = kernel == GTMOE_KERNEL_GATEUP;
     if (L->last_path == GTMOE_PATH_FP32) {
         const GemvArgs &a = L->last_gemv[gateup ? 0 : 1];
@@ -1947,6 +1991,24 @@ int32_t gtmoe_layer_load_weights(gtmoe_layer *L, gtmoe_weights_file *f, const ch
                 return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
                             "saved parameter \"%s\" has %llu values but the parameter it's loading into has %llu",
                             wn.c_str(), (unsigned long long)wi.count, (unsigned long long)want);
+            // compressed rows are decoded at their stored shape: the codes and
+            // scales must each fit that shape, not only sum to the right total
+            if (wi.stored_as == kStoredRows) {
+                const uint64_t sb = (wi.width + 15) / 16;
+                const uint64_t codes_need = wi.precision == GTMOE_INT8      ? wi.rows * wi.width
+                                            : wi.precision == GTMOE_FP4     ? wi.rows * ((wi.width + 1) / 2)
+                                            : wi.precision == GTMOE_FLOAT32 ? wi.rows * wi.width * 4
+                                                                            : wi.rows * wi.width * 8;
+                const uint64_t scales_need =
+                    (wi.precision == GTMOE_INT8 || wi.precision == GTMOE_FP4) ? wi.rows * sb : 0;
+                if (wi.code_bytes != codes_need || wi.scale_count != scales_need)
+                    return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                                "saved parameter \"%s\" holds %llu value bytes and %llu scales, %llux%llu rows need "
+                                "%llu and %llu",
+                                wn.c_str(), (unsigned long long)wi.code_bytes, (unsigned long long)wi.scale_count,
+                                (unsigned long long)wi.rows, (unsigned long long)wi.width,
+                                (unsigned long long)codes_need, (unsigned long long)scales_need);
+            }
             continue;
         }
         if (wi.stored_as != kStoredRows)

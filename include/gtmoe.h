@@ -159,9 +159,12 @@ int32_t gtmoe_forward(gtmoe_layer *layer, int32_t tokens, const double *inputs, 
 
 /* Forward over device-resident fp32 activations (inputs and outputs T x d in
  * HBM, row-major, any 4-byte-aligned addresses; token_ids T int64 in HBM or
- * NULL), enqueued on `stream` (a hipStream_t; NULL = the context's stream)
- * without synchronising.  Hash
- * routing ids must be non-negative: the device cannot panic.  For callers
+ * NULL), enqueued on `stream` without synchronising.  `stream` is a
+ * hipStream_t; NULL is the device's null stream, which orders this forward
+ * after work the caller enqueued on the null stream (torch's default stream,
+ * for example) and before work enqueued there later.  Inputs and outputs must
+ * not overlap (GTMOE_ERR_INVALID_ARGUMENT): a forward does not run in place.
+ * Hash routing ids must be non-negative: the device cannot panic.  For callers
  * that keep activations on the GPU between layers; no reference counterpart
  * beyond Forward itself. */
 int32_t gtmoe_forward_device(gtmoe_layer *layer, int32_t tokens, const float *inputs,
@@ -197,12 +200,14 @@ int32_t gtmoe_route_from_logits(gtmoe_layer *layer, int32_t tokens, const double
  * l = 0..n_layers-1 (the residual of transformer.Block.Forward,
  * transformer/block.go:71-77).  x is T x d float64, updated in place; every
  * layer needs gtmoe_set_norm_weights and the same d.  When chosen/gates are
- * given they receive [n_layers][T][k] of each layer's routing. */
+ * given they receive [n_layers][T][k] of each layer's routing; every layer
+ * must then have the same k (GTMOE_ERR_INVALID_ARGUMENT otherwise). */
 int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, double *x,
                             const int64_t *token_ids, uint32_t flags, int32_t *chosen, double *gates);
 
 /* The same stack over a device-resident fp32 x (T x d in HBM, updated in
- * place), enqueued on `stream` without synchronising. */
+ * place), enqueued on `stream` without synchronising (NULL: the null stream,
+ * as for gtmoe_forward_device). */
 int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers, int32_t tokens, float *x,
                                    const int64_t *token_ids, uint32_t flags, void *stream);
 
@@ -210,10 +215,13 @@ int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers,
  * The decode step replayed without per-kernel launches: the kernels of
  * gtmoe_forward_device (one layer) or gtmoe_stack_forward_device (a stack)
  * for a fixed token count are recorded once into an instantiated hipGraph
- * and replayed by gtmoe_graph_launch on any stream.  The graph keeps the
- * device pointers it was recorded with: the caller refills the same buffers
- * between replays and keeps them alive; the layers must not be destroyed or
- * re-uploaded with other shapes while the graph exists.  Each replay counts
+ * and replayed by gtmoe_graph_launch on any stream (NULL: the null stream).
+ * The graph keeps the device pointers it was recorded with: the caller
+ * refills the same buffers between replays and keeps them alive.  While a
+ * graph exists, its layers keep their workspace in place: a forward on one
+ * of them with more tokens than any earlier call needed, and
+ * gtmoe_layer_destroy, return GTMOE_ERR_INVALID_ARGUMENT until the graph is
+ * destroyed.  Each replay counts
  * as a forward of every recorded layer (gtmoe_last_routing etc. read it).
  * Workspace is sized before recording; no replay allocates.  There is no
  * reference counterpart (the reference has no device graph); this serves
@@ -242,8 +250,8 @@ int32_t gtmoe_timing_read(gtmoe_context *ctx, int32_t capacity, char *names, dou
 int32_t gtmoe_last_path(const gtmoe_layer *layer, int32_t *path);
 
 /* Launch one expert kernel of the last forward on this layer again, with the
- * same arguments and workspace, on `stream` (a hipStream_t; NULL = the
- * context's stream), without synchronising.  Bracketing a burst of these with
+ * same arguments and workspace, on `stream` (a hipStream_t; NULL = the null
+ * stream), without synchronising.  Bracketing a burst of these with
  * events gives the kernel's duration free of per-launch event skew -- the
  * per-dispatch timing of Recorder.MeasureTime (gpu/compute.go:670-694) for a
  * single program.  kernel: GTMOE_KERNEL_GATEUP (gate/up + SwiGLU) or

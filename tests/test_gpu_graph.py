@@ -119,3 +119,34 @@ def test_graph_capture_rejects_bad_arguments(ctx):
             gt.Graph.capture_forward(m, 4, 0, 0)  # null buffers
     finally:
         m.destroy()
+
+
+def test_graph_keeps_its_layers_workspace(ctx):
+    """A recorded graph holds pointers into its layer's workspace: while it
+    exists a forward that would need a larger workspace, and destroying the
+    layer, are refused; after the graph is destroyed both work again."""
+    say("graph keeps the workspace it was recorded with")
+    d = 64
+    spec = make_moe(gt.encode_rows, d=d, h=96, E=4, k=2, S=1, precision=INT8, seed=41)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        T = 4
+        xg, yg = dev(np.random.default_rng(42).standard_normal((T, d))), torch.empty(T, d, device="cuda")
+        g = gt.Graph.capture_forward(m, T, xg.data_ptr(), yg.data_ptr(), path=gt.PATH_FP32)
+        big = np.random.default_rng(43).standard_normal((300, d))
+        with pytest.raises(gt.InvalidArgument, match="destroy the graphs first"):
+            m.forward(big)
+        with pytest.raises(gt.InvalidArgument, match="recorded graph"):
+            m.destroy()
+        assert m.handle
+        m.forward(big[:T])  # within the recorded workspace: allowed
+        g.launch()
+        torch.cuda.synchronize()
+        assert np.all(np.isfinite(yg.cpu().numpy()))
+        g.destroy()
+        y = m.forward(big)
+        r = m.last_routing()
+    finally:
+        m.destroy()
+    ref = oracle.moe_forward_routed(spec, big, r.chosen, r.gates)
+    assert rel_err(y, ref.outputs) <= 2e-2

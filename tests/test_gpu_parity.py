@@ -422,3 +422,49 @@ def test_small_stack_fp32(ctx):
             m.destroy()
     ref = oracle.stack_forward_routed(layers, norms, x0, chosen, gates)
     assert rel_err(x, ref) <= FP32_TOL
+
+
+def test_device_forward_refuses_overlapping_buffers(ctx):
+    """A forward does not run in place: overlapping inputs and outputs are
+    refused before anything is enqueued (the routing may clear the outputs
+    while input rows are still being read)."""
+    say("device forward in place refused")
+    spec = make_moe(gt.encode_rows, d=32, h=48, E=4, k=2, S=0, precision=INT8, seed=17)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        buf = torch.zeros(8 * 32 + 16, device="cuda")
+        with pytest.raises(gt.InvalidArgument, match="overlap"):
+            m.forward_device(8, buf.data_ptr(), buf.data_ptr())
+        with pytest.raises(gt.InvalidArgument, match="overlap"):
+            m.forward_device(8, buf.data_ptr(), buf[16:].data_ptr())
+        # adjacent, not overlapping: accepted
+        x = torch.from_numpy(np.random.default_rng(18).standard_normal(8 * 32).astype(np.float32)).cuda()
+        buf[:8 * 32].copy_(x)
+        out = torch.empty(8 * 32, device="cuda")
+        m.forward_device(8, buf.data_ptr(), out.data_ptr(), path=gt.PATH_FP32)
+        torch.cuda.synchronize()
+        r = m.last_routing()
+    finally:
+        m.destroy()
+    xs = x.cpu().numpy().astype(np.float64).reshape(8, 32)
+    ref = oracle.moe_forward_routed(spec, xs, r.chosen, r.gates)
+    assert rel_err(out.cpu().numpy().reshape(8, 32), ref.outputs) <= FP32_TOL
+
+
+def test_stack_routing_outputs_need_one_k(ctx):
+    """gtmoe_stack_forward's routing outputs are [n_layers][T][k]: layers
+    with different k are refused when they are asked for, and run when not."""
+    say("stack with different k")
+    specs = [make_moe(gt.encode_rows, d=32, h=48, E=6, k=k, S=1, seed=19 + k, precision=INT8) for k in (2, 3)]
+    ms = [gt.MixtureOfExperts.from_spec(ctx, s) for s in specs]
+    try:
+        for m in ms:
+            m.set_norm_weights(np.ones(32))
+        x0 = np.random.default_rng(20).standard_normal((5, 32))
+        with pytest.raises(gt.InvalidArgument, match="one k"):
+            gt.stack_forward(ms, x0, with_routing=True)
+        x = gt.stack_forward(ms, x0)
+    finally:
+        for m in ms:
+            m.destroy()
+    assert np.all(np.isfinite(x))

@@ -5,6 +5,7 @@ for bit; the forward is then checked against the oracle as in the other GPU
 tests.  Refusals follow checkSavedParameterFits (weightfile/weightfile.go:69-87)
 and leave a fresh layer without weights."""
 import copy
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -128,6 +129,17 @@ def test_layer_load_refusals(ctx, tmp_path):
 
     router_count = [(n, np.ones(4 * 63) if n == "moe.router.weights" else v) for n, v in good]
     expect(router_count, gt.InvalidArgument, 'saved parameter "moe.router.weights" has 252 values')
+
+    # a router stored as Int8 rows of another shape (8 x 32, as many values)
+    # whose codes and scales sum to the right byte count but do not fit that
+    # shape each (252 codes and 17 scales instead of 256 and 16):
+    # RowsFromSnapshot's byte sum takes it, decoding it at 8 x 32 would read
+    # past the codes, so the load refuses it first
+    r = gt.encode_rows(INT8, oracle.decode_rows(spec.router.weights).reshape(8, 32))
+    unbalanced = SimpleNamespace(precision=INT8, rows=8, width=32, values=r.values.reshape(-1)[:252].copy(),
+                                 scales=np.concatenate([r.scales.reshape(-1), [1.0]]).astype(np.float32))
+    router_split = [(n, unbalanced if n == "moe.router.weights" else v) for n, v in good]
+    expect(router_split, gt.InvalidArgument, "holds 252 value bytes and 17 scales, 8x32 rows need 256 and 16")
 
 
 def test_router_rows_of_another_shape(ctx, tmp_path):
