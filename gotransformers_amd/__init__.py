@@ -31,7 +31,7 @@ EXPORTED = [
     "gtmoe_abi_version", "gtmoe_device_count", "gtmoe_open", "gtmoe_close", "gtmoe_last_error",
     "gtmoe_encode_rows", "gtmoe_layer_create", "gtmoe_layer_destroy", "gtmoe_upload_rows",
     "gtmoe_set_balance_biases", "gtmoe_get_balance_biases", "gtmoe_set_norm_weights", "gtmoe_forward",
-    "gtmoe_forward_device", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
+    "gtmoe_forward_device", "gtmoe_forward_device_noalloc", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
     "gtmoe_route_from_logits", "gtmoe_stack_forward", "gtmoe_stack_forward_device", "gtmoe_timing_enable",
     "gtmoe_timing_reset", "gtmoe_timing_read", "gtmoe_last_path", "gtmoe_relaunch",
     "gtmoe_graph_capture_forward", "gtmoe_graph_capture_stack", "gtmoe_graph_launch", "gtmoe_graph_destroy",
@@ -92,6 +92,7 @@ def library():
         "gtmoe_set_norm_weights": ([P, P], i32),
         "gtmoe_forward": ([P, i32, P, P, P, u32], i32),
         "gtmoe_forward_device": ([P, i32, P, P, P, u32, P], i32),
+        "gtmoe_forward_device_noalloc": ([P, i32, P, P, P, u32, P], i32),
         "gtmoe_last_routing": ([P, P, P, P, P, P, P], i32),
         "gtmoe_last_expert_load": ([P, P], i32),
         "gtmoe_update_balance": ([P, dbl], i32),
@@ -410,6 +411,13 @@ class MixtureOfExperts:
         """Forward over device-resident fp32 buffers (raw device addresses)."""
         self.ctx.check(library().gtmoe_forward_device(self.handle, tokens, inputs_ptr, token_ids_ptr, outputs_ptr,
                                                        path, stream))
+
+    def forward_device_noalloc(self, tokens, inputs_ptr, outputs_ptr, token_ids_ptr=None, path=PATH_AUTO,
+                               stream=None):
+        """forward_device with its intermediates in the library's fixed
+        scratch area: the call allocates nothing (gtmoe.h)."""
+        self.ctx.check(library().gtmoe_forward_device_noalloc(self.handle, tokens, inputs_ptr, token_ids_ptr,
+                                                               outputs_ptr, path, stream))
 
     def last_routing(self):
         T = C.c_int32(0)

@@ -55,6 +55,8 @@ struct gtmoe_context {
     std::vector<TimingRecord> pending;
     std::vector<hipEvent_t> spare_events;
     std::map<std::string, std::pair<double, int>> totals;
+    void *scratch = nullptr;  // device address of the no-allocation forward's scratch area on this device
+    std::string scratch_error;
 };
 
 namespace {
@@ -777,6 +779,47 @@ int32_t capture(gtmoe_context *ctx, F &&record, gtmoe_graph *g)
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Scratch area of gtmoe_forward_device_noalloc: the intermediates of that
+// forward live here instead of in a layer's workspace.  Each GPU the library
+// runs on holds its own copy from the library's load until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory: the
+// device address on each GPU comes from hipGetSymbolAddress, queried once per
+// device with that device current, and only that address is ever handed to
+// kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[GTMOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+bool g_scratch_queried[kMaxScratchDevices] = {};
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+hipError_t g_scratch_status[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on `device`, which must be current; null
+// with `err` set when it cannot be had.
+void *scratch_address(int device, std::string &err)
+{
+    if (device < 0 || device >= kMaxScratchDevices) {
+        err = "device index beyond the scratch table";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_queried[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_status[device] = e;
+        g_scratch_ptr[device] = e == hipSuccess ? p : nullptr;
+        g_scratch_queried[device] = true;
+    }
+    if (!g_scratch_ptr[device]) err = std::string("hipGetSymbolAddress: ") + hipGetErrorString(g_scratch_status[device]);
+    return g_scratch_ptr[device];
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
@@ -1191,6 +1234,7 @@ int32_t gtmoe_open(int32_t device, gtmoe_context **out)
     if (hipSetDevice(device) != hipSuccess) return fail(nullptr, GTMOE_ERR_DEVICE, "hipSetDevice(%d) failed", device);
     gtmoe_context *ctx = new gtmoe_context;
     ctx->device = device;
+    ctx->scratch = scratch_address(device, ctx->scratch_error);
     if (prop.multiProcessorCount > 0) ctx->compute_units = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
@@ -1531,6 +1575,65 @@ int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs
     if (rc == GTMOE_OK) rc = ensure_workspace(L, tokens);
     if (rc != GTMOE_OK) return rc;
     return forward_device_run(L, tokens, inputs, token_ids, outputs, path, (hipStream_t)stream);
+}
+
+int32_t gtmoe_forward_device_noalloc(gtmoe_layer *L, int32_t tokens, const float *inputs, const int64_t *token_ids,
+                                     float *outputs, uint32_t flags, void *stream)
+{
+    int32_t rc = check_layer_call(L);
+    if (rc != GTMOE_OK) return rc;
+    gtmoe_context *ctx = L->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int path = 0;
+    rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
+    if (rc != GTMOE_OK) return rc;
+    if (!ctx->scratch)
+        return fail(ctx, GTMOE_ERR_DEVICE, "no scratch area on device %d (%s)", ctx->device,
+                    ctx->scratch_error.c_str());
+    const int T = tokens;
+    Workspace w{};
+    const size_t need = layout_workspace(L, T > 0 ? T : 1, false, nullptr, w);
+    if (need > (size_t)GTMOE_NOALLOC_SCRATCH_BYTES)
+        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                    "a forward of %d tokens on this layer needs %zu bytes of intermediates; the forward without "
+                    "allocation has %zu",
+                    T, need, (size_t)GTMOE_NOALLOC_SCRATCH_BYTES);
+    hipStream_t s = (hipStream_t)stream;
+    layout_workspace(L, T > 0 ? T : 1, false, (char *)ctx->scratch, w);
+    auto enqueue = [&]() -> int32_t {
+        // Padding columns of the activation rows are read (against zero
+        // weights) and never written; the area holds whatever the last call
+        // on this GPU left, so they are cleared here (fill kernels, no memset
+        // nodes under graph capture).
+        if (T > 0 && L->dp != L->d) {
+            RUN(ctx, s, "clear_scratch", launch_fill_i32(reinterpret_cast<int32_t *>(w.xf), T * L->dp, 0, s));
+            RUN(ctx, s, "clear_scratch", launch_fill_i32(reinterpret_cast<int32_t *>(w.xb), T * L->dp / 2, 0, s));
+        }
+        if (T > 0 && L->hp != L->h) {
+            const int P = T * (L->S + L->k);
+            RUN(ctx, s, "clear_scratch", launch_fill_i32(reinterpret_cast<int32_t *>(w.hidden32), P * L->hp, 0, s));
+            RUN(ctx, s, "clear_scratch",
+                launch_fill_i32(reinterpret_cast<int32_t *>(w.hidden16), P * L->hp / 2, 0, s));
+        }
+        return forward_device_run(L, T, inputs, token_ids, outputs, path, s);
+    };
+    // the layer's own workspace is left untouched; timing is off for the
+    // call (its events would be created on first use)
+    Workspace own = L->ws;
+    L->ws = w;
+    const bool timing = ctx->timing;
+    ctx->timing = false;
+    rc = enqueue();
+    ctx->timing = timing;
+    L->ws = own;
+    // the call's routing lives in the shared area, which the next call on
+    // this GPU overwrites: the layer keeps no state of it
+    L->last_T = -1;
+    L->relaunch_ready = false;
+    L->dispatch_pending = false;
+    L->load_on_host = false;
+    return rc;
 }
 
 int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen, double *gates, int32_t *load,

@@ -170,6 +170,27 @@ int32_t gtmoe_forward(gtmoe_layer *layer, int32_t tokens, const double *inputs, 
 int32_t gtmoe_forward_device(gtmoe_layer *layer, int32_t tokens, const float *inputs,
                              const int64_t *token_ids, float *outputs, uint32_t flags, void *stream);
 
+/* ---- a forward that allocates nothing -----------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  The forward of gtmoe_forward_device (same arguments,
+ * kernels and results), with every intermediate buffer taken from a fixed
+ * scratch area inside the library instead of the layer's workspace: the call
+ * allocates and frees nothing.  The area is GTMOE_NOALLOC_SCRATCH_BYTES on
+ * each GPU, held from the library's load until the process ends.  A call
+ * whose intermediates do not fit returns GTMOE_ERR_INVALID_ARGUMENT: a layer
+ * of d = 2048, h = 1024 and 1 + 4 experts per token fits 792 tokens, one of
+ * d = 1024, h = 2048 and 2 experts per token 1715.  Every call on
+ * one GPU shares that GPU's area and finds there what the last call left:
+ * calls enqueued on one stream are ordered, but calls that overlap in time on
+ * one GPU (other streams, other threads) race.  The call keeps no routing
+ * state on the layer: gtmoe_last_routing, gtmoe_last_expert_load and
+ * gtmoe_relaunch answer GTMOE_ERR_NOT_READY until the next forward of another
+ * kind, and per-kernel timing leaves its kernels out. */
+#define GTMOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int32_t gtmoe_forward_device_noalloc(gtmoe_layer *layer, int32_t tokens, const float *inputs,
+                                     const int64_t *token_ids, float *outputs, uint32_t flags, void *stream);
+
 /* The routing state of the last forward on this layer, any pointer may be
  * NULL: chosen T x k expert indices and gates T x k (lastChosenExperts,
  * lastGates), load E (lastExpertLoad), rows_for_expert T*k token indices with
