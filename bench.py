@@ -1,35 +1,45 @@
-"""Benchmark of the MoE layer forward on one MI355X.
+"""Benchmark of the MoE forward path on one MI355X.
 
-Default workload (the decode configuration the metric is quoted on): one MoE
-layer, d=1024, 16 routed experts, top-2, SwiGLU hidden 2048, Int8 expert
-weights (per-16 absmax/127 block scales), fp32 router, a batch of 32 tokens
-with N(0,1) activations resident in HBM; weights N(0, 0.02), seed 0.  A step
-is one layer forward (router, top-k, dispatch, gate/up, down, combine).
-Four copies of the layer's weights (4 x 126 MB) are used round-robin so the
-256 MB Infinity Cache cannot hold the weight set.
+Default workload (the largest configuration that fits one GPU): a stack of
+24 blocks x <- x + MoE(RMSNorm(x)), each MoE layer d=2048, 64 routed experts
+plus 1 shared expert, top-4, SwiGLU hidden 1024, FP4 expert weights (per-16
+absmax/6 fp32 block scales), fp32 router; a prefill chunk of 8192 tokens
+with N(0,1) activations resident in HBM; weights N(0, 0.02) from seeded
+generators (four distinct weight sets cycled over the 24 layers, every layer
+with its own resident copy, 7.4 GB).  A step is one pass of the 24-block
+stack over the chunk (RMSNorm, router, top-k, dispatch, gate/up, down,
+combine and residual per block).
 
-Other workloads (--workload): c2 with --tokens 1/8/32; c3 (FP4 prefill,
-d=1024, 64+1 experts, top-6, h=512, T=4096); c4 (Int8 prefill, d=2048, 128
-experts, top-8, h=768, T=16384, Zipf(1.2) router-bias skew); c5d / c5p (24
-blocks RMSNorm + MoE + residual, d=2048, 64+1 experts, top-4, h=1024, FP4,
-T=64 / T=8192; four distinct seeded weight sets cycled over the 24 layers,
-every layer with its own resident copy).
+`value` is tokens per second from the median of the per-step durations,
+each bracketed by a HIP event pair on the stream the kernels run on (the
+residual stream's reset before each step is outside the events).  The line
+also reports the mean over the same steps and the wall clock of all of them.
+
+`roofline` is for the dominant kernel (the MFMA grouped gate/up GEMM on the
+prefill path, the dequant-GEMV gate/up on the decode path): achieved =
+algorithmic FLOPs or bytes per launch / mean launch time, the mean taken by
+one HIP event pair around a burst of back-to-back relaunches of that kernel
+over every resident layer; `step_frac` is the whole step's algorithmic work
+over the step time against the same peak.  `traffic` is the HBM bytes per
+launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes for the same
+workload, read from profiles/traffic.json and reported only when the
+kernel sources it was measured on are the ones built now (null otherwise).
+
+`detail.workloads` repeats the measurement, without CPU baseline, for the
+other configurations: the decode chunk of the same stack (T=64), one Int8
+decode layer (d=1024, 16 experts, top-2, h=2048) at T=1, 8 and 32 with four
+weight copies used round-robin (504 MB, beyond the 256 MB Infinity Cache),
+one FP4 prefill layer (d=1024, 64+1 experts, top-6, h=512, T=4096) and one
+Int8 prefill layer with Zipf(1.2) router-bias skew (d=2048, 128 experts,
+top-8, h=768, T=16384).  --workload picks another headline; --no-detail
+skips the rest.
+
+`cpu_baseline` times the CPU restatement of the reference algorithm
+(oracle/, float64, the reference's SplitAcrossThreads policy) on a bounded
+sample of the headline workload's tokens, on all host cores and on one.
 
 --adapters R times a training step instead: forward and backward through
-the host API with rank-R adapters on every layer of the mixture.
-
-Prints one JSON line.  `value` comes from the timed steps (synchronised on
-both sides, no per-kernel events).  `roofline` is for the dominant kernel:
-HBM-bound gemv_gateup (decode) or MFMA-bound mfma_gateup (prefill); achieved
-= algorithmic bytes or FLOPs per launch / mean launch time, the mean taken by
-one HIP event pair (torch.cuda.Event on the stream the kernels run on) around
-a burst of back-to-back relaunches of that kernel over every resident layer
-copy, which keeps per-launch event skew out of the figure.  A further pass
-with an event pair around every kernel gives the per-kernel breakdown in
-`detail`.  `cpu_baseline` times the
-CPU restatement of the reference algorithm (oracle/, float64, the
-reference's SplitAcrossThreads policy) on a bounded sample of the same
-workload on the host cores."""
+the host API with rank-R adapters on every layer of the mixture."""
 from __future__ import annotations
 
 import argparse
@@ -76,10 +86,16 @@ def gateup_bytes(c, load, T):
     return active * 2 * expert_bytes(c, c["h"], c["d"]) + T * c["d"] * 4 + (int(load.sum()) + c["S"] * T) * c["h"] * 4
 
 
-def step_bytes(c, load, T):
-    active = int(np.count_nonzero(load)) + c["S"]
+def step_bytes(c, loads, T):
+    """Algorithmic HBM bytes of one step: per layer, the three matrices of
+    every expert with load > 0 plus the shared experts, the router, and the
+    token rows in and out (fp32)."""
     per_expert = 2 * expert_bytes(c, c["h"], c["d"]) + expert_bytes(c, c["d"], c["h"])
-    return active * per_expert + c["E"] * c["d"] * 4 + c["E"] * 8 + 2 * T * c["d"] * 4
+    total = 0
+    for load in loads:
+        active = int(np.count_nonzero(load)) + c["S"]
+        total += active * per_expert + c["E"] * c["d"] * 4 + c["E"] * 8 + 2 * T * c["d"] * 4
+    return total
 
 
 def gateup_flops(c, load, T):
@@ -93,12 +109,15 @@ def layer_flops(c, T):
 
 
 def make_specs(gt, c):
-    from tests.moe_fixtures import FLOAT32, FP4, INT8, make_moe, zipf_router_bias
+    """The workload's distinct weight sets, each expert drawn N(0, 0.02) from
+    its own seeded generator and encoded on a thread pool."""
+    from tests.moe_fixtures import FLOAT32, FP4, INT8, make_moe_parallel, zipf_router_bias
     prec = {"int8": INT8, "fp4": FP4, "fp32": FLOAT32}[c["prec"]]
     bias = zipf_router_bias(c["E"], 1.2, seed=c["seed"], scale=c["zipf"]) if "zipf" in c else None
     sets = c.get("sets", 1)
-    return [make_moe(gt.encode_rows, d=c["d"], h=c["h"], E=c["E"], k=c["k"], S=c["S"], precision=prec,
-                     router_precision=FLOAT32, seed=c["seed"] + 101 * i, router_bias=bias) for i in range(sets)]
+    return [make_moe_parallel(gt.encode_rows, d=c["d"], h=c["h"], E=c["E"], k=c["k"], S=c["S"], precision=prec,
+                              router_precision=FLOAT32, seed=c["seed"] + 101 * i, router_bias=bias,
+                              threads=min(16, host_cores())) for i in range(sets)]
 
 
 def host_cores():
@@ -108,38 +127,79 @@ def host_cores():
         return os.cpu_count() or 1
 
 
-def cpu_baseline(c, specs, budget_s):
-    """The CPU restatement of the reference forward on the host cores, timed
-    on a bounded sample of the workload's tokens."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_once(c, specs, budget_s, threads, tokens):
+    """The CPU restatement of the reference forward (float64, the
+    reference's SplitAcrossThreads policy over `threads` threads), timed on
+    `tokens` of the workload's tokens for about budget_s seconds."""
     import oracle
-    cores = host_cores()
-    tokens = min(c["T"], 32)
     x = np.random.default_rng(0).normal(size=(tokens, c["d"]))
     reps, t0 = 0, time.perf_counter()
     while True:
         if c["layers"] > 1:
             norms = [np.ones(c["d"])] * c["layers"]
             layers = [specs[i % len(specs)] for i in range(c["layers"])]
-            oracle.stack_forward(layers, norms, x, threads=cores)
+            oracle.stack_forward(layers, norms, x, threads=threads)
         else:
-            oracle.moe_forward(specs[0], x, threads=cores)
+            oracle.moe_forward(specs[0], x, threads=threads)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    what = f"{c['layers']}-layer stack" if c["layers"] > 1 else "layer"
-    return {"value": tokens * reps / el, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{reps} forwards of the {what} over {tokens} of the workload's tokens "
-                      f"(float64 restatement, SplitAcrossThreads over {cores} threads), {el:.1f} s"}
+    what = f"{c['layers']}-block stack" if c["layers"] > 1 else "layer"
+    return {"value": tokens * reps / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} forward(s) of the {what} over {tokens} of the workload's tokens "
+                      f"(float64 restatement, SplitAcrossThreads over {threads} thread(s)), {el:.1f} s"}
 
 
-def traffic_from_profiles(key):
+def cpu_baseline(c, specs, budget_s):
+    """All host cores, then one core (half the budget each), with the CPU model."""
+    cores = host_cores()
+    allc = cpu_baseline_once(c, specs, budget_s / 2, cores, min(c["T"], 32))
+    one = cpu_baseline_once(c, specs, budget_s / 2, 1, min(c["T"], 4 if c["layers"] > 1 else 8))
+    allc["cpu_model"] = cpu_model()
+    allc["one_core"] = one
+    return allc
+
+
+# the sources a kernel's measured traffic depends on
+TRAFFIC_SOURCES = {
+    "mfma_gateup": ["experts_mfma.hip", "common.h"],
+    "gemv_gateup": ["experts_gemv.hip", "common.h"],
+}
+
+
+def sources_digest(kernel):
+    import hashlib
+    h = hashlib.sha256()
+    for name in TRAFFIC_SOURCES[kernel]:
+        with open(os.path.join(ROOT, "gotransformers_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def traffic_from_profiles(kernel, key):
+    """HBM bytes per launch of `kernel` measured (rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes) on workload `key`, if it was measured on the kernel
+    sources built now; None otherwise."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         entry = json.load(f).get(key)
-    return None if entry is None else entry.get("bytes_per_launch")
+    if entry is None or entry.get("sources") != sources_digest(kernel):
+        return None
+    return entry.get("bytes_per_launch")
 
 
 def transposed_bytes(c, load, T):
@@ -235,15 +295,186 @@ def adapter_bench(args, c):
     print(json.dumps(line), flush=True)
 
 
+
+
+NAMES = {"c2": "C2 decode: MoE layer", "c3": "C3 prefill: MoE layer", "c4": "C4 skewed prefill: MoE layer",
+         "c5d": "C5 decode: 24-block stack", "c5p": "C5 prefill: 24-block stack"}
+
+
+def workload_name(key, c):
+    return (f"{NAMES[key]} d={c['d']} E={c['E']}+{c['S']} shared k={c['k']} h={c['h']} "
+            f"{c['prec']} experts, T={c['T']}")
+
+
+def build_layers(gt, ctx, c, specs):
+    n_obj = c["copies"] * c["layers"]
+    layers = [gt.MixtureOfExperts.from_spec(ctx, specs[i % len(specs)]) for i in range(n_obj)]
+    if c["layers"] > 1:
+        for m in layers:
+            m.set_norm_weights(np.ones(c["d"]))
+    return layers
+
+
+def measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=False, n_detail=20):
+    """One workload on resident layers: per-step event times, the dominant
+    kernel's relaunch burst and the per-kernel breakdown."""
+    T, d = c["T"], c["d"]
+    sptr = stream.cuda_stream
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x0 = torch.randn(T, d, generator=g, dtype=torch.float32).cuda()
+    x = x0.clone()
+    y = torch.empty(T, d, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    graphs = []
+    if graph:  # the step recorded once per weight copy and replayed as a HIP graph
+        if c["layers"] > 1:
+            graphs = [gt.Graph.capture_stack(layers, T, x.data_ptr(), path=gt.PATH_AUTO)]
+        else:
+            graphs = [gt.Graph.capture_forward(m, T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO)
+                      for m in layers]
+
+    def prepare(i):
+        if c["layers"] > 1:
+            x.copy_(x0)  # the stack updates x in place
+
+    def step(i):
+        if c["layers"] > 1:
+            if graphs:
+                graphs[0].launch(stream=sptr)
+            else:
+                gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
+        elif graphs:
+            graphs[i % c["copies"]].launch(stream=sptr)
+        else:
+            layers[i % c["copies"]].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            prepare(i)
+            step(i)
+        torch.cuda.synchronize()
+        path = layers[0].last_path
+        loads = [m.last_expert_load() for m in layers[:c["layers"]]]
+
+        # timed steps: an event pair on the kernels' stream around each step
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            prepare(i)
+            evs[i][0].record(stream)
+            step(i)
+            evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        step_ms = np.array([a.elapsed_time(b) for a, b in evs])
+
+        # the dominant kernel: a burst of relaunches of each layer's gate/up
+        # kernel of its last forward, rotating over every resident layer (so
+        # weight reads keep missing the Infinity Cache), one event pair
+        n_burst = max(len(layers), (200 if path == gt.PATH_FP32 else 20) // len(layers) * len(layers))
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for m in layers:
+            m.relaunch(gt.KERNEL_GATEUP, stream=sptr)
+        ev0.record(stream)
+        for i in range(n_burst):
+            layers[i % len(layers)].relaunch(gt.KERNEL_GATEUP, stream=sptr)
+        ev1.record(stream)
+        ev1.synchronize()
+        kmean_s = ev0.elapsed_time(ev1) / n_burst / 1e3
+
+        # per-kernel breakdown: the library's event pair around every kernel
+        ctx.timing(True)
+        ctx.timing_reset()
+        n_detail = min(steps, n_detail)
+        for i in range(n_detail):
+            prepare(i)
+            step(i)
+        times = ctx.timing_read()
+        ctx.timing(False)
+    for gr in graphs:
+        gr.destroy()
+
+    decode = path == gt.PATH_FP32
+    med_s = float(np.median(step_ms)) / 1e3
+    if decode:
+        kernel = "gemv_gateup"
+        per_launch = gateup_bytes(c, loads[0], T)
+        achieved = per_launch / kmean_s / 1e9
+        step_work = step_bytes(c, loads, T) * (1 if c["layers"] > 1 else 1)
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+        step_achieved = step_work / med_s / 1e9
+    else:
+        kernel = "mfma_gateup"
+        per_launch = gateup_flops(c, loads[0], T)
+        achieved = per_launch / kmean_s / 1e12
+        step_work = layer_flops(c, T) * c["layers"]
+        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / MFMA_BF16_PEAK_TFLOPS}
+        step_achieved = step_work / med_s / 1e12
+    roof.update({"traffic": traffic_from_profiles(kernel, f"{kernel}/{key}_t{T}"), "kernel": kernel,
+                 "algorithmic_per_launch": per_launch, "mean_launch_us": kmean_s * 1e6, "launches": n_burst,
+                 "step_achieved": step_achieved, "step_frac": step_achieved / roof["peak"],
+                 "step_algorithmic": step_work})
+    return {
+        "path": path, "decode": decode, "loads": loads, "ms_median": med_s * 1e3,
+        "ms_mean": float(step_ms.mean()), "ms_min": float(step_ms.min()), "ms_max": float(step_ms.max()),
+        "wall_ms": wall_ms, "value": T / med_s, "roofline": roof,
+        "kernel_ms_per_step": {k: v[0] / n_detail for k, v in sorted(times.items())},
+    }
+
+
+def summary(key, c, r):
+    roof = r["roofline"]
+    return {"workload": workload_name(key, c), "tokens_per_s": r["value"], "ms_per_step_median": r["ms_median"],
+            "ms_per_step_mean": r["ms_mean"], "path": "fp32 dequant-GEMV" if r["decode"] else "bf16 MFMA grouped GEMM",
+            "kernel": roof["kernel"], "kernel_us": roof["mean_launch_us"], "bound": roof["bound"],
+            "kernel_achieved": roof["achieved"], "kernel_frac": roof["frac"], "traffic": roof["traffic"],
+            "step_achieved": roof["step_achieved"], "step_frac": roof["step_frac"], "unit": roof["unit"],
+            "kernel_ms_per_step": r["kernel_ms_per_step"],
+            "active_experts_layer0": int(np.count_nonzero(r["loads"][0]))}
+
+
+def run_detail(gt, torch, ctx, stream, keys, shared, args):
+    """The other workloads, each on its own resident layers (the C5 decode
+    chunk reuses the stack of the C5 prefill headline when it was built)."""
+    out = []
+    for key, tokens in keys:
+        c = dict(WORKLOADS[key])
+        if tokens:
+            c["T"] = tokens
+        reuse = shared.get(c.get("seed"), None) if key in ("c5d", "c5p") else None
+        layers = reuse if reuse is not None else build_layers(gt, ctx, c, make_specs(gt, c))
+        steps = 50 if c["layers"] > 1 or c["T"] * c["k"] > 8 * c["E"] else 200
+        try:
+            r = measure(gt, torch, ctx, c, key, layers, steps, max(5, c["copies"]), stream)
+        finally:
+            if reuse is None:
+                for m in layers:
+                    m.destroy()
+        s = summary(key, c, r)
+        if key == "c4":
+            load = np.sort(r["loads"][0])[::-1]
+            s["realized_load_desc_first8"] = load[:8].tolist()
+            s["realized_load_median"] = int(np.median(load))
+            s["realized_load_min"] = int(load[-1])
+        out.append(s)
+        print(f"detail {key} T={c['T']}: {s['tokens_per_s']:.0f} tokens/s, {s['kernel']} "
+              f"{s['kernel_frac'] * 100:.1f}% of peak, step {s['step_frac'] * 100:.1f}%", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c5p", choices=sorted(WORKLOADS))
     ap.add_argument("--tokens", type=int, default=None)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-detail", action="store_true", help="measure the headline workload only")
     ap.add_argument("--graph", action="store_true", help="replay each step as a recorded HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (for PMC byte-counter calibration)")
@@ -259,7 +490,8 @@ def main():
     import torch
     import gotransformers_amd as gt
 
-    c = dict(WORKLOADS[args.workload])
+    key = args.workload
+    c = dict(WORKLOADS[key])
     if args.tokens:
         c["T"] = args.tokens
     if args.adapters:
@@ -269,158 +501,65 @@ def main():
         adapter_bench(args, c)
         return
     T, d = c["T"], c["d"]
-    prefill_like = T * c["k"] > 8 * c["E"]
-    steps = args.steps or (400 if not prefill_like and c["layers"] == 1 else 30 if c["layers"] == 1 else 10)
-    warmup = args.warmup if args.warmup is not None else max(3, steps // 10)
+    steps = args.steps or (200 if c["layers"] == 1 and T * c["k"] <= 8 * c["E"] else 50)
+    warmup = args.warmup if args.warmup is not None else max(3, min(10, steps // 10))
     warmup = max(warmup, c["copies"])  # every weight copy has run a forward before the relaunch burst
 
     specs = make_specs(gt, c)
     ctx = gt.Context(0)
-    n_obj = c["copies"] * c["layers"]
-    layers = [gt.MixtureOfExperts.from_spec(ctx, specs[i % len(specs)]) for i in range(n_obj)]
-    if c["layers"] > 1:
-        for m in layers:
-            m.set_norm_weights(np.ones(d))
-    g = torch.Generator(device="cpu").manual_seed(0)
-    x0 = torch.randn(T, d, generator=g, dtype=torch.float32).cuda()
-    x = x0.clone()
-    y = torch.empty(T, d, dtype=torch.float32, device="cuda")
-
-    # a stream of our own (default priority): its handle is non-null, so the
-    # library launches on it and torch events recorded on it bracket our kernels
+    # a stream of our own (default priority): the library launches on it and
+    # the events recorded on it bracket our kernels
     stream = torch.cuda.Stream()
-    sptr = stream.cuda_stream
-    torch.cuda.set_stream(stream)
-
-    graphs = []
-    if args.graph:  # the step recorded once per weight copy and replayed as a HIP graph
-        if c["layers"] > 1:
-            graphs = [gt.Graph.capture_stack(layers, T, x.data_ptr(), path=gt.PATH_AUTO)]
-        else:
-            graphs = [gt.Graph.capture_forward(m, T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO)
-                      for m in layers]
-
-    def step(i):
-        if c["layers"] > 1:
-            x.copy_(x0)
-            if graphs:
-                graphs[0].launch(stream=sptr)
-            else:
-                gt.stack_forward_device(layers, T, x.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
-        elif graphs:
-            graphs[i % c["copies"]].launch(stream=sptr)
-        else:
-            layers[i % c["copies"]].forward_device(T, x.data_ptr(), y.data_ptr(), path=gt.PATH_AUTO, stream=sptr)
-
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    path = layers[0].last_path
-    load = layers[0].last_expert_load()
-
-    # timed region: K steps bracketed by synchronisation (no per-kernel events)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(i)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_plain = (t1 - t0) * 1e3 / steps
-
-    # the dominant kernel: a burst of relaunches of the last forward's
-    # gate/up kernel on the same stream, rotating through every resident
-    # layer (so weight reads keep missing the Infinity Cache), bracketed by
-    # one HIP event pair
-    n_burst = max(len(layers), (200 if path == gt.PATH_FP32 else 20) // len(layers) * len(layers))
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for m in layers:
-        m.relaunch(gt.KERNEL_GATEUP, stream=sptr)
-    ev0.record(stream)
-    for i in range(n_burst):
-        layers[i % len(layers)].relaunch(gt.KERNEL_GATEUP, stream=sptr)
-    ev1.record(stream)
-    ev1.synchronize()
-    kmean_s = ev0.elapsed_time(ev1) / n_burst / 1e3
-    klaunch = n_burst
-
-    # per-kernel breakdown: event pairs around every kernel over a few steps
-    ctx.timing(True)
-    ctx.timing_reset()
-    n_detail = min(steps, 50)
-    torch.cuda.synchronize()
-    t2 = time.perf_counter()
-    for i in range(n_detail):
-        step(i)
-    torch.cuda.synchronize()
-    t3 = time.perf_counter()
-    times = ctx.timing_read()
-    ctx.timing(False)
-    ms_events = (t3 - t2) * 1e3 / n_detail
+    layers = build_layers(gt, ctx, c, specs)
+    r = measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=args.graph)
 
     if args.copy_calibration:
         a = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
         b.copy_(a)
         torch.cuda.synchronize()
+        del a, b
 
-    decode = path == gt.PATH_FP32
-    dominant = "gemv_gateup" if decode else "mfma_gateup"
-    key = f"{dominant}/{args.workload}_t{T}"
-    if decode:
-        per_launch = gateup_bytes(c, load, T)
-        achieved = per_launch / kmean_s / 1e9
-        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profiles(key)}
-    else:
-        per_launch = gateup_flops(c, load, T)
-        achieved = per_launch / kmean_s / 1e12
-        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic_from_profiles(key)}
-    roof.update({"kernel": dominant, "algorithmic_per_launch": per_launch, "mean_launch_us": kmean_s * 1e6,
-                 "launches": klaunch})
-
-    for g in graphs:
-        g.destroy()
+    detail_workloads = []
+    if not args.no_detail:
+        plan = [("c5d", None), ("c5p", None), ("c2", 1), ("c2", 8), ("c2", 32), ("c3", None), ("c4", None)]
+        plan = [(k, t) for k, t in plan if not (k == key and (t or WORKLOADS[k]["T"]) == T)]
+        shared = {c["seed"]: layers} if key in ("c5d", "c5p") else {}
+        detail_workloads = run_detail(gt, torch, ctx, stream, plan, shared, args)
     for m in layers:
         m.destroy()
     ctx.close()
 
     cpu = None if args.no_cpu else cpu_baseline(c, specs, args.cpu_seconds)
 
-    names = {"c2": "C2 decode: MoE layer", "c3": "C3 prefill: MoE layer", "c4": "C4 skewed prefill: MoE layer",
-             "c5d": "C5 decode: 24-block stack", "c5p": "C5 prefill: 24-block stack"}
-    workload = (f"{names[args.workload]} d={d} E={c['E']}+{c['S']} shared k={c['k']} h={c['h']} "
-                f"{c['prec']} experts, T={T}")
-    step_layers = c["layers"]
+    decode = r["decode"]
     line = {
         "metric": METRIC,
-        "value": T / (ms_plain / 1e3),
+        "value": r["value"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": ms_plain,
+        "ms_per_step": r["ms_median"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if decode else "bf16",
         "data": "synthetic",
-        "config": {"workload": workload, "tokens": T, "d_model": d, "routed_experts": c["E"],
+        "config": {"workload": workload_name(key, c), "tokens": T, "d_model": d, "routed_experts": c["E"],
                    "shared_experts": c["S"], "top_k": c["k"], "expert_hidden": c["h"],
-                   "expert_weights": f"{c['prec']} per-16 fp32 scales", "layers_per_step": step_layers,
+                   "expert_weights": f"{c['prec']} per-16 fp32 scales", "layers_per_step": c["layers"],
                    "weight_copies": c["copies"],
                    "path": "fp32 dequant-GEMV" if decode else "bf16 MFMA grouped GEMM",
-                   "hip_graph": bool(graphs)},
-        "roofline": roof,
+                   "hip_graph": bool(args.graph), "step_timing": "median of per-step HIP event pairs"},
+        "roofline": r["roofline"],
         "cpu_baseline": cpu,
         "detail": {
-            "ms_per_step_with_kernel_events": ms_events,
-            "kernel_ms_per_step_events": {k: v[0] / n_detail for k, v in sorted(times.items())},
-            "active_experts_layer0": int(np.count_nonzero(load)),
-            "step_algorithmic_bytes": step_bytes(c, load, T) * step_layers,
-            "step_hbm_frac": step_bytes(c, load, T) * step_layers / (ms_plain / 1e3) / 1e9 / HBM_PEAK_GBS,
-            "step_flops": layer_flops(c, T) * step_layers,
-            "step_mfma_frac": layer_flops(c, T) * step_layers / (ms_plain / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "ms_per_step_mean": r["ms_mean"], "ms_per_step_min": r["ms_min"], "ms_per_step_max": r["ms_max"],
+            "wall_ms_per_step": r["wall_ms"],
+            "kernel_ms_per_step_events": r["kernel_ms_per_step"],
+            "active_experts_layer0": int(np.count_nonzero(r["loads"][0])),
+            "workloads": detail_workloads,
         },
     }
     print(json.dumps(line), flush=True)

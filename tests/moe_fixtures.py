@@ -49,3 +49,22 @@ def zipf_router_bias(E, s, seed, scale=1.0):
     bias = np.empty(E)
     bias[perm] = scale * np.log(p / p[0])
     return bias
+
+
+def make_moe_parallel(encode, *, d, h, E, k, S=0, precision=INT8, router_precision=FLOAT32, seed=0, std=0.02,
+                      router_std=0.02, router_bias=None, threads=16):
+    """A layer like make_moe's (weights N(0, std), biases 0), with every
+    expert drawn from its own generator (SeedSequence(seed).spawn) so that
+    the experts are drawn and encoded on a thread pool: for the
+    configuration-sized layers (hundreds of millions of weights)."""
+    from concurrent.futures import ThreadPoolExecutor
+    seqs = np.random.SeedSequence(seed).spawn(S + E + 1)
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as pool:
+        experts = list(pool.map(lambda q: make_expert(encode, precision, d, h, np.random.default_rng(q), std),
+                                seqs[:S + E]))
+    router = make_layer(encode, router_precision, E, d, np.random.default_rng(seqs[S + E]), router_std, 0.0, LINEAR)
+    if router_bias is not None:
+        router.biases = np.asarray(router_bias, np.float64)
+    return SimpleNamespace(vector_size=d, hidden_size=h, experts_per_token=k, use_hash_routing=False,
+                           shared=experts[:S], routed=experts[S:], router=router, balance_biases=np.zeros(E),
+                           precision=precision, clamp_limit=0.0)
