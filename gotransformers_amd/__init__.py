@@ -28,7 +28,7 @@ ROLES = {("shared", "gate"): 1, ("shared", "up"): 2, ("shared", "down"): 3,
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOT_READY, ERR_OUT_OF_MEMORY = range(6)
 
 EXPORTED = [
-    "gtmoe_abi_version", "gtmoe_device_count", "gtmoe_open", "gtmoe_close", "gtmoe_last_error",
+    "gtmoe_abi_version", "gtmoe_device_count", "gtmoe_open", "gtmoe_close", "gtmoe_last_error", "gtmoe_test_inject_failure",
     "gtmoe_encode_rows", "gtmoe_layer_create", "gtmoe_layer_destroy", "gtmoe_upload_rows",
     "gtmoe_set_balance_biases", "gtmoe_get_balance_biases", "gtmoe_set_norm_weights", "gtmoe_forward",
     "gtmoe_forward_device", "gtmoe_forward_device_noalloc", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
@@ -75,7 +75,10 @@ def library():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() or gotransformers_amd/build.py")
-    L = C.CDLL(LIB_PATH)
+    try:
+        L = C.CDLL(LIB_PATH)
+    except OSError as e:
+        raise ImportError(f"cannot load {LIB_PATH}: {e}") from e
     P, i32, u32, dbl = C.c_void_p, C.c_int32, C.c_uint32, C.c_double
     sig = {
         "gtmoe_abi_version": ([], i32),
@@ -83,6 +86,7 @@ def library():
         "gtmoe_open": ([i32, P], i32),
         "gtmoe_close": ([P], i32),
         "gtmoe_last_error": ([P], C.c_char_p),
+        "gtmoe_test_inject_failure": ([C.c_char_p, i32], i32),
         "gtmoe_encode_rows": ([i32, i32, i32, P, P, P], i32),
         "gtmoe_layer_create": ([P, C.POINTER(LayerDesc), P], i32),
         "gtmoe_layer_destroy": ([P], i32),
@@ -146,6 +150,12 @@ def _check(code, ctx_handle=None):
     if code == ERR_INVALID_ARGUMENT:
         raise InvalidArgument(code, msg)
     raise GtmoeError(code, msg)
+
+
+def inject_failure(entry_point, status):
+    """Test hook: the next call of `entry_point` on this thread answers
+    `status` instead of running (gtmoe_test_inject_failure)."""
+    _check(library().gtmoe_test_inject_failure(entry_point.encode(), status))
 
 
 def device_count():

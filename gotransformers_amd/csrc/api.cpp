@@ -55,6 +55,7 @@ struct gtmoe_context {
     std::vector<TimingRecord> pending;
     std::vector<hipEvent_t> spare_events;
     std::map<std::string, std::pair<double, int>> totals;
+    bool closed = false;      // gtmoe_close ran: the handle stays readable, every call answers an error
     void *scratch = nullptr;  // device address of the no-allocation forward's scratch area on this device
     std::string scratch_error;
 };
@@ -121,6 +122,33 @@ int32_t run(gtmoe_context *ctx, hipStream_t s, const char *name, F &&fn)
         int32_t rc_ = run((ctx), (s), (name), [&]() { return (expr); }); \
         if (rc_ != GTMOE_OK) return rc_;                             \
     } while (0)
+
+// One failure armed by gtmoe_test_inject_failure on this thread: the next
+// call of the named entry point answers `status` instead of running.
+thread_local std::string g_inject_entry;
+thread_local int32_t g_inject_status = GTMOE_OK;
+
+bool take_injection(const char *entry, int32_t *status)
+{
+    if (g_inject_status == GTMOE_OK || g_inject_entry != entry) return false;
+    *status = g_inject_status;
+    g_inject_status = GTMOE_OK;
+    g_inject_entry.clear();
+    return true;
+}
+
+// Entry into a call on a context: its lock, then the refusals every call
+// shares (a closed context, an injected failure), then its device current.
+#define ENTER_NODEV(c)                                                                                     \
+    std::lock_guard<std::recursive_mutex> lock_((c)->mu);                                                  \
+    do {                                                                                                   \
+        if ((c)->closed) return fail((c), GTMOE_ERR_INVALID_ARGUMENT, "the context is closed");           \
+        int32_t inj_ = GTMOE_OK;                                                                           \
+        if (take_injection(__func__, &inj_)) return fail((c), inj_, "injected failure in %s", __func__);  \
+    } while (0)
+#define ENTER(c)      \
+    ENTER_NODEV(c);   \
+    HIP_TRY((c), hipSetDevice((c)->device))
 
 }  // namespace
 
@@ -1221,6 +1249,8 @@ int32_t gtmoe_open(int32_t device, gtmoe_context **out)
 {
     if (!out) return fail(nullptr, GTMOE_ERR_INVALID_ARGUMENT, "out is null");
     *out = nullptr;
+    int32_t injected = GTMOE_OK;
+    if (take_injection(__func__, &injected)) return fail(nullptr, injected, "injected failure in %s", __func__);
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n == 0) return fail(nullptr, GTMOE_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
@@ -1247,18 +1277,22 @@ int32_t gtmoe_open(int32_t device, gtmoe_context **out)
 int32_t gtmoe_close(gtmoe_context *ctx)
 {
     if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
-    {
-        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-        (void)hipSetDevice(ctx->device);
-        (void)hipStreamSynchronize(ctx->stream);
-        for (auto &r : ctx->pending) {
-            (void)hipEventDestroy(r.start);
-            (void)hipEventDestroy(r.stop);
-        }
-        for (auto e : ctx->spare_events) (void)hipEventDestroy(e);
-        (void)hipStreamDestroy(ctx->stream);
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    if (ctx->closed) return GTMOE_OK;  // closing twice does nothing (gpu/gpu_test.go:145-154)
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    for (auto &r : ctx->pending) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
     }
-    delete ctx;
+    ctx->pending.clear();
+    for (auto e : ctx->spare_events) (void)hipEventDestroy(e);
+    ctx->spare_events.clear();
+    (void)hipStreamDestroy(ctx->stream);
+    ctx->stream = nullptr;
+    // The handle is not freed: a closed context keeps answering, as a closed
+    // gpu.Device does (gpu/device.go:729-731), with an error instead of work.
+    ctx->closed = true;
     return GTMOE_OK;
 }
 
@@ -1267,11 +1301,19 @@ const char *gtmoe_last_error(const gtmoe_context *ctx)
     return ctx ? ctx->error.c_str() : g_open_error.c_str();
 }
 
+int32_t gtmoe_test_inject_failure(const char *entry_point, int32_t status)
+{
+    if (!entry_point || status < GTMOE_OK || status > GTMOE_ERR_OUT_OF_MEMORY) return GTMOE_ERR_INVALID_ARGUMENT;
+    g_inject_entry = entry_point;
+    g_inject_status = status;
+    return GTMOE_OK;
+}
+
 int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtmoe_layer **out)
 {
     if (!ctx || !desc || !out) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     *out = nullptr;
+    ENTER(ctx);
     const gtmoe_layer_desc &D = *desc;
     // buildMixtureOfExperts checks (mixtureofexperts.go:47-56) and NewLayer's
     if (D.shared_experts < 0)
@@ -1364,8 +1406,7 @@ int32_t gtmoe_upload_rows(gtmoe_layer *L, int32_t role, int32_t index, const gtm
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (!biases) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "biases are null");
     if (role < GTMOE_ROLE_ROUTER || role > GTMOE_ROLE_ROUTED_DOWN)
         return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown role %d", role);
@@ -1427,8 +1468,7 @@ int32_t gtmoe_set_balance_biases(gtmoe_layer *L, const double *biases)
 {
     if (!L || !biases) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     L->balance_host.assign(biases, biases + L->E);
     HIP_TRY(ctx, hipMemcpy(L->balance, biases, sizeof(double) * L->E, hipMemcpyHostToDevice));
     return GTMOE_OK;
@@ -1445,8 +1485,7 @@ int32_t gtmoe_set_norm_weights(gtmoe_layer *L, const double *weights)
 {
     if (!L || !weights) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     std::vector<float> w(weights, weights + L->d);
     HIP_TRY(ctx, hipMemcpy(L->norm_w, w.data(), sizeof(float) * L->d, hipMemcpyHostToDevice));
     L->norm_host.swap(w);
@@ -1460,8 +1499,7 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     int32_t rc = check_layer_call(L);
     if (rc != GTMOE_OK) return rc;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     const int T = tokens;
     if (T < 0) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "negative number of tokens");
     if (T > 0 && (!inputs || !outputs)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "inputs or outputs are null");
@@ -1568,8 +1606,7 @@ int32_t gtmoe_forward_device(gtmoe_layer *L, int32_t tokens, const float *inputs
     int32_t rc = check_layer_call(L);
     if (rc != GTMOE_OK) return rc;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     int path = 0;
     rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
     if (rc == GTMOE_OK) rc = ensure_workspace(L, tokens);
@@ -1583,8 +1620,7 @@ int32_t gtmoe_forward_device_noalloc(gtmoe_layer *L, int32_t tokens, const float
     int32_t rc = check_layer_call(L);
     if (rc != GTMOE_OK) return rc;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     int path = 0;
     rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
     if (rc != GTMOE_OK) return rc;
@@ -1641,8 +1677,7 @@ int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen,
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (L->last_T < 0) return fail(ctx, GTMOE_ERR_NOT_READY, "call Forward before reading its routing");
     const int T = L->last_T;
     if (tokens_out) *tokens_out = T;
@@ -1668,8 +1703,7 @@ int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen,
 int32_t gtmoe_last_expert_load(gtmoe_layer *L, int32_t *load)
 {
     if (!L || !load) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(L->ctx->mu);
-    HIP_TRY(L->ctx, hipSetDevice(L->ctx->device));
+    ENTER(L->ctx);
     int32_t rc = fetch_load(L);
     if (rc != GTMOE_OK) return rc;
     memcpy(load, L->last_load.data(), sizeof(int32_t) * L->E);
@@ -1680,8 +1714,7 @@ int32_t gtmoe_update_balance(gtmoe_layer *L, double rate)
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     // mixtureofexperts.go:293-310
     if (L->last_T < 0 || L->desc.use_hash_routing) return GTMOE_OK;
     int32_t rc = fetch_load(L);
@@ -1702,8 +1735,7 @@ int32_t gtmoe_route_from_logits(gtmoe_layer *L, int32_t tokens, const double *lo
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     const int T = tokens;
     if (T < 0 || (T > 0 && !logits)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "bad logits");
     int32_t rc = ensure_workspace(L, T);
@@ -1789,8 +1821,7 @@ int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_
     gtmoe_context *ctx = nullptr;
     int32_t rc = stack_common(layers, n_layers, tokens, &ctx);
     if (rc != GTMOE_OK) return rc;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     const int T = tokens;
     if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
     if (T > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
@@ -1847,8 +1878,7 @@ int32_t gtmoe_stack_forward_device(gtmoe_layer *const *layers, int32_t n_layers,
     gtmoe_context *ctx = nullptr;
     int32_t rc = stack_common(layers, n_layers, tokens, &ctx);
     if (rc != GTMOE_OK) return rc;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
     if (tokens > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
     for (int l = 0; l < n_layers; ++l)
@@ -1865,8 +1895,7 @@ int32_t gtmoe_graph_capture_forward(gtmoe_layer *L, int32_t tokens, const float 
     int32_t rc = check_layer_call(L);
     if (rc != GTMOE_OK) return rc;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     int path = 0;
     rc = check_forward_device(L, tokens, inputs, token_ids, outputs, flags, &path);
     if (rc == GTMOE_OK) rc = ensure_workspace(L, tokens);
@@ -1895,8 +1924,7 @@ int32_t gtmoe_graph_capture_stack(gtmoe_layer *const *layers, int32_t n_layers, 
     gtmoe_context *ctx = nullptr;
     int32_t rc = stack_common(layers, n_layers, tokens, &ctx);
     if (rc != GTMOE_OK) return rc;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (flags > GTMOE_PATH_BF16) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown flags %u", flags);
     if (tokens > 0 && !x) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "x is null");
     gtmoe_graph *g = new gtmoe_graph;
@@ -1930,8 +1958,7 @@ int32_t gtmoe_graph_launch(gtmoe_graph *g, void *stream)
 {
     if (!g || !g->exec) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = g->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     hipStream_t s = (hipStream_t)stream;
     HIP_TRY(ctx, hipGraphLaunch(g->exec, s));
     for (size_t i = 0; i < g->layers.size(); ++i) {
@@ -1956,7 +1983,7 @@ int32_t gtmoe_graph_destroy(gtmoe_graph *g)
 int32_t gtmoe_timing_enable(gtmoe_context *ctx, int32_t enabled)
 {
     if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    ENTER_NODEV(ctx);
     ctx->timing = enabled != 0;
     return GTMOE_OK;
 }
@@ -1983,7 +2010,7 @@ static int32_t collect_timing(gtmoe_context *ctx)
 int32_t gtmoe_timing_reset(gtmoe_context *ctx)
 {
     if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    ENTER_NODEV(ctx);
     int32_t rc = collect_timing(ctx);
     ctx->totals.clear();
     return rc;
@@ -1993,7 +2020,7 @@ int32_t gtmoe_timing_read(gtmoe_context *ctx, int32_t capacity, char *names, dou
                           int32_t *count)
 {
     if (!ctx || !count) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    ENTER_NODEV(ctx);
     int32_t rc = collect_timing(ctx);
     if (rc != GTMOE_OK) return rc;
     int i = 0;
@@ -2016,8 +2043,7 @@ int32_t gtmoe_relaunch(gtmoe_layer *L, int32_t kernel, void *stream)
 {
     if (!L || (kernel != GTMOE_KERNEL_GATEUP && kernel != GTMOE_KERNEL_DOWN)) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (L->last_T <= 0 || !L->relaunch_ready)
         return fail(ctx, GTMOE_ERR_NOT_READY, "no forward with tokens to launch again");
     hipStream_t s = (hipStream_t)stream;
@@ -2047,7 +2073,7 @@ int32_t gtmoe_layer_load_weights(gtmoe_layer *L, gtmoe_weights_file *f, const ch
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    ENTER(ctx);
     if (!f || !name) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "weights file or layer name is null");
 
     // MixtureOfExperts.Parameters order (mixtureofexperts.go:312-324):
@@ -2191,8 +2217,7 @@ int32_t gtmoe_layer_add_adapters(gtmoe_layer *L, int32_t rank, double alpha, uin
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (rank < 1)
         return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "Model.AddLowRankAdapters: rank must be at least 1, got %d", rank);
     if (L->has_adapters)
@@ -2219,8 +2244,7 @@ int32_t gtmoe_layer_remove_adapters(gtmoe_layer *L)
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     free_adapters(L);
     return GTMOE_OK;
@@ -2229,7 +2253,7 @@ int32_t gtmoe_layer_remove_adapters(gtmoe_layer *L)
 int32_t gtmoe_layer_adapter_rank(gtmoe_layer *L, int32_t role, int32_t index, int32_t *rank)
 {
     if (!L || !rank) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(L->ctx->mu);
+    ENTER_NODEV(L->ctx);
     int g = 0;
     const AdapterSet *a = adapter_of(L, role, index, &g);
     if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
@@ -2241,8 +2265,7 @@ int32_t gtmoe_layer_set_adapter(gtmoe_layer *L, int32_t role, int32_t index, con
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     int g = 0;
     AdapterSet *a = adapter_of(L, role, index, &g);
     if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
@@ -2267,8 +2290,7 @@ int32_t gtmoe_layer_get_adapter(gtmoe_layer *L, int32_t role, int32_t index, dou
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     int g = 0;
     AdapterSet *a = adapter_of(L, role, index, &g);
     if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
@@ -2294,8 +2316,7 @@ int32_t gtmoe_layer_adapter_gradients(gtmoe_layer *L, int32_t role, int32_t inde
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     int g = 0;
     AdapterSet *a = adapter_of(L, role, index, &g);
     if (!a) return L->has_adapters ? GTMOE_ERR_INVALID_ARGUMENT : GTMOE_ERR_NOT_READY;
@@ -2317,8 +2338,7 @@ int32_t gtmoe_layer_zero_adapter_gradients(gtmoe_layer *L)
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (!L->has_adapters) return fail(ctx, GTMOE_ERR_NOT_READY, "the layer has no low-rank adapters");
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     for (AdapterSet *a : {&L->ad_gate, &L->ad_up, &L->ad_down, &L->ad_router}) {
@@ -2334,8 +2354,7 @@ int32_t gtmoe_backward(gtmoe_layer *L, int32_t tokens, const double *output_grad
     int32_t rc = check_layer_call(L);
     if (rc != GTMOE_OK) return rc;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    ENTER(ctx);
     if (!L->has_adapters)
         return fail(ctx, GTMOE_ERR_UNSUPPORTED,
                     "mixture of experts: weights are compressed for running the model, call DecompressWeights before "

@@ -327,7 +327,7 @@ int32_t gtmoe_weights_file_values(gtmoe_weights_file *f, int32_t index, double *
     if ((int64_t)v.size() != count)
         return file_fail(f, "parameter \"%s\" holds %llu values, not %lld", e.name.c_str(),
                          (unsigned long long)v.size(), (long long)count);
-    memcpy(out, v.data(), v.size() * sizeof(double));
+    if (!v.empty()) memcpy(out, v.data(), v.size() * sizeof(double));
     return GTMOE_OK;
 }
 

@@ -103,7 +103,16 @@ typedef struct gtmoe_rows {
 
 /* ---- library and context -------------------------------------------------
  * gtmoe_open replaces the device bring-up of gpu.Open/openDevice
- * (gpu/device.go:90-130); gtmoe_close replaces Device.Close. */
+ * (gpu/device.go:90-130); without a gfx950 device it fails (GTMOE_ERR_DEVICE
+ * or GTMOE_ERR_UNSUPPORTED, text in gtmoe_last_error(NULL)) and the caller
+ * answers on the CPU.  gtmoe_close replaces Device.Close: it waits for the
+ * device and releases the context's stream and events, but the handle stays
+ * readable, as a closed gpu.Device does (gpu/device.go:729-731,
+ * gpu/gpu_test.go:145-154): a second gtmoe_close does nothing, any other call
+ * on the context or its layers answers GTMOE_ERR_INVALID_ARGUMENT with "the
+ * context is closed" in gtmoe_last_error, and gtmoe_layer_destroy still frees
+ * a layer.  A closed context's own few hundred bytes stay allocated until the
+ * process ends. */
 int32_t gtmoe_abi_version(void);
 int32_t gtmoe_device_count(int32_t *count);
 int32_t gtmoe_open(int32_t device, gtmoe_context **out);
@@ -111,6 +120,14 @@ int32_t gtmoe_close(gtmoe_context *ctx);
 /* Text of the last failure on this context (Device.LastError,
  * gpu/device.go:749-753).  With ctx NULL: the last failure of gtmoe_open. */
 const char *gtmoe_last_error(const gtmoe_context *ctx);
+
+/* Test hook, no counterpart in the reference: the next call of the entry
+ * point named `entry_point` (e.g. "gtmoe_forward") made on this thread
+ * answers `status` with the text "injected failure in <entry point>" instead
+ * of running, as a failing HIP call would; later calls run normally.  For
+ * testing a caller's fallback (the CPU answer and lastError of
+ * gpu/device.go:733-737).  Armed per thread; one failure at a time. */
+int32_t gtmoe_test_inject_failure(const char *entry_point, int32_t status);
 
 /* ---- quantization ---------------------------------------------------------
  * Rows.Append over `rows` rows of float64 values (lowprecision/rows.go:38-79,
