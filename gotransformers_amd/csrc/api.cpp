@@ -178,6 +178,7 @@ struct Workspace {
     uint16_t *hidden16 = nullptr;  // [P][hp] bf16
     float *slot_out = nullptr;    // [P][d] fp32 (fp32 path) or bf16 (MFMA path)
     int32_t *chunk_cnt = nullptr;  // [chunks][E] scratch of the many-token dispatch
+    float *inv = nullptr;          // [T] inverse RMS of rows the previous stack layer's combine normalised
 };
 
 // Low-rank adapters of one weight role over all groups (G = S + E), or of
@@ -357,7 +358,8 @@ double decoded_value(const gtmoe_rows *r, int row, int i)
 // The buffers of a forward for `cap` tokens laid out from `base` (256-byte
 // aligned parts); returns the bytes they take.  With base null only the size
 // is computed.  Without host staging the float64 rows of the host-API calls
-// and the residual of a host-API stack are left out (device forwards only).
+// and the stack-only buffers (a host-API stack's residual, the rows' inverse
+// RMS) are left out (single-layer device forwards only).
 size_t layout_workspace(const gtmoe_layer *L, int cap, bool host_staging, char *base, Workspace &w)
 {
     const size_t P = (size_t)cap * (L->S + L->k);
@@ -380,6 +382,7 @@ size_t layout_workspace(const gtmoe_layer *L, int cap, bool host_staging, char *
         {(void **)&w.tok, P * 4},                       {(void **)&w.hidden32, P * L->hp * 4},
         {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
         {(void **)&w.chunk_cnt, (size_t)dispatch_chunks(cap) * L->E * 4},
+        {(void **)&w.inv, hs * cap * 4},
     };
     size_t off = 0;
     for (const Part &p : parts) {
@@ -466,7 +469,7 @@ struct PendingCombine {
 // Otherwise: convert or RMSNorm into ws.xf / ws.xb, router and top-k (or hash
 // routing), then the dispatch.  token_ids: device pointer (hash routing).
 int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t *token_ids, int path, hipStream_t s,
-                          float *zero_out = nullptr, const PendingCombine *pend = nullptr)
+                          float *zero_out = nullptr, const PendingCombine *pend = nullptr, bool prenormed = false)
 {
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
@@ -532,6 +535,24 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
             launch_combine(T, pend->d, pend->S, pend->k, pend->slot, false, pend->pos, pend->gates,
                            (const float *)in.x, (float *)in.x, nullptr, s));
     if (zero_out) RUN(ctx, s, "zero_out", launch_fill_i32(reinterpret_cast<int32_t *>(zero_out), T * L->d, 0, s));
+    if (prenormed) {
+        // the previous layer's combine wrote the bf16 normalised rows and each
+        // row's inverse RMS; the router reads the raw rows (stride d == dp)
+        // against its rows times the norm weights
+        if (!hash) {
+            RUN(ctx, s, "router",
+                launch_router((const float *)in.x, L->d, T, L->d, L->router_wn, L->dp, L->router_b, L->E, w.logits,
+                              s, w.inv));
+            RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
+        } else {
+            RUN(ctx, s, "hash_route",
+                launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
+        }
+        RUN(ctx, s, "dispatch",
+            launch_dispatch(w.chosen, T, L->k, L->E, L->S, bm, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
+                            w.tile_off, w.tile_desc, w.chunk_cnt, s));
+        return GTMOE_OK;
+    }
     if (in.norm) {
         RUN(ctx, s, "rmsnorm", launch_rmsnorm((const float *)in.x, T, L->d, L->norm_w, xf, L->dp, xb, L->dp, s));
     } else if (in.f64) {
@@ -1782,6 +1803,7 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
     gtmoe_context *ctx = layers[0]->ctx;
     PendingCombine pending{};
     bool have_pending = false;
+    bool prenormed = false;  // this layer's norm was done by the previous layer's combine
     for (int l = 0; l < n_layers; ++l) {
         gtmoe_layer *L = layers[l];
         const int path = choose_path(L, T, flags);
@@ -1794,17 +1816,33 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
             continue;
         }
         Workspace &w = L->ws;
-        rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s, nullptr, have_pending ? &pending : nullptr);
+        rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s, nullptr, have_pending ? &pending : nullptr,
+                               prenormed);
         have_pending = false;
+        prenormed = false;
         if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
         if (rc != GTMOE_OK) return rc;
         const int32_t *pos = L->skipped_dispatch ? nullptr : w.pos;
+        gtmoe_layer *N = l + 1 < n_layers ? layers[l + 1] : nullptr;
         // on the fp32 path the next layer's routing kernel, which reads x
         // anyway, does this layer's combine (one launch fewer per layer)
-        if (l + 1 < n_layers && path == GTMOE_PATH_FP32 &&
-            fused_route_fits(T, layers[l + 1]->k, layers[l + 1]->dp)) {
+        if (N && path == GTMOE_PATH_FP32 && fused_route_fits(T, N->k, N->dp)) {
             pending = PendingCombine{w.slot_out, pos, w.gates32, L->S, L->k, L->d};
             have_pending = true;
+        } else if (N && path == GTMOE_PATH_BF16 && choose_path(N, T, flags) == GTMOE_PATH_BF16 &&
+                   !fused_route_fits(T, N->k, N->dp) && N->d == N->dp && combine_norm_fits(L->d, true)) {
+            // on the bf16 path the combine, which holds whole rows, also does
+            // the next layer's RMSNorm: its bf16 rows and inverse RMS
+            rc = ensure_workspace(N, T);
+            if (rc != GTMOE_OK) return rc;
+            CombineNorm cn;
+            cn.w = N->norm_w;
+            cn.xb = N->ws.xb;
+            cn.ldb = N->dp;
+            cn.inv = N->ws.inv;
+            RUN(ctx, s, "combine_norm",
+                launch_combine(T, L->d, L->S, L->k, w.slot_out, true, pos, w.gates32, x, x, nullptr, s, cn));
+            prenormed = true;
         } else {
             RUN(ctx, s, "combine",
                 launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, pos, w.gates32, x, x, nullptr,

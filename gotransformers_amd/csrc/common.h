@@ -205,8 +205,10 @@ hipError_t launch_convert_inputs_f32(const float *x, int T, int d, float *xf, in
                                      hipStream_t s);
 hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *xf, int ldf, uint16_t *xb, int ldb,
                           hipStream_t s);
+// row_scale (optional, [T]): each row's logits are scale * dot + bias (the
+// inverse RMS of a row whose norm weights are folded into w).
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
-                         double *logits, hipStream_t s);
+                         double *logits, hipStream_t s, const float *row_scale = nullptr);
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
                        double *gates, float *gates32, hipStream_t s);
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,
@@ -225,8 +227,19 @@ hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hi
 hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 hipError_t launch_mfma_down(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 int mfma_tile_m();
+// The next stack layer's RMSNorm done by the combine (bf16 slot rows, d <=
+// 2048, d % 8 == 0, with a residual, fp32 output of stride d): w its norm
+// weights [d], xb its bf16 rows [T][ldb], inv the rows' inverse RMS [T].
+struct CombineNorm {
+    const float *w = nullptr;
+    uint16_t *xb = nullptr;
+    int ldb = 0;
+    float *inv = nullptr;
+};
+bool combine_norm_fits(int d, bool slot_bf16);
 hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool slot_bf16, const int32_t *pos,
-                          const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s);
+                          const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s,
+                          const CombineNorm &norm = CombineNorm{});
 hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s);
 hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);
 

@@ -170,15 +170,81 @@ __device__ __forceinline__ float load1(const uint16_t *p) { return __uint_as_flo
 // bf16: 16-byte loads); the routed rows (KB >= k of them, rows past k re-read
 // row 0 and are not added) are requested before the adds, which keep the
 // reference's order.  vec_io: residual and outputs are 16-byte aligned.
+//
+// With norm.w set (a stack whose next layer takes bf16 rows; the row fits
+// one workgroup, d <= 256 C, and its stride is d): the next layer's RMSNorm
+// (normalization/rmsnorm.go:33-53) is done here on the new row, which the
+// workgroup holds whole -- its bf16 normalised row and its inverse RMS are
+// written, so the next layer needs no pass of its own over the residual.
 template <typename SlotT, int KB>
 __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k, const SlotT *__restrict__ slot_out,
                                                       const int32_t *__restrict__ pos,
                                                       const float *__restrict__ gates32,
                                                       const float *__restrict__ residual, float *__restrict__ out32,
-                                                      double *__restrict__ out64, bool vec_io)
+                                                      double *__restrict__ out64, bool vec_io, CombineNorm norm)
 {
     constexpr int C = sizeof(SlotT) == 2 ? 8 : 4;
+    __shared__ float partial[4];
     const int t = blockIdx.x;
+    if (norm.w) {
+        // one row per workgroup: every thread takes part in the reduction
+        const int j0 = threadIdx.x * C;
+        const bool mine = j0 < d;
+        float acc[C];
+#pragma unroll
+        for (int q = 0; q < C; ++q) acc[q] = 0.f;
+        if (mine) {
+            int p[KB];
+            float g[KB];
+#pragma unroll
+            for (int i = 0; i < KB; ++i) {
+                const int ii = i < k ? i : 0;
+                p[i] = S * T + (pos ? pos[(size_t)t * k + ii] : t * k + ii);
+                g[i] = gates32[(size_t)t * k + ii];
+            }
+            float v[KB][C];
+#pragma unroll
+            for (int i = 0; i < KB; ++i) loadC<C>(slot_out + (size_t)p[i] * d + j0, v[i]);
+            for (int s = 0; s < S; ++s) {
+                float u[C];
+                loadC<C>(slot_out + ((size_t)s * T + t) * d + j0, u);
+#pragma unroll
+                for (int q = 0; q < C; ++q) acc[q] += u[q];
+            }
+#pragma unroll
+            for (int i = 0; i < KB; ++i)
+                if (i < k)
+#pragma unroll
+                    for (int q = 0; q < C; ++q) acc[q] = fmaf(g[i], v[i][q], acc[q]);
+            const size_t o = (size_t)t * d + j0;
+            float r[C];
+            loadC<C>(residual + o, r);
+#pragma unroll
+            for (int q = 0; q < C; ++q) acc[q] = r[q] + acc[q];
+#pragma unroll
+            for (int q = 0; q < C; q += 4)
+                *reinterpret_cast<float4 *>(out32 + o + q) = make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < C; ++q) ss = fmaf(acc[q], acc[q], ss);
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float total = partial[0] + partial[1] + partial[2] + partial[3];
+        const float inv = 1.0f / sqrtf(total / (float)d + 1e-6f);
+        if (threadIdx.x == 0) norm.inv[t] = inv;
+        if (mine) {
+            float w[C];
+            loadC<C>(norm.w + j0, w);
+#pragma unroll
+            for (int q = 0; q < C; q += 4)
+                *reinterpret_cast<uint2 *>(norm.xb + (size_t)t * norm.ldb + j0 + q) =
+                    to_bf16x4(acc[q] * inv * w[q], acc[q + 1] * inv * w[q + 1], acc[q + 2] * inv * w[q + 2],
+                              acc[q + 3] * inv * w[q + 3]);
+        }
+        return;
+    }
     const int j0 = (blockIdx.y * 256 + threadIdx.x) * C;
     if (j0 >= d) return;
     int p[KB];
@@ -240,22 +306,29 @@ __global__ __launch_bounds__(256) void combine_kernel(int T, int d, int S, int k
     }
 }
 
+bool combine_norm_fits(int d, bool slot_bf16) { return slot_bf16 && d % 8 == 0 && d <= 2048; }
+
 hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool slot_bf16, const int32_t *pos,
-                          const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s)
+                          const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s,
+                          const CombineNorm &norm)
 {
     if (T <= 0) return hipSuccess;
     if (k < 1 || k > 8) return hipErrorInvalidValue;
     auto aligned = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
     const bool vec_io = aligned(residual) && aligned(out32) && aligned(out64);  // null counts as aligned
+    if (norm.w && (!combine_norm_fits(d, slot_bf16) || !residual || !out32 || out64 || !vec_io || !norm.xb ||
+                   !norm.inv || norm.ldb < d || norm.ldb % 8 != 0 || !aligned(norm.xb) || !aligned(norm.w)))
+        return hipErrorInvalidValue;
     auto go = [&](auto kb_tag) {
         constexpr int KB = decltype(kb_tag)::value;
         if (slot_bf16)
             hipLaunchKernelGGL((combine_kernel<uint16_t, KB>), dim3(T, (d + 2047) / 2048), dim3(256), 0, s, T, d, S,
                                k, static_cast<const uint16_t *>(slot_out), pos, gates32, residual, out32, out64,
-                               vec_io);
+                               vec_io, norm);
         else
             hipLaunchKernelGGL((combine_kernel<float, KB>), dim3(T, (d + 1023) / 1024), dim3(256), 0, s, T, d, S, k,
-                               static_cast<const float *>(slot_out), pos, gates32, residual, out32, out64, vec_io);
+                               static_cast<const float *>(slot_out), pos, gates32, residual, out32, out64, vec_io,
+                               norm);
     };
     if (k <= 2) go(std::integral_constant<int, 2>{});
     else if (k <= 4) go(std::integral_constant<int, 4>{});

@@ -151,7 +151,8 @@ __device__ double affinity(double logit)
 __global__ __launch_bounds__(256) void router_small_kernel(const float *__restrict__ x, int ldx, int T, int kp,
                                                            const float *__restrict__ w, int ldw,
                                                            const double *__restrict__ bias, int E,
-                                                           double *__restrict__ logits)
+                                                           double *__restrict__ logits,
+                                                           const float *__restrict__ row_scale)
 {
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -168,6 +169,7 @@ __global__ __launch_bounds__(256) void router_small_kernel(const float *__restri
         acc = fmaf(a.w, b.w, acc);
     }
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (row_scale) acc = row_scale[t] * acc;
     if (lane == 0) logits[(size_t)t * E + e] = (double)acc + bias[e];
 }
 
@@ -183,7 +185,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ x, int ldx, int T, int kp,
                                                           const float *__restrict__ w, int ldw,
                                                           const double *__restrict__ bias, int E,
-                                                          double *__restrict__ logits)
+                                                          double *__restrict__ logits,
+                                                          const float *__restrict__ row_scale)
 {
     __shared__ float red[4][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -234,24 +237,29 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
     for (int j = 0; j < 4; ++j) {
         const int i = 4 * wave + j;
         const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), e = e0 + r;
-        const float v = red[0][i][lane] + red[1][i][lane] + red[2][i][lane] + red[3][i][lane];
-        if (t < T && e < E) logits[(size_t)t * E + e] = (double)v + bias[e];
+        float v = red[0][i][lane] + red[1][i][lane] + red[2][i][lane] + red[3][i][lane];
+        if (t < T && e < E) {
+            if (row_scale) v = row_scale[t] * v;
+            logits[(size_t)t * E + e] = (double)v + bias[e];
+        }
     }
 }
 
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
-                         double *logits, hipStream_t s)
+                         double *logits, hipStream_t s, const float *row_scale)
 {
     if (T <= 0) return hipSuccess;
     if (T <= 256) {
         // rows are zero-padded to a multiple of 64 values
         const int kp = (d + 63) / 64 * 64;
         dim3 grid((T * E + 3) / 4);
-        hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits);
+        hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
+                           row_scale);
     } else {
         const int kp = (d + 63) / 64 * 64;
         dim3 grid((T + 31) / 32, (E + 31) / 32);
-        hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits);
+        hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
+                           row_scale);
     }
     return hipGetLastError();
 }

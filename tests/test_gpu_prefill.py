@@ -249,3 +249,33 @@ def test_device_buffers_off_16_byte_alignment(ctx, path, T):
         m.destroy()
     assert np.all(np.isfinite(a))
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("d,hash_mid", [(128, False), (128, True), (96, False)])
+def test_bf16_stack_norm_done_by_the_combine(ctx, d, hash_mid):
+    """A bf16 stack past the fused routing (T*k > 2048).  With d a multiple of
+    64 each layer's combine also writes the next layer's normalised bf16 rows
+    and inverse RMS, and the next router reads the raw rows against its rows
+    times the norm weights; d = 96 keeps the separate RMSNorm pass.  A
+    hash-routed middle layer takes the normalised rows without a router."""
+    say(f"bf16 stack, norm in the combine, d={d} hash_mid={hash_mid}")
+    T = 600
+    rng = np.random.default_rng(70 + d)
+    specs = [make_moe(gt.encode_rows, d=d, h=64, E=8, k=4, S=1, precision=FP4, seed=71 + i, std=0.1,
+                      bias_std=0.01, use_hash=hash_mid and i == 1) for i in range(3)]
+    norms = [1.0 + 0.2 * rng.standard_normal(d) for _ in range(3)]
+    x0 = rng.standard_normal((T, d))
+    ids = rng.integers(0, 10000, T) if hash_mid else None
+    ms = [gt.MixtureOfExperts.from_spec(ctx, s) for s in specs]
+    try:
+        for m, w in zip(ms, norms):
+            m.set_norm_weights(w)
+        x, chosen, gates = gt.stack_forward(ms, x0, ids, path=gt.PATH_BF16, with_routing=True)
+        assert all(m.last_path == gt.PATH_BF16 for m in ms)
+    finally:
+        for m in ms:
+            m.destroy()
+    ref = oracle.stack_forward_routed(specs, norms, x0, chosen, gates, threads=16)
+    e = rel_err(x, ref)
+    say(f"[d={d} hash_mid={hash_mid}] max rel err {e:.3e}")
+    assert e <= BF16_TOL
