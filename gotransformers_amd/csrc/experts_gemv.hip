@@ -389,6 +389,15 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
         }
     }
 
+    // the epilogue's biases are requested before the ring, so that the loads
+    // in flight at the main loop's entry are the ring's alone, in ring order,
+    // as on its back edge
+    const int row = panel * 64 + lane;
+    const bool writer = wave < 4 && row < a.rows;
+    float bias[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) bias[m] = writer ? (m == 0 ? a.b0 : a.b1)[(size_t)g * a.rows + row] : 0.f;
+
     constexpr int kDepth = ring_depth<PREC, MATS, NQ>();
     // Every load of the ring is issued unconditionally, so that the compiler
     // can count the loads in flight and wait for one chunk at a time (loads
@@ -397,12 +406,16 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
     const int clast = c1 > c0 ? c1 - 1 : c0;
     ChunkRegs<PREC, MATS> r[kDepth];
 #pragma unroll
-    for (int i = 0; i < kDepth; ++i) load_chunk<PREC, MATS>(r[i], src, vo, min(c0 + i, clast));
-    const int row = panel * 64 + lane;
-    const bool writer = wave < 4 && row < a.rows;
-    float bias[MATS];
-#pragma unroll
-    for (int m = 0; m < MATS; ++m) bias[m] = writer ? (m == 0 ? a.b0 : a.b1)[(size_t)g * a.rows + row] : 0.f;
+    for (int i = 0; i < kDepth; ++i) {
+        // the scheduling barriers keep the ring's loads in ring order here
+        // and in the loop: the compiler's wait before each chunk must hold
+        // for the loads in flight both at the loop's entry and on its back
+        // edge, so a different order here (say all codes, then all scales)
+        // would make it wait for the next chunk's loads as well
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk<PREC, MATS>(r[i], src, vo, min(c0 + i, clast));
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     uint4 *xhi = reinterpret_cast<uint4 *>(lds);
     uint4 *xlo = xhi + (size_t)ng8 * NT;
@@ -435,14 +448,25 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
         for (int q = 0; q < NQ; ++q) acc[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // ring of kDepth chunk buffers: once chunk ch is computed, its buffer
-    // takes chunk ch + kDepth
-    for (int ch = c0; ch < c1; ch += kDepth) {
+    // takes chunk ch + kDepth.  The loop body computes every buffer with no
+    // branch, so the loads in flight on its back edge are exactly the ring's
+    // and the compiler waits, before each chunk, for that chunk's loads only
+    // (with a conditional compute in the body it also waited for the next
+    // buffer's loads, leaving about one chunk in flight); the last
+    // c1 - ch < kDepth chunks, already in the ring, are computed after it.
+    int ch = c0;
+    for (; ch + kDepth <= c1; ch += kDepth) {
 #pragma unroll
         for (int j = 0; j < kDepth; ++j) {
-            if (ch + j < c1) compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
+            compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
+            __builtin_amdgcn_sched_barrier(0);
             load_chunk<PREC, MATS>(r[j], src, vo, min(ch + j + kDepth, clast));
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+#pragma unroll
+    for (int j = 0; j + 1 < kDepth; ++j)
+        if (ch + j < c1) compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
 
     // sum the NW partial K ranges through LDS; wave v < 4 then finishes
     // tokens 4q + v of every quad
