@@ -1065,13 +1065,13 @@ RowsArgs rows_args(const DeviceMatrix &m, const float *in, int ld_in, const int3
     return r;
 }
 
-// Row chunks for the transposed product over `rows` rows: enough one-wave
+// Row chunks for the transposed product over `rows` rows: enough four-wave
 // workgroups for about four waves per SIMD (one chunk when the tiles alone
 // do that).
 int transposed_chunks(const gtmoe_layer *L, int rows, int ntiles, int colblocks)
 {
     const int busy = ntiles * colblocks;
-    int want = (16 * L->ctx->compute_units + busy - 1) / std::max(busy, 1);
+    int want = (4 * L->ctx->compute_units + busy - 1) / std::max(busy, 1);
     want = std::min(want, (rows + rows_transposed_chunk_rows() - 1) / rows_transposed_chunk_rows());
     return std::max(1, std::min(want, L->tw.chunks));
 }

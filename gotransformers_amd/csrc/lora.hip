@@ -42,51 +42,70 @@ __device__ __forceinline__ float fp4_value(uint32_t code)
     return (code & 8) ? -v : v;
 }
 
-// The 16 values of block b (columns 16b .. 16b+15) of row r, without the
-// block scale (Int8, FP4) or as stored (Float32).
+// out[p][i] = sum_r grad[p][r] * W[r][i] for the group's rows r: the
+// reference's Rows.AddScaledRowTo over every row with scale grad[p][r]
+// (target_i += (grad * blockScale) * value).  Lane = one block of 16 columns
+// (blockIdx.x * 64 + lane), the kTrTile positions of tile blockIdx.y, rows
+// [blockIdx.z * chunk_rows, +chunk_rows).  The four waves take a quarter of
+// every staged run of rows each and request kTrBatch rows' codes and scales
+// before their arithmetic (enough bytes in flight to stream the rows at
+// decode sizes); their partial sums are added in wave order through LDS.
+// With more than one row chunk each writes its partial sums to
+// partial[blockIdx.z] (same layout as out) and sum_chunks_kernel adds them
+// in chunk order.  Every column of the padded width is written (zero past
+// the matrix).
 template <int PREC>
-__device__ __forceinline__ void block_values(const char *codes, int r, int b, int row_bytes, float (&w)[16])
+__device__ __forceinline__ void load_block_raw(const char *codes, int r, int b, int row_bytes, uint4 (&q)[PREC == kFloat32 ? 4 : 1])
 {
     if constexpr (PREC == kInt8) {
-        const uint4 q = *reinterpret_cast<const uint4 *>(codes + panel_unit_offset(r, b, row_bytes));
-        const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+        q[0] = *reinterpret_cast<const uint4 *>(codes + panel_unit_offset(r, b, row_bytes));
+    } else if constexpr (PREC == kFP4) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(codes + panel_unit_offset(r, b >> 1, row_bytes) + 8 * (b & 1));
+        q[0] = make_uint4(v.x, v.y, 0u, 0u);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = *reinterpret_cast<const uint4 *>(codes + panel_unit_offset(r, 4 * b + u, row_bytes));
+    }
+}
+
+template <int PREC>
+__device__ __forceinline__ void decode_block(const uint4 (&q)[PREC == kFloat32 ? 4 : 1], float (&w)[16])
+{
+    if constexpr (PREC == kInt8) {
+        const uint32_t d[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
 #pragma unroll
         for (int v = 0; v < 16; ++v) w[v] = (float)(int8_t)(d[v >> 2] >> (8 * (v & 3)));
     } else if constexpr (PREC == kFP4) {
-        const uint2 q = *reinterpret_cast<const uint2 *>(codes + panel_unit_offset(r, b >> 1, row_bytes) + 8 * (b & 1));
-        const uint32_t d[2] = {q.x, q.y};
+        const uint32_t d[2] = {q[0].x, q[0].y};
 #pragma unroll
         for (int v = 0; v < 16; ++v) w[v] = fp4_value(d[v >> 3] >> (4 * (v & 7)));
     } else {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float4 f = *reinterpret_cast<const float4 *>(codes + panel_unit_offset(r, 4 * b + u, row_bytes));
-            w[4 * u] = f.x;
-            w[4 * u + 1] = f.y;
-            w[4 * u + 2] = f.z;
-            w[4 * u + 3] = f.w;
+            w[4 * u] = __uint_as_float(q[u].x);
+            w[4 * u + 1] = __uint_as_float(q[u].y);
+            w[4 * u + 2] = __uint_as_float(q[u].z);
+            w[4 * u + 3] = __uint_as_float(q[u].w);
         }
     }
 }
 
-// out[p][i] = sum_r grad[p][r] * W[r][i] for the group's rows r: the
-// reference's Rows.AddScaledRowTo over every row with scale grad[p][r]
-// (target_i += (grad * blockScale) * value).  Lane = one block of 16 columns
-// (blockIdx.x * 64 + lane), the kTrTile positions of tile blockIdx.y, rows
-// [blockIdx.z * chunk_rows, +chunk_rows); with more than one row chunk each
-// writes its partial sums to partial[blockIdx.z] (same layout as out) and
-// sum_chunks_kernel adds them in chunk order.  Every column of the padded
-// width is written (zero past the matrix).
+constexpr int kTrWaves = 4;
+constexpr int kTrBatch = 8;
+
 template <int PREC>
-__global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a, int chunk_rows, float *__restrict__ partial,
-                                                             long long partial_stride)
+__global__ __launch_bounds__(64 * kTrWaves) void rows_transposed_kernel(RowsArgs a, int chunk_rows,
+                                                                        float *__restrict__ partial,
+                                                                        long long partial_stride)
 {
     __shared__ float gs[kTrTile][kTrRows];
+    __shared__ float red[kTrWaves - 1][16][64];
     const int4 td = a.tiles[blockIdx.y];
     const int g = td.x, p0 = td.y, m = td.z;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int b = blockIdx.x * 64 + lane;  // block of 16 columns
     const bool live = b < a.nblocks;
+    const int bl = live ? b : 0;  // loads of dead lanes stay in bounds and are not used
     const char *codes = reinterpret_cast<const char *>(a.values) + (size_t)g * a.w_group_stride;
     const float *sc = a.scales + (size_t)g * a.s_group_stride;
     float acc[kTrTile][16];
@@ -97,33 +116,58 @@ __global__ __launch_bounds__(64) void rows_transposed_kernel(RowsArgs a, int chu
     const int nbeg = blockIdx.z * chunk_rows, nend = min(a.rows, nbeg + chunk_rows);
     for (int n0 = nbeg; n0 < nend; n0 += kTrRows) {
         __syncthreads();
-        for (int idx = lane; idx < kTrTile * kTrRows; idx += 64) {
+        for (int idx = threadIdx.x; idx < kTrTile * kTrRows; idx += 64 * kTrWaves) {
             const int q = idx / kTrRows, c = idx - q * kTrRows;
             gs[q][c] = q < m && n0 + c < nend ? a.in[(size_t)(p0 + q) * a.ld_in + n0 + c] : 0.f;
         }
         __syncthreads();
-        if (!live) continue;
         const int nn = min(kTrRows, nend - n0);
-#pragma unroll 4
-        for (int c = 0; c < nn; ++c) {
-            const int r = n0 + c;
-            float w[16];
-            block_values<PREC>(codes, r, b, a.row_bytes, w);
-            const float s = PREC == kFloat32 ? 1.f : sc[panel_scale_index(r, b, a.nblocks)];
+        const int ca = wave * nn / kTrWaves, cb = (wave + 1) * nn / kTrWaves;
+        for (int c0 = ca; c0 < cb; c0 += kTrBatch) {
+            uint4 q[kTrBatch][PREC == kFloat32 ? 4 : 1];
+            float s[kTrBatch];
 #pragma unroll
-            for (int q = 0; q < kTrTile; ++q) {
-                const float cs = PREC == kFloat32 ? gs[q][c] : gs[q][c] * s;
+            for (int u = 0; u < kTrBatch; ++u) {
+                const int r = n0 + min(c0 + u, cb - 1);
+                load_block_raw<PREC>(codes, r, bl, a.row_bytes, q[u]);
+                s[u] = PREC == kFloat32 ? 1.f : sc[panel_scale_index(r, bl, a.nblocks)];
+            }
 #pragma unroll
-                for (int v = 0; v < 16; ++v) acc[q][v] = fmaf(cs, w[v], acc[q][v]);
+            for (int u = 0; u < kTrBatch; ++u) {
+                if (c0 + u >= cb) break;  // wave-uniform
+                float w[16];
+                decode_block<PREC>(q[u], w);
+#pragma unroll
+                for (int qq = 0; qq < kTrTile; ++qq) {
+                    const float cs = PREC == kFloat32 ? gs[qq][c0 + u] : gs[qq][c0 + u] * s[u];
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[qq][v] = fmaf(cs, w[v], acc[qq][v]);
+                }
             }
         }
     }
-    if (!live) return;
+    // add the waves' partial sums in wave order, one position at a time
     float *dst = gridDim.z == 1 ? a.out : partial + (size_t)blockIdx.z * partial_stride;
-    for (int q = 0; q < m; ++q) {
-        float4 *o = reinterpret_cast<float4 *>(dst + (size_t)(p0 + q) * a.ld_out + 16 * b);
+    for (int qq = 0; qq < kTrTile; ++qq) {
+        __syncthreads();
+        if (wave > 0) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) o[u] = make_float4(acc[q][4 * u], acc[q][4 * u + 1], acc[q][4 * u + 2], acc[q][4 * u + 3]);
+            for (int v = 0; v < 16; ++v) red[wave - 1][v][lane] = acc[qq][v];
+        }
+        __syncthreads();
+        if (wave == 0 && live && qq < m) {
+            float o[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float t = acc[qq][v];
+#pragma unroll
+                for (int w2 = 0; w2 < kTrWaves - 1; ++w2) t += red[w2][v][lane];
+                o[v] = t;
+            }
+            float4 *out = reinterpret_cast<float4 *>(dst + (size_t)(p0 + qq) * a.ld_out + 16 * b);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) out[u] = make_float4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]);
+        }
     }
 }
 
@@ -408,10 +452,15 @@ hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, 
     const long long stride = (long long)a.tiles_positions * a.ld_out;
     const dim3 grid((a.nblocks + 63) / 64, ntiles, chunks);
     switch (precision) {
-    case kInt8: hipLaunchKernelGGL(rows_transposed_kernel<kInt8>, grid, dim3(64), 0, s, a, chunk_rows, partial, stride); break;
-    case kFP4: hipLaunchKernelGGL(rows_transposed_kernel<kFP4>, grid, dim3(64), 0, s, a, chunk_rows, partial, stride); break;
+    case kInt8:
+        hipLaunchKernelGGL(rows_transposed_kernel<kInt8>, grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial, stride);
+        break;
+    case kFP4:
+        hipLaunchKernelGGL(rows_transposed_kernel<kFP4>, grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial, stride);
+        break;
     case kFloat32:
-        hipLaunchKernelGGL(rows_transposed_kernel<kFloat32>, grid, dim3(64), 0, s, a, chunk_rows, partial, stride);
+        hipLaunchKernelGGL(rows_transposed_kernel<kFloat32>, grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial,
+                           stride);
         break;
     default: return hipErrorInvalidValue;
     }
@@ -422,7 +471,7 @@ hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, 
 }
 
 int rows_transposed_tile() { return kTrTile; }
-int rows_transposed_chunk_rows() { return 32; }
+int rows_transposed_chunk_rows() { return 32 * kTrWaves; }
 
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
                             hipStream_t s)
