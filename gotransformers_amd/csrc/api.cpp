@@ -213,7 +213,7 @@ struct TrainWorkspace {
     double *zero_bias = nullptr;     // [E]
     float *partial = nullptr;        // [chunks][P][max(dp, hp)] row-chunk sums of the transposed product
     int chunks = 1;                  // row chunks the partial buffer holds
-    int P = 0, ntiles_tr = 0;
+    int P = 0, ntiles_tr = 0, tile_tr = 4;
 };
 
 struct gtmoe_layer {
@@ -1114,7 +1114,7 @@ int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64
     if (P != T * (S + k)) return fail(ctx, GTMOE_ERR_DEVICE, "dispatch placed %d positions, expected %d", P, T * (S + k));
     std::vector<int32_t> pgroup(P);
     std::vector<int4> ttr;
-    const int bt = rows_transposed_tile();
+    const int bt = rows_transposed_tile(P, G);
     for (int g = 0; g < G; ++g) {
         for (int p = goff[g]; p < goff[g + 1]; ++p) pgroup[p] = g;
         for (int p = goff[g]; p < goff[g + 1]; p += bt) ttr.push_back(make_int4(g, p, std::min(bt, goff[g + 1] - p), 0));
@@ -1123,6 +1123,7 @@ int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64
     HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_tr, ttr.data(), sizeof(int4) * ttr.size(), hipMemcpyHostToDevice, s));
     tw.P = P;
     tw.ntiles_tr = (int)ttr.size();
+    tw.tile_tr = bt;
 
     // the bare products x W^T by the decode GEMV kernels (raw mode, over the
     // dispatch's slices), then the adapter terms and the biases
@@ -1215,7 +1216,7 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
         RowsArgs r = rows_args(m, in, ld_in, nullptr, out, ld_out, tw.tiles_tr);
         r.tiles_positions = P;
         const int chunks = transposed_chunks(L, m.rows, tw.ntiles_tr, (m.nblocks + 63) / 64);
-        return launch_rows_transposed(r, m.precision, tw.ntiles_tr, chunks, tw.partial, s);
+        return launch_rows_transposed(r, m.precision, tw.ntiles_tr, tw.tile_tr, chunks, tw.partial, s);
     };
     RUN(ctx, s, "rows_transposed", transposed(L->down, tw.eg, d, tw.hgrad, hp));
     RUN(ctx, s, "lora_backward",

@@ -246,9 +246,9 @@ hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t
 // Adapter path (lora.hip, route.hip).
 // out = in W over `chunks` row chunks; partial: chunks * positions * ld_out
 // floats of scratch when chunks > 1
-hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int chunks, float *partial,
+hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int tile, int chunks, float *partial,
                                   hipStream_t s);
-int rows_transposed_tile();
+int rows_transposed_tile(int positions, int groups);
 // smallest row chunk worth a workgroup of its own
 int rows_transposed_chunk_rows();
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,

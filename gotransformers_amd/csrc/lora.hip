@@ -32,7 +32,6 @@ namespace gtmoe {
 
 namespace {
 
-constexpr int kTrTile = 4;    // positions per workgroup of rows_transposed_kernel
 constexpr int kTrRows = 128;  // gradient rows staged per step
 
 __device__ __forceinline__ float fp4_value(uint32_t code)
@@ -45,7 +44,7 @@ __device__ __forceinline__ float fp4_value(uint32_t code)
 // out[p][i] = sum_r grad[p][r] * W[r][i] for the group's rows r: the
 // reference's Rows.AddScaledRowTo over every row with scale grad[p][r]
 // (target_i += (grad * blockScale) * value).  Lane = one block of 16 columns
-// (blockIdx.x * 64 + lane), the kTrTile positions of tile blockIdx.y, rows
+// (blockIdx.x * 64 + lane), the TILE positions of tile blockIdx.y, rows
 // [blockIdx.z * chunk_rows, +chunk_rows).  The four waves take a quarter of
 // every staged run of rows each and request kTrBatch rows' codes and scales
 // before their arithmetic (enough bytes in flight to stream the rows at
@@ -93,12 +92,12 @@ __device__ __forceinline__ void decode_block(const uint4 (&q)[PREC == kFloat32 ?
 constexpr int kTrWaves = 4;
 constexpr int kTrBatch = 8;
 
-template <int PREC>
+template <int PREC, int TILE>
 __global__ __launch_bounds__(64 * kTrWaves) void rows_transposed_kernel(RowsArgs a, int chunk_rows,
                                                                         float *__restrict__ partial,
                                                                         long long partial_stride)
 {
-    __shared__ float gs[kTrTile][kTrRows];
+    __shared__ float gs[TILE][kTrRows];
     __shared__ float red[kTrWaves - 1][16][64];
     const int4 td = a.tiles[blockIdx.y];
     const int g = td.x, p0 = td.y, m = td.z;
@@ -108,15 +107,15 @@ __global__ __launch_bounds__(64 * kTrWaves) void rows_transposed_kernel(RowsArgs
     const int bl = live ? b : 0;  // loads of dead lanes stay in bounds and are not used
     const char *codes = reinterpret_cast<const char *>(a.values) + (size_t)g * a.w_group_stride;
     const float *sc = a.scales + (size_t)g * a.s_group_stride;
-    float acc[kTrTile][16];
+    float acc[TILE][16];
 #pragma unroll
-    for (int q = 0; q < kTrTile; ++q)
+    for (int q = 0; q < TILE; ++q)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[q][v] = 0.f;
     const int nbeg = blockIdx.z * chunk_rows, nend = min(a.rows, nbeg + chunk_rows);
     for (int n0 = nbeg; n0 < nend; n0 += kTrRows) {
         __syncthreads();
-        for (int idx = threadIdx.x; idx < kTrTile * kTrRows; idx += 64 * kTrWaves) {
+        for (int idx = threadIdx.x; idx < TILE * kTrRows; idx += 64 * kTrWaves) {
             const int q = idx / kTrRows, c = idx - q * kTrRows;
             gs[q][c] = q < m && n0 + c < nend ? a.in[(size_t)(p0 + q) * a.ld_in + n0 + c] : 0.f;
         }
@@ -138,7 +137,7 @@ __global__ __launch_bounds__(64 * kTrWaves) void rows_transposed_kernel(RowsArgs
                 float w[16];
                 decode_block<PREC>(q[u], w);
 #pragma unroll
-                for (int qq = 0; qq < kTrTile; ++qq) {
+                for (int qq = 0; qq < TILE; ++qq) {
                     const float cs = PREC == kFloat32 ? gs[qq][c0 + u] : gs[qq][c0 + u] * s[u];
 #pragma unroll
                     for (int v = 0; v < 16; ++v) acc[qq][v] = fmaf(cs, w[v], acc[qq][v]);
@@ -148,7 +147,7 @@ __global__ __launch_bounds__(64 * kTrWaves) void rows_transposed_kernel(RowsArgs
     }
     // add the waves' partial sums in wave order, one position at a time
     float *dst = gridDim.z == 1 ? a.out : partial + (size_t)blockIdx.z * partial_stride;
-    for (int qq = 0; qq < kTrTile; ++qq) {
+    for (int qq = 0; qq < TILE; ++qq) {
         __syncthreads();
         if (wave > 0) {
 #pragma unroll
@@ -443,25 +442,34 @@ inline dim3 cols_grid(int cols, int rows) { return dim3((cols + 255) / 256, rows
 
 }  // namespace
 
-hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int chunks, float *partial,
+namespace {
+
+template <int PREC>
+void launch_transposed_prec(const RowsArgs &a, int tile, dim3 grid, int chunk_rows, float *partial, long long stride,
+                            hipStream_t s)
+{
+    if (tile == 8)
+        hipLaunchKernelGGL((rows_transposed_kernel<PREC, 8>), grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial,
+                           stride);
+    else
+        hipLaunchKernelGGL((rows_transposed_kernel<PREC, 4>), grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial,
+                           stride);
+}
+
+}  // namespace
+
+hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int tile, int chunks, float *partial,
                                   hipStream_t s)
 {
     if (ntiles <= 0) return hipSuccess;
-    if (chunks < 1 || (chunks > 1 && !partial)) return hipErrorInvalidValue;
+    if (chunks < 1 || (chunks > 1 && !partial) || (tile != 4 && tile != 8)) return hipErrorInvalidValue;
     const int chunk_rows = (a.rows + chunks - 1) / chunks;
     const long long stride = (long long)a.tiles_positions * a.ld_out;
     const dim3 grid((a.nblocks + 63) / 64, ntiles, chunks);
     switch (precision) {
-    case kInt8:
-        hipLaunchKernelGGL(rows_transposed_kernel<kInt8>, grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial, stride);
-        break;
-    case kFP4:
-        hipLaunchKernelGGL(rows_transposed_kernel<kFP4>, grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial, stride);
-        break;
-    case kFloat32:
-        hipLaunchKernelGGL(rows_transposed_kernel<kFloat32>, grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial,
-                           stride);
-        break;
+    case kInt8: launch_transposed_prec<kInt8>(a, tile, grid, chunk_rows, partial, stride, s); break;
+    case kFP4: launch_transposed_prec<kFP4>(a, tile, grid, chunk_rows, partial, stride, s); break;
+    case kFloat32: launch_transposed_prec<kFloat32>(a, tile, grid, chunk_rows, partial, stride, s); break;
     default: return hipErrorInvalidValue;
     }
     if (chunks > 1)
@@ -470,7 +478,10 @@ hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, 
     return hipGetLastError();
 }
 
-int rows_transposed_tile() { return kTrTile; }
+// Positions per workgroup of the transposed product: eight once the groups
+// average eight positions (each decoded weight then feeds twice the
+// multiply-adds), else four.
+int rows_transposed_tile(int positions, int groups) { return positions >= 8 * groups ? 8 : 4; }
 int rows_transposed_chunk_rows() { return 32 * kTrWaves; }
 
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
