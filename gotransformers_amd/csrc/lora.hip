@@ -231,7 +231,17 @@ __global__ __launch_bounds__(256) void lora_up_bias_kernel(LoraArgs a, const flo
     const float *B = a.B + ((size_t)g * a.rows + n) * a.R;
     const float *up = u + (size_t)p * a.R;
     float s = 0.f;
-    for (int j = 0; j < a.R; ++j) s = fmaf(B[j], up[j], s);
+    if ((a.R & 3) == 0) {  // the row's ranks as float4 runs (rows are 16-byte aligned)
+        for (int j = 0; j < a.R; j += 4) {
+            const float4 b4 = *reinterpret_cast<const float4 *>(B + j);
+            s = fmaf(b4.x, up[j], s);
+            s = fmaf(b4.y, up[j + 1], s);
+            s = fmaf(b4.z, up[j + 2], s);
+            s = fmaf(b4.w, up[j + 3], s);
+        }
+    } else {
+        for (int j = 0; j < a.R; ++j) s = fmaf(B[j], up[j], s);
+    }
     OutT &o = out[(size_t)p * ld_out + n];
     if constexpr (sizeof(OutT) == 8) {
         o = (o + (double)(a.scale[g] * s)) + bias64[n];
@@ -254,27 +264,58 @@ __global__ __launch_bounds__(256) void lora_grad_up_kernel(LoraArgs a, const flo
     dB[(size_t)g * a.rows * a.R + idx] += (double)(a.scale[g] * s);
 }
 
-// t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one wave per
-// (position, rank j), unconditional loads as in lora_down_kernel.
+// t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one workgroup per
+// position and 16 ranks: lane l of wave w takes rows n = 64 (4 i + w) + l,
+// reading the gradient once and each row's 16 ranks of B as contiguous
+// float4 runs; each wave adds its lanes' partial sums, and the four waves'
+// sums are added in wave order through LDS.
+constexpr int kTRanks = 16;
+
 __global__ __launch_bounds__(256) void lora_t_kernel(LoraArgs a, const float *__restrict__ grad, int ld_g,
                                                      float *__restrict__ t)
 {
-    const int lane = threadIdx.x & 63;
-    const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wv >= a.P * a.R) return;  // wave-uniform
-    const int p = wv / a.R, j = wv - p * a.R;
+    __shared__ float part[4][kTRanks];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nj = (a.R + kTRanks - 1) / kTRanks;
+    const int p = blockIdx.x / nj, j0 = (blockIdx.x - p * nj) * kTRanks;
     const int g = a.pgroup ? a.pgroup[p] : 0;
     const float *gr = grad + (size_t)p * ld_g;
-    const float *B = a.B + (size_t)g * a.rows * a.R + j;
-    float s = 0.f;
-#pragma unroll 8
-    for (int n = lane; n < a.rows + 63; n += 64) {
-        const int c = min(n, a.rows - 1);
-        const float d = gr[c] * B[(size_t)c * a.R];
-        s += n < a.rows ? d : 0.f;
+    const float *B = a.B + (size_t)g * a.rows * a.R;
+    const bool vec = (a.R & 3) == 0 && j0 + kTRanks <= a.R;
+    float s[kTRanks];
+#pragma unroll
+    for (int j = 0; j < kTRanks; ++j) s[j] = 0.f;
+#pragma unroll 2
+    for (int n = 64 * wave + lane; n < a.rows; n += 256) {
+        const float gv = gr[n];
+        const float *br = B + (size_t)n * a.R + j0;
+        if (vec) {
+#pragma unroll
+            for (int q = 0; q < kTRanks / 4; ++q) {
+                const float4 b4 = *reinterpret_cast<const float4 *>(br + 4 * q);
+                s[4 * q] = fmaf(gv, b4.x, s[4 * q]);
+                s[4 * q + 1] = fmaf(gv, b4.y, s[4 * q + 1]);
+                s[4 * q + 2] = fmaf(gv, b4.z, s[4 * q + 2]);
+                s[4 * q + 3] = fmaf(gv, b4.w, s[4 * q + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kTRanks; ++j)
+                if (j0 + j < a.R) s[j] = fmaf(gv, br[j], s[j]);
+        }
     }
-    s = wave_sum(s);
-    if (lane == 0) t[(size_t)p * a.R + j] = a.scale[g] * s;
+#pragma unroll
+    for (int j = 0; j < kTRanks; ++j) s[j] = wave_sum(s[j]);
+    if (lane < kTRanks) {
+        float v = s[0];
+#pragma unroll
+        for (int j = 1; j < kTRanks; ++j)
+            if (lane == j) v = s[j];
+        part[wave][lane] = v;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kTRanks && j0 + lane < a.R)
+        t[(size_t)p * a.R + j0 + lane] = a.scale[g] * (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
 }
 
 // dA[g][j][i] += sum_{p in g} t[p][j] * in[row(p)][i], i < width
@@ -517,8 +558,7 @@ hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, 
 {
     if (a.P <= 0 || a.R <= 0) return hipSuccess;
     hipLaunchKernelGGL(lora_grad_up_kernel, cols_grid(a.rows * a.R, a.G), dim3(256), 0, s, a, grad, ld_g, u, dB);
-    const int waves = a.P * a.R;
-    hipLaunchKernelGGL(lora_t_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, a, grad, ld_g, t);
+    hipLaunchKernelGGL(lora_t_kernel, dim3(a.P * ((a.R + kTRanks - 1) / kTRanks)), dim3(256), 0, s, a, grad, ld_g, t);
     hipLaunchKernelGGL(lora_grad_down_kernel, cols_grid(a.R * a.width, a.G), dim3(256), 0, s, a, t, in, ld_in,
                        in_tok, dA);
     hipLaunchKernelGGL(lora_dx_kernel, cols_grid(a.width, a.P), dim3(256), 0, s, a, t, dx, ld_dx);
