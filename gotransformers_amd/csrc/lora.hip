@@ -337,19 +337,35 @@ __global__ __launch_bounds__(256) void lora_grad_down_kernel(LoraArgs a, const f
     dA[((size_t)g * a.R + j) * a.kin + i] += (double)s;
 }
 
-// dx[p][i] += sum_j t[p][j] * A[g][j][i], i < width
+// dx[p][i] += sum_j t[p][j] * A[g][j][i], i < width; thread i takes
+// positions 8 blockIdx.y .. + 7 and keeps its column of A (up to 16 ranks) in
+// registers while the group stays the same.
+constexpr int kDxPositions = 8;
+
 __global__ __launch_bounds__(256) void lora_dx_kernel(LoraArgs a, const float *__restrict__ t,
                                                       float *__restrict__ dx, int ld_dx)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    const int p = blockIdx.y;
     if (i >= a.width) return;
-    const int g = a.pgroup ? a.pgroup[p] : 0;
-    const float *A = a.A + (size_t)g * a.R * a.kin + i;
-    const float *tp = t + (size_t)p * a.R;
-    float s = 0.f;
-    for (int j = 0; j < a.R; ++j) s = fmaf(tp[j], A[(size_t)j * a.kin], s);
-    dx[(size_t)p * ld_dx + i] += s;
+    const int pb = blockIdx.y * kDxPositions, pe = min(a.P, pb + kDxPositions);
+    int gcur = -1;
+    float ac[16];
+    for (int p = pb; p < pe; ++p) {
+        const int g = a.pgroup ? a.pgroup[p] : 0;
+        const float *A = a.A + (size_t)g * a.R * a.kin + i;
+        if (g != gcur) {  // uniform
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ac[j] = A[(size_t)min(j, a.R - 1) * a.kin];  // in bounds; j >= R unused
+            gcur = g;
+        }
+        const float *tp = t + (size_t)p * a.R;
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (j < a.R) s = fmaf(tp[j], ac[j], s);
+        for (int j = 16; j < a.R; ++j) s = fmaf(tp[j], A[(size_t)j * a.kin], s);
+        dx[(size_t)p * ld_dx + i] += s;
+    }
 }
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + __expf(-x)); }
@@ -561,7 +577,8 @@ hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, 
     hipLaunchKernelGGL(lora_t_kernel, dim3(a.P * ((a.R + kTRanks - 1) / kTRanks)), dim3(256), 0, s, a, grad, ld_g, t);
     hipLaunchKernelGGL(lora_grad_down_kernel, cols_grid(a.R * a.width, a.G), dim3(256), 0, s, a, t, in, ld_in,
                        in_tok, dA);
-    hipLaunchKernelGGL(lora_dx_kernel, cols_grid(a.width, a.P), dim3(256), 0, s, a, t, dx, ld_dx);
+    hipLaunchKernelGGL(lora_dx_kernel, dim3((a.width + 255) / 256, (a.P + kDxPositions - 1) / kDxPositions), dim3(256),
+                       0, s, a, t, dx, ld_dx);
     return hipGetLastError();
 }
 
