@@ -338,16 +338,15 @@ __global__ __launch_bounds__(256) void lora_grad_down_kernel(LoraArgs a, const f
 }
 
 // dx[p][i] += sum_j t[p][j] * A[g][j][i], i < width; thread i takes
-// positions 8 blockIdx.y .. + 7 and keeps its column of A (up to 16 ranks) in
-// registers while the group stays the same.
-constexpr int kDxPositions = 8;
-
+// positions pp blockIdx.y .. + pp - 1 and keeps its column of A (up to 16
+// ranks) in registers while the group stays the same (pp = 8 when there are
+// positions enough to fill the GPU that way, else 1).
 __global__ __launch_bounds__(256) void lora_dx_kernel(LoraArgs a, const float *__restrict__ t,
-                                                      float *__restrict__ dx, int ld_dx)
+                                                      float *__restrict__ dx, int ld_dx, int pp)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= a.width) return;
-    const int pb = blockIdx.y * kDxPositions, pe = min(a.P, pb + kDxPositions);
+    const int pb = blockIdx.y * pp, pe = min(a.P, pb + pp);
     int gcur = -1;
     float ac[16];
     for (int p = pb; p < pe; ++p) {
@@ -577,8 +576,9 @@ hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, 
     hipLaunchKernelGGL(lora_t_kernel, dim3(a.P * ((a.R + kTRanks - 1) / kTRanks)), dim3(256), 0, s, a, grad, ld_g, t);
     hipLaunchKernelGGL(lora_grad_down_kernel, cols_grid(a.R * a.width, a.G), dim3(256), 0, s, a, t, in, ld_in,
                        in_tok, dA);
-    hipLaunchKernelGGL(lora_dx_kernel, dim3((a.width + 255) / 256, (a.P + kDxPositions - 1) / kDxPositions), dim3(256),
-                       0, s, a, t, dx, ld_dx);
+    const int pp = (long long)((a.width + 255) / 256) * (a.P / 8) >= 1024 ? 8 : 1;
+    hipLaunchKernelGGL(lora_dx_kernel, dim3((a.width + 255) / 256, (a.P + pp - 1) / pp), dim3(256), 0, s, a, t, dx,
+                       ld_dx, pp);
     return hipGetLastError();
 }
 
