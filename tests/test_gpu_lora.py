@@ -55,13 +55,20 @@ CASES = {
     "hash routing": (32, 48, 6, 2, 1, FP4, 0.0, True, 11),
     "C2 int8 decode": (1024, 2048, 16, 2, 0, INT8, 0.0, False, 8),
     "C3 fp4 layer": (1024, 512, 64, 6, 1, FP4, 0.0, False, 64),
+    # many positions per group: the transposed product's eight-position
+    # tiles and dx's eight positions per thread
+    "many positions per expert": (1024, 128, 4, 1, 1, INT8, 0.0, False, 1024),
 }
+# adapter rank per case (4 unless listed): sixteen ranks take the float4 runs
+# of t = s g Up, five the scalar paths
+RANKS = {"many positions per expert": 16, "small fp4 two shared": 5, "clamped": 16}
 
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_adapter_forward_and_backward(ctx, name):
     d, h, E, k, S, prec, clamp, hashed, T = CASES[name]
-    rank, alpha = 4, 8.0
+    rank = RANKS.get(name, 4)
+    alpha = 2.0 * rank
     say(f"adapters {name}: d={d} h={h} E={E} k={k} S={S} precision={prec} T={T}")
     spec = make_moe(gt.encode_rows, d=d, h=h, E=E, k=k, S=S, precision=prec, seed=21, std=0.05, router_std=0.05,
                     bias_std=0.02, clamp=clamp, use_hash=hashed)
