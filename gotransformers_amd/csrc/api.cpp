@@ -213,7 +213,13 @@ struct TrainWorkspace {
     double *zero_bias = nullptr;     // [E]
     float *partial = nullptr;        // [chunks][P][max(dp, hp)] row-chunk sums of the transposed product
     int chunks = 1;                  // row chunks the partial buffer holds
-    int P = 0, ntiles_tr = 0, tile_tr = 4;
+    int4 *otiles = nullptr;          // [P/64 + G] position tiles of the adapter gradients
+    int32_t *otoff = nullptr;        // [G + 1] first tile of every group
+    int4 *rtiles = nullptr;          // [T/64 + 1] the router's token tiles
+    int32_t *rtoff = nullptr;        // {0, tiles}
+    float *outer = nullptr;          // [P/64 + G][R][max(dp, hp, E)] tile sums of the adapter gradients
+    int P = 0, ntiles_tr = 0, tile_tr = 4, notiles = 0, nrtiles = 0;
+    bool osingle = false;  // no group has more than one tile of otiles
 };
 
 struct gtmoe_layer {
@@ -1013,7 +1019,12 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
              [&] { return get(tw.lgf, (size_t)cap * E); }, [&] { return get(tw.dxr, (size_t)cap * dp); },
              [&] { return get(tw.pgroup, P); }, [&] { return get(tw.tiles_tr, P + L->G); },
              [&] { return get(tw.goff_router, (size_t)2); }, [&] { return get(tw.zero_bias, E); },
-             [&] { return get(tw.partial, (size_t)tw.chunks * P * std::max(hp, dp)); }}) {
+             [&] { return get(tw.partial, (size_t)tw.chunks * P * std::max(hp, dp)); },
+             [&] { return get(tw.otiles, P / lora_outer_tile_positions() + L->G); },
+             [&] { return get(tw.otoff, (size_t)L->G + 1); },
+             [&] { return get(tw.rtiles, (size_t)cap / lora_outer_tile_positions() + 1); },
+             [&] { return get(tw.rtoff, (size_t)2); },
+             [&] { return get(tw.outer, (P / lora_outer_tile_positions() + L->G) * R * std::max({hp, dp, E})); }}) {
         rc = step();
         if (rc != GTMOE_OK) {
             free_train_workspace(tw);
@@ -1026,7 +1037,9 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
     return GTMOE_OK;
 }
 
-LoraArgs lora_args(const AdapterSet &a, int P, const int32_t *pgroup, const int32_t *goff)
+LoraArgs lora_args(const AdapterSet &a, int P, const int32_t *pgroup, const int32_t *goff,
+                   const int4 *otiles = nullptr, const int32_t *otoff = nullptr, int notiles = 0,
+                   bool otile_single = false)
 {
     LoraArgs l{};
     l.A = a.A;
@@ -1040,6 +1053,10 @@ LoraArgs lora_args(const AdapterSet &a, int P, const int32_t *pgroup, const int3
     l.P = P;
     l.pgroup = pgroup;
     l.goff = goff;
+    l.otiles = otiles;
+    l.otoff = otoff;
+    l.notiles = notiles;
+    l.otile_single = otile_single;
     return l;
 }
 
@@ -1068,11 +1085,12 @@ RowsArgs rows_args(const DeviceMatrix &m, const float *in, int ld_in, const int3
 // Row chunks for the transposed product over `rows` rows: enough four-wave
 // workgroups for about four waves per SIMD (one chunk when the tiles alone
 // do that).
-int transposed_chunks(const gtmoe_layer *L, int rows, int ntiles, int colblocks)
+int transposed_chunks(const gtmoe_layer *L, int rows, int ntiles, int nblocks, int tile)
 {
-    const int busy = ntiles * colblocks;
+    const int busy = ntiles * rows_transposed_colblocks(nblocks, tile);
+    const int unit = rows_transposed_chunk_rows(tile);
     int want = (4 * L->ctx->compute_units + busy - 1) / std::max(busy, 1);
-    want = std::min(want, (rows + rows_transposed_chunk_rows() - 1) / rows_transposed_chunk_rows());
+    want = std::min(want, (rows + unit - 1) / unit);
     return std::max(1, std::min(want, L->tw.chunks));
 }
 
@@ -1112,18 +1130,32 @@ int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64
     HIP_TRY(ctx, hipStreamSynchronize(s));
     const int P = goff[G];
     if (P != T * (S + k)) return fail(ctx, GTMOE_ERR_DEVICE, "dispatch placed %d positions, expected %d", P, T * (S + k));
-    std::vector<int32_t> pgroup(P);
-    std::vector<int4> ttr;
-    const int bt = rows_transposed_tile(P, G);
+    std::vector<int32_t> pgroup(P), otoff(G + 1);
+    std::vector<int4> ttr, otr, rtr;
+    const int bt = rows_transposed_tile(P, G), ot = lora_outer_tile_positions();
     for (int g = 0; g < G; ++g) {
         for (int p = goff[g]; p < goff[g + 1]; ++p) pgroup[p] = g;
         for (int p = goff[g]; p < goff[g + 1]; p += bt) ttr.push_back(make_int4(g, p, std::min(bt, goff[g + 1] - p), 0));
+        otoff[g] = (int32_t)otr.size();
+        for (int p = goff[g]; p < goff[g + 1]; p += ot) otr.push_back(make_int4(g, p, std::min(ot, goff[g + 1] - p), 0));
     }
+    otoff[G] = (int32_t)otr.size();
+    bool osingle = true;
+    for (int g = 0; g < G; ++g) osingle = osingle && otoff[g + 1] - otoff[g] <= 1;
+    for (int p = 0; p < T; p += ot) rtr.push_back(make_int4(0, p, std::min(ot, T - p), 0));
+    const int32_t rtoff[2] = {0, (int32_t)rtr.size()};
     HIP_TRY(ctx, hipMemcpyAsync(tw.pgroup, pgroup.data(), sizeof(int32_t) * P, hipMemcpyHostToDevice, s));
     HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_tr, ttr.data(), sizeof(int4) * ttr.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(tw.otiles, otr.data(), sizeof(int4) * otr.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(tw.otoff, otoff.data(), sizeof(int32_t) * (G + 1), hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(tw.rtiles, rtr.data(), sizeof(int4) * rtr.size(), hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(tw.rtoff, rtoff, sizeof rtoff, hipMemcpyHostToDevice, s));
     tw.P = P;
     tw.ntiles_tr = (int)ttr.size();
     tw.tile_tr = bt;
+    tw.notiles = (int)otr.size();
+    tw.nrtiles = (int)rtr.size();
+    tw.osingle = osingle;
 
     // the bare products x W^T by the decode GEMV kernels (raw mode, over the
     // dispatch's slices), then the adapter terms and the biases
@@ -1215,13 +1247,14 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
     auto transposed = [&](const DeviceMatrix &m, const float *in, int ld_in, float *out, int ld_out) {
         RowsArgs r = rows_args(m, in, ld_in, nullptr, out, ld_out, tw.tiles_tr);
         r.tiles_positions = P;
-        const int chunks = transposed_chunks(L, m.rows, tw.ntiles_tr, (m.nblocks + 63) / 64);
+        const int chunks = transposed_chunks(L, m.rows, tw.ntiles_tr, m.nblocks, tw.tile_tr);
         return launch_rows_transposed(r, m.precision, tw.ntiles_tr, tw.tile_tr, chunks, tw.partial, s);
     };
     RUN(ctx, s, "rows_transposed", transposed(L->down, tw.eg, d, tw.hgrad, hp));
     RUN(ctx, s, "lora_backward",
-        launch_lora_backward(lora_args(L->ad_down, P, tw.pgroup, w.goff), tw.eg, d, tw.u_down, w.hidden32, hp,
-                             nullptr, tw.t, tw.hgrad, hp, L->ad_down.dA, L->ad_down.dB, s));
+        launch_lora_backward(lora_args(L->ad_down, P, tw.pgroup, w.goff, tw.otiles, tw.otoff, tw.notiles, tw.osingle), tw.eg, d,
+                             tw.u_down, w.hidden32, hp, nullptr, tw.t, tw.hgrad, hp, L->ad_down.dA, L->ad_down.dB,
+                             tw.outer, s));
     RUN(ctx, s, "swiglu_backward",
         launch_swiglu_backward(tw.hgrad, tw.gpre, tw.upre, P, L->h, hp, limit, tw.ggrad, tw.ugrad, s));
     struct Role {
@@ -1233,8 +1266,8 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
                           Role{L->up, L->ad_up, tw.ugrad, tw.u_up, tw.dxu}}) {
         RUN(ctx, s, "rows_transposed", transposed(r.m, r.grad, hp, r.dx, dp));
         RUN(ctx, s, "lora_backward",
-            launch_lora_backward(lora_args(r.a, P, tw.pgroup, w.goff), r.grad, hp, r.u, w.xf, dp, w.tok, tw.t, r.dx,
-                                 dp, r.a.dA, r.a.dB, s));
+            launch_lora_backward(lora_args(r.a, P, tw.pgroup, w.goff, tw.otiles, tw.otoff, tw.notiles, tw.osingle), r.grad, hp,
+                                 r.u, w.xf, dp, w.tok, tw.t, r.dx, dp, r.a.dA, r.a.dB, tw.outer, s));
     }
     RUN(ctx, s, "gather_input_grad", launch_gather_input_grad(tw.dxg, tw.dxu, dp, d, T, S, k, w.pos, tw.dx, s));
     if (!L->desc.use_hash_routing) {
@@ -1243,8 +1276,10 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
                                    tw.lgf, s));
         RUN(ctx, s, "router_input_grad", launch_router_input_grad(tw.lgf, T, E, L->router_w, dp, d, tw.dxr, dp, s));
         RUN(ctx, s, "lora_backward",
-            launch_lora_backward(lora_args(L->ad_router, T, nullptr, tw.goff_router), tw.lgf, E, tw.u_router, w.xf,
-                                 dp, nullptr, tw.t, tw.dxr, dp, L->ad_router.dA, L->ad_router.dB, s));
+            launch_lora_backward(lora_args(L->ad_router, T, nullptr, tw.goff_router, tw.rtiles, tw.rtoff, tw.nrtiles,
+                                           tw.nrtiles <= 1),
+                                 tw.lgf, E, tw.u_router, w.xf, dp, nullptr, tw.t, tw.dxr, dp, L->ad_router.dA,
+                                 L->ad_router.dB, tw.outer, s));
         RUN(ctx, s, "add_rows", launch_add_rows_f64(tw.dxr, dp, d, T, tw.dx, s));
     }
     HIP_TRY(ctx, hipMemcpyAsync(input_grads, tw.dx, sizeof(double) * T * d, hipMemcpyDeviceToHost, s));

@@ -136,6 +136,13 @@ struct LoraArgs {
     const float *A, *B, *scale;
     int R, kin, width, rows, G, P;
     const int32_t *pgroup, *goff;
+    // tiles of at most lora_outer_tile_positions() positions of one group
+    // (group, first position, positions, 0), every group's in position
+    // order, and the first tile of every group (otoff[G + 1])
+    const int4 *otiles;
+    const int32_t *otoff;
+    int notiles;
+    bool otile_single;  // no group has more than one tile
 };
 
 // Tokens per work slice of the GEMV path (the dispatch's tile size there).
@@ -249,17 +256,21 @@ hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t
 hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, int tile, int chunks, float *partial,
                                   hipStream_t s);
 int rows_transposed_tile(int positions, int groups);
-// smallest row chunk worth a workgroup of its own
-int rows_transposed_chunk_rows();
+// smallest row chunk worth a workgroup of its own, and workgroups across the
+// columns, for tiles of `tile` positions
+int rows_transposed_chunk_rows(int tile);
+int rows_transposed_colblocks(int nblocks, int tile);
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
                             hipStream_t s);
 hipError_t launch_lora_up_bias(const LoraArgs &a, const float *u, float *out, int ld_out, const float *bias,
                                hipStream_t s);
 hipError_t launch_lora_up_bias_f64(const LoraArgs &a, const float *u, double *out, int ld_out, const double *bias,
                                    hipStream_t s);
+// scratch: a.notiles * a.R * max(a.rows, a.width) floats
 hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, const float *u, const float *in,
                                 int ld_in, const int32_t *in_tok, float *t, float *dx, int ld_dx, double *dA,
-                                double *dB, hipStream_t s);
+                                double *dB, float *scratch, hipStream_t s);
+int lora_outer_tile_positions();
 hipError_t launch_swiglu_forward(const float *gpre, const float *upre, int P, int h, int hp, float limit,
                                  float *hidden, hipStream_t s);
 hipError_t launch_swiglu_backward(const float *hgrad, const float *gpre, const float *upre, int P, int h, int hp,

@@ -34,12 +34,8 @@ namespace {
 
 constexpr int kTrRows = 128;  // gradient rows staged per step
 
-__device__ __forceinline__ float fp4_value(uint32_t code)
-{
-    const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
-    const float v = mag[code & 7];
-    return (code & 8) ? -v : v;
-}
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // out[p][i] = sum_r grad[p][r] * W[r][i] for the group's rows r: the
 // reference's Rows.AddScaledRowTo over every row with scale grad[p][r]
@@ -75,9 +71,24 @@ __device__ __forceinline__ void decode_block(const uint4 (&q)[PREC == kFloat32 ?
 #pragma unroll
         for (int v = 0; v < 16; ++v) w[v] = (float)(int8_t)(d[v >> 2] >> (8 * (v & 3)));
     } else if constexpr (PREC == kFP4) {
-        const uint32_t d[2] = {q[0].x, q[0].y};
+        // e2m1 pairs, even value in the low nibble; the conversion's scale
+        // operand stays 1.0 (it only takes a power of two)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) w[v] = fp4_value(d[v >> 3] >> (4 * (v & 7)));
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t d = u ? q[0].y : q[0].x;
+            const f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
+            const f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
+            const f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
+            const f32x2 f3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3);
+            w[8 * u] = f0[0];
+            w[8 * u + 1] = f0[1];
+            w[8 * u + 2] = f1[0];
+            w[8 * u + 3] = f1[1];
+            w[8 * u + 4] = f2[0];
+            w[8 * u + 5] = f2[1];
+            w[8 * u + 6] = f3[0];
+            w[8 * u + 7] = f3[1];
+        }
     } else {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -170,6 +181,143 @@ __global__ __launch_bounds__(64 * kTrWaves) void rows_transposed_kernel(RowsArgs
     }
 }
 
+// The same product on the matrix cores, for groups of many positions:
+// out = G W with G the [positions][rows] gradients and W the group's
+// dequantized rows, as fp32 16x16x4 MFMAs (the products keep fp32 operands;
+// the only difference from the lane kernel is the summation order and that
+// the block scale multiplies the weight, (scale * value), before the
+// gradient does).  A workgroup takes kMtPositions positions of one tile,
+// kMtBlocks 16-column blocks and the rows [blockIdx.z * chunk_rows,
+// +chunk_rows) in steps of one 64-row panel: the block's codes and scales
+// are dequantized once into LDS as [column][row] and the gradients staged as
+// [position][row], so every lane reads four consecutive rows of its column
+// or position with one 16-byte LDS read (the four k of four MFMAs).  Wave w
+// owns blocks 2w and 2w+1 for all the positions: 2 x 2 accumulator tiles.
+// The next panel's loads are issued before the current panel's MFMAs.
+// Rows past the chunk and positions past the tile are staged as zeros.
+constexpr int kMtPositions = 32;
+constexpr int kMtBlocks = 8;
+constexpr int kMtRows = 64;
+constexpr int kMtPitch = kMtRows + 4;  // floats; a 16-lane b128 read then touches every bank once
+
+template <int PREC>
+__global__ __launch_bounds__(256) void rows_transposed_mfma_kernel(RowsArgs a, int chunk_rows,
+                                                                   float *__restrict__ partial,
+                                                                   long long partial_stride)
+{
+    __shared__ __attribute__((aligned(16))) float bs[kMtBlocks * 16][kMtPitch];
+    __shared__ __attribute__((aligned(16))) float as[kMtPositions][kMtPitch];
+    const int4 td = a.tiles[blockIdx.y];
+    const int g = td.x, p0 = td.y, m = td.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int b0 = blockIdx.x * kMtBlocks;
+    const char *codes = reinterpret_cast<const char *>(a.values) + (size_t)g * a.w_group_stride;
+    const float *sc = a.scales + (size_t)g * a.s_group_stride;
+    const int nbeg = blockIdx.z * chunk_rows, nend = min(a.rows, nbeg + chunk_rows);
+
+    // staging registers of thread (wave, lane): row n0 + lane of blocks
+    // b0 + wave + 4 j (j < 2), and row n0 + lane of positions wave + 4 j
+    // (j < 8).  Loads are unconditional at clamped indices (the panel's rows
+    // past the chunk repeat its last row), and what lies outside is zeroed
+    // after the load: the gradients always, the weights through a zero scale
+    // (their values are then finite) or, for fp32 rows, directly.
+    uint4 q[2][PREC == kFloat32 ? 4 : 1];
+    float s[2], x[8];
+    bool ok[2];
+    auto fetch = [&](int n0) {
+        const int rr = min(lane, nend - 1 - n0);  // row inside the panel
+        const bool row_ok = n0 + lane < nend;
+        const char *pc = codes + (size_t)(n0 >> 6) * 64 * a.row_bytes;
+        const float *ps = sc + (size_t)(n0 >> 6) * 64 * a.nblocks;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int b = min(b0 + wave + 4 * j, a.nblocks - 1);
+            ok[j] = row_ok && b0 + wave + 4 * j < a.nblocks;
+            if constexpr (PREC == kInt8) {
+                q[j][0] = *reinterpret_cast<const uint4 *>(pc + (size_t)b * 1024 + rr * 16);
+            } else if constexpr (PREC == kFP4) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(pc + (size_t)(b >> 1) * 1024 + rr * 16 + 8 * (b & 1));
+                q[j][0] = make_uint4(v.x, v.y, 0u, 0u);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    q[j][u] = *reinterpret_cast<const uint4 *>(pc + (size_t)(4 * b + u) * 1024 + rr * 16);
+            }
+            if constexpr (PREC != kFloat32) {
+                const float v = ps[(b >> 2) * 256 + rr * 4 + (b & 3)];
+                s[j] = ok[j] ? v : 0.f;
+            }
+        }
+        const float *col = a.in + n0 + rr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int qq = wave + 4 * j;
+            const float v = col[(size_t)(p0 + min(qq, m - 1)) * a.ld_in];
+            x[j] = row_ok && qq < m ? v : 0.f;
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int bb = wave + 4 * j;
+            float w[16];
+            decode_block<PREC>(q[j], w);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                bs[bb * 16 + v][lane] = PREC == kFloat32 ? (ok[j] ? w[v] : 0.f) : s[j] * w[v];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) as[wave + 4 * j][lane] = x[j];
+    };
+
+    const int li = lane & 15, kg = lane >> 4;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nbeg < nend) fetch(nbeg);
+    for (int n0 = nbeg; n0 < nend; n0 += kMtRows) {
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (n0 + kMtRows < nend) fetch(n0 + kMtRows);
+        const int steps = min(kMtRows, nend - n0 + 15) >> 4;
+        for (int st = 0; st < steps; ++st) {
+            const int c = 16 * st + 4 * kg;
+            f32x4 av[2], bv[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) av[mt] = *reinterpret_cast<const f32x4 *>(&as[16 * mt + li][c]);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+                bv[nt] = *reinterpret_cast<const f32x4 *>(&bs[16 * (2 * wave + nt) + li][c]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt][e], bv[nt][e], acc[mt][nt], 0, 0, 0);
+        }
+    }
+    // accumulator register v of lane l: position 4 (l / 16) + v of the
+    // 16-position tile, column l % 16 of the block
+    float *dst = gridDim.z == 1 ? a.out : partial + (size_t)blockIdx.z * partial_stride;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int b = b0 + 2 * wave + nt;
+        if (b >= a.nblocks) continue;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int qq = 16 * mt + 4 * kg + v;
+                if (qq < m) dst[(size_t)(p0 + qq) * a.ld_out + 16 * b + li] = acc[mt][nt][v];
+            }
+    }
+}
+
 // out[p][i] = sum over chunks c (in order) of partial[c][p][i], i < cols
 __global__ __launch_bounds__(256) void sum_chunks_kernel(const float *__restrict__ partial, long long stride,
                                                          int chunks, int cols, int ld, float *__restrict__ out)
@@ -250,18 +398,112 @@ __global__ __launch_bounds__(256) void lora_up_bias_kernel(LoraArgs a, const flo
     }
 }
 
-// dB[g][n][j] += scale[g] * sum_{p in g} grad[p][n] * u[p][j]
-__global__ __launch_bounds__(256) void lora_grad_up_kernel(LoraArgs a, const float *__restrict__ grad, int ld_g,
-                                                           const float *__restrict__ u, double *__restrict__ dB)
+// The adapter gradients are sums over each group's positions of outer
+// products: dB[g] += scale[g] * grad^T u and dA[g] += t^T in.  They run in
+// two steps.  lora_outer_kernel sums one tile of at most kOpPositions
+// positions of a group (tiles from the host, in position order):
+//   partial[tile][j][c] = sum over the tile's p of U[p][j] * V[row(p)][c]
+// for 16 ranks j (chunk blockIdx.z) and 64 columns c (blockIdx.x); wave w
+// takes positions p0 + w + 4 i, every lane keeps one column's 16 rank sums
+// (U's row is wave-uniform and comes through scalar loads), and the four
+// waves' sums are added in wave order through LDS.  lora_tiles_sum_kernel
+// then adds each group's tile partials in tile order, in float64, to the
+// accumulator; when every group is a single tile the outer kernel adds its
+// sums to the accumulator itself (each output has one writer).
+constexpr int kOpPositions = 64;
+
+struct OuterArgs {
+    const int4 *tiles;
+    const float *U;  // [positions][R]
+    int R;
+    const float *V;  // rows ld_v apart
+    int ld_v;
+    const int32_t *v_row;  // V's row of every position, or null for the position itself
+    int width;             // columns c
+    float *partial;        // [tiles][R][width], or null: add to dst directly
+    const float *scale;    // factor of group g, or null for 1
+    double *dst;           // dst[g * gs + j * js + c * cs]
+    long long gs, js, cs;
+};
+
+template <bool FULL>  // FULL: all 16 ranks of the chunk exist
+__device__ __forceinline__ void outer_tile(const float *__restrict__ U, int R, int j0, int p0, int m, int wave,
+                                           const float (&v)[16], float (&acc)[16])
 {
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int g = blockIdx.y;
-    if (idx >= a.rows * a.R) return;
-    const int n = idx / a.R, j = idx - n * a.R;
-    float s = 0.f;
-#pragma unroll 8
-    for (int p = a.goff[g]; p < a.goff[g + 1]; ++p) s = fmaf(grad[(size_t)p * ld_g + n], u[(size_t)p * a.R + j], s);
-    dB[(size_t)g * a.rows * a.R + idx] += (double)(a.scale[g] * s);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float *u = U + (size_t)(p0 + min(wave + 4 * i, m - 1)) * R + j0;
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) acc[jj] = fmaf(FULL ? u[jj] : u[min(jj, R - 1 - j0)], v[i], acc[jj]);
+    }
+}
+
+__global__ __launch_bounds__(256) void lora_outer_kernel(OuterArgs a)
+{
+    __shared__ float red[4][16][64];
+    const int4 td = a.tiles[blockIdx.y];
+    const int g = td.x, p0 = td.y, m = td.z;
+    const float *__restrict__ U = a.U;
+    const float *__restrict__ V = a.V;
+    const int R = a.R, width = a.width;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = blockIdx.x * 64 + lane, cc = min(c, width - 1);
+    const int j0 = blockIdx.z * 16;
+    float v[16], acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = min(wave + 4 * i, m - 1);
+        const int row = a.v_row ? a.v_row[p0 + k] : p0 + k;
+        const float x = V[(size_t)row * a.ld_v + cc];
+        v[i] = wave + 4 * i < m ? x : 0.f;  // positions past the tile add nothing
+        acc[i] = 0.f;
+    }
+    if (R - j0 >= 16)
+        outer_tile<true>(U, R, j0, p0, m, wave, v, acc);
+    else
+        outer_tile<false>(U, R, j0, p0, m, wave, v, acc);
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) red[wave][jj][lane] = acc[jj];
+    __syncthreads();
+    // wave w finishes ranks 4 w .. 4 w + 3
+    if (c >= width) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int jj = 4 * wave + e;
+        if (j0 + jj >= R) break;
+        const float t = ((red[0][jj][lane] + red[1][jj][lane]) + red[2][jj][lane]) + red[3][jj][lane];
+        if (a.partial) {
+            a.partial[((size_t)blockIdx.y * R + j0 + jj) * width + c] = t;
+        } else {
+            const double f = a.scale ? (double)a.scale[g] : 1.0;
+            a.dst[(size_t)g * a.gs + (size_t)(j0 + jj) * a.js + (size_t)c * a.cs] += f * (double)t;
+        }
+    }
+}
+
+// dst[g][j][c] (strides gs, js, cs) += factor * sum over the tiles
+// [toff[g], toff[g+1]) in order of partial[tile][j][c], factor = scale[g]
+// (or 1 without scales)
+__global__ __launch_bounds__(256) void lora_tiles_sum_kernel(OuterArgs a, const int32_t *__restrict__ toff)
+{
+    const int c = blockIdx.x * 256 + threadIdx.x, j = blockIdx.y, g = blockIdx.z;
+    if (c >= a.width) return;
+    double sum = 0.0;
+    for (int t = toff[g]; t < toff[g + 1]; ++t) sum += (double)a.partial[((size_t)t * a.R + j) * a.width + c];
+    if (a.scale) sum *= (double)a.scale[g];
+    a.dst[(size_t)g * a.gs + (size_t)j * a.js + (size_t)c * a.cs] += sum;
+}
+
+// dst += the sums of `o` over every group's tiles: one launch when no group
+// has more than one tile, else tile partials in scratch and their sum
+void launch_outer(OuterArgs o, int ntiles, int groups, bool single, const int32_t *toff, float *scratch,
+                  hipStream_t s)
+{
+    o.partial = single ? nullptr : scratch;
+    hipLaunchKernelGGL(lora_outer_kernel, dim3((o.width + 63) / 64, ntiles, (o.R + 15) / 16), dim3(256), 0, s, o);
+    if (o.partial)
+        hipLaunchKernelGGL(lora_tiles_sum_kernel, dim3((o.width + 255) / 256, o.R, groups), dim3(256), 0, s, o, toff);
 }
 
 // t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one workgroup per
@@ -316,25 +558,6 @@ __global__ __launch_bounds__(256) void lora_t_kernel(LoraArgs a, const float *__
     __syncthreads();
     if (wave == 0 && lane < kTRanks && j0 + lane < a.R)
         t[(size_t)p * a.R + j0 + lane] = a.scale[g] * (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
-}
-
-// dA[g][j][i] += sum_{p in g} t[p][j] * in[row(p)][i], i < width
-__global__ __launch_bounds__(256) void lora_grad_down_kernel(LoraArgs a, const float *__restrict__ t,
-                                                             const float *__restrict__ in, int ld_in,
-                                                             const int32_t *__restrict__ in_tok,
-                                                             double *__restrict__ dA)
-{
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int g = blockIdx.y;
-    if (idx >= a.R * a.width) return;
-    const int j = idx / a.width, i = idx - j * a.width;
-    float s = 0.f;
-#pragma unroll 8
-    for (int p = a.goff[g]; p < a.goff[g + 1]; ++p) {
-        const int row = in_tok ? in_tok[p] : p;
-        s = fmaf(t[(size_t)p * a.R + j], in[(size_t)row * ld_in + i], s);
-    }
-    dA[((size_t)g * a.R + j) * a.kin + i] += (double)s;
 }
 
 // dx[p][i] += sum_j t[p][j] * A[g][j][i], i < width; thread i takes
@@ -504,7 +727,9 @@ template <int PREC>
 void launch_transposed_prec(const RowsArgs &a, int tile, dim3 grid, int chunk_rows, float *partial, long long stride,
                             hipStream_t s)
 {
-    if (tile == 8)
+    if (tile == kMtPositions)
+        hipLaunchKernelGGL((rows_transposed_mfma_kernel<PREC>), grid, dim3(256), 0, s, a, chunk_rows, partial, stride);
+    else if (tile == 8)
         hipLaunchKernelGGL((rows_transposed_kernel<PREC, 8>), grid, dim3(64 * kTrWaves), 0, s, a, chunk_rows, partial,
                            stride);
     else
@@ -518,10 +743,16 @@ hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, 
                                   hipStream_t s)
 {
     if (ntiles <= 0) return hipSuccess;
-    if (chunks < 1 || (chunks > 1 && !partial) || (tile != 4 && tile != 8)) return hipErrorInvalidValue;
-    const int chunk_rows = (a.rows + chunks - 1) / chunks;
+    if (chunks < 1 || (chunks > 1 && !partial) || (tile != 4 && tile != 8 && tile != kMtPositions))
+        return hipErrorInvalidValue;
+    const bool mfma = tile == kMtPositions;
+    int chunk_rows = (a.rows + chunks - 1) / chunks;
+    if (mfma) {  // whole panels per chunk, and no empty chunk
+        chunk_rows = (chunk_rows + kMtRows - 1) / kMtRows * kMtRows;
+        chunks = (a.rows + chunk_rows - 1) / chunk_rows;
+    }
     const long long stride = (long long)a.tiles_positions * a.ld_out;
-    const dim3 grid((a.nblocks + 63) / 64, ntiles, chunks);
+    const dim3 grid(rows_transposed_colblocks(a.nblocks, tile), ntiles, chunks);
     switch (precision) {
     case kInt8: launch_transposed_prec<kInt8>(a, tile, grid, chunk_rows, partial, stride, s); break;
     case kFP4: launch_transposed_prec<kFP4>(a, tile, grid, chunk_rows, partial, stride, s); break;
@@ -534,11 +765,19 @@ hipError_t launch_rows_transposed(const RowsArgs &a, int precision, int ntiles, 
     return hipGetLastError();
 }
 
-// Positions per workgroup of the transposed product: eight once the groups
-// average eight positions (each decoded weight then feeds twice the
-// multiply-adds), else four.
-int rows_transposed_tile(int positions, int groups) { return positions >= 8 * groups ? 8 : 4; }
-int rows_transposed_chunk_rows() { return 32 * kTrWaves; }
+// Positions per workgroup of the transposed product: the matrix-core kernel's
+// 32 once the groups average 16 positions, eight once they average eight
+// (each decoded weight then feeds twice the multiply-adds), else four.
+int rows_transposed_tile(int positions, int groups)
+{
+    return positions >= 16 * groups ? kMtPositions : positions >= 8 * groups ? 8 : 4;
+}
+int lora_outer_tile_positions() { return kOpPositions; }
+int rows_transposed_chunk_rows(int tile) { return tile == kMtPositions ? kMtRows : 32 * kTrWaves; }
+int rows_transposed_colblocks(int nblocks, int tile)
+{
+    return tile == kMtPositions ? (nblocks + kMtBlocks - 1) / kMtBlocks : (nblocks + 63) / 64;
+}
 
 hipError_t launch_lora_down(const LoraArgs &a, const float *in, int ld_in, const int32_t *in_tok, float *u,
                             hipStream_t s)
@@ -569,13 +808,19 @@ hipError_t launch_lora_up_bias_f64(const LoraArgs &a, const float *u, double *ou
 
 hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, const float *u, const float *in,
                                 int ld_in, const int32_t *in_tok, float *t, float *dx, int ld_dx, double *dA,
-                                double *dB, hipStream_t s)
+                                double *dB, float *scratch, hipStream_t s)
 {
     if (a.P <= 0 || a.R <= 0) return hipSuccess;
-    hipLaunchKernelGGL(lora_grad_up_kernel, cols_grid(a.rows * a.R, a.G), dim3(256), 0, s, a, grad, ld_g, u, dB);
+    if (a.notiles <= 0 || !a.otiles || !a.otoff || !scratch) return hipErrorInvalidValue;
+    // dB += scale grad^T u: columns are B's rows n, the sums land at dB[g][n][j]
+    launch_outer(OuterArgs{a.otiles, u, a.R, grad, ld_g, nullptr, a.rows, nullptr, a.scale, dB,
+                           (long long)a.rows * a.R, 1LL, (long long)a.R},
+                 a.notiles, a.G, a.otile_single, a.otoff, scratch, s);
     hipLaunchKernelGGL(lora_t_kernel, dim3(a.P * ((a.R + kTRanks - 1) / kTRanks)), dim3(256), 0, s, a, grad, ld_g, t);
-    hipLaunchKernelGGL(lora_grad_down_kernel, cols_grid(a.R * a.width, a.G), dim3(256), 0, s, a, t, in, ld_in,
-                       in_tok, dA);
+    // dA += t^T in: columns are the inputs i, the sums land at dA[g][j][i]
+    launch_outer(OuterArgs{a.otiles, t, a.R, in, ld_in, in_tok, a.width, nullptr, nullptr, dA, (long long)a.R * a.kin,
+                           (long long)a.kin, 1LL},
+                 a.notiles, a.G, a.otile_single, a.otoff, scratch, s);
     const int pp = (long long)((a.width + 255) / 256) * (a.P / 8) >= 1024 ? 8 : 1;
     hipLaunchKernelGGL(lora_dx_kernel, dim3((a.width + 255) / 256, (a.P + pp - 1) / pp), dim3(256), 0, s, a, t, dx,
                        ld_dx, pp);

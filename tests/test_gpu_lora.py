@@ -55,9 +55,17 @@ CASES = {
     "hash routing": (32, 48, 6, 2, 1, FP4, 0.0, True, 11),
     "C2 int8 decode": (1024, 2048, 16, 2, 0, INT8, 0.0, False, 8),
     "C3 fp4 layer": (1024, 512, 64, 6, 1, FP4, 0.0, False, 64),
-    # many positions per group: the transposed product's eight-position
-    # tiles and dx's eight positions per thread
+    # many positions per group: the transposed product on the matrix cores
+    # (32-position tiles, the down layer's rows in sixteen chunks) and dx's
+    # eight positions per thread
     "many positions per expert": (1024, 128, 4, 1, 1, INT8, 0.0, False, 1024),
+    # the matrix-core product over FP4 rows with a partial last panel (d = 200
+    # rows of the down layer, its gradient rows 200 floats apart) and half a
+    # workgroup of column blocks (h = 40: four blocks)
+    "many positions fp4 ragged": (200, 40, 3, 2, 1, FP4, 0.0, False, 256),
+    "many positions float32": (48, 40, 2, 1, 0, FLOAT32, 0.0, False, 160),
+    # fourteen positions per group on average: eight-position tiles
+    "eight-position tiles": (96, 64, 8, 2, 0, INT8, 0.0, False, 56),
 }
 # adapter rank per case (4 unless listed): sixteen ranks take the float4 runs
 # of t = s g Up, five the scalar paths
