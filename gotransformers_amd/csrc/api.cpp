@@ -213,13 +213,18 @@ struct TrainWorkspace {
     double *zero_bias = nullptr;     // [E]
     float *partial = nullptr;        // [chunks][P][max(dp, hp)] row-chunk sums of the transposed product
     int chunks = 1;                  // row chunks the partial buffer holds
-    int4 *otiles = nullptr;          // [P/64 + G] position tiles of the adapter gradients
-    int32_t *otoff = nullptr;        // [G + 1] first tile of every group
-    int4 *rtiles = nullptr;          // [T/64 + 1] the router's token tiles
-    int32_t *rtoff = nullptr;        // {0, tiles}
-    float *outer = nullptr;          // [P/64 + G][R][max(dp, hp, E)] tile sums of the adapter gradients
-    int P = 0, ntiles_tr = 0, tile_tr = 4, notiles = 0, nrtiles = 0;
-    bool osingle = false;  // no group has more than one tile of otiles
+    // position tiles of the adapter gradients (LoraArgs::otiles) of the
+    // experts' groups and of the router's one group of tokens
+    struct OuterTiles {
+        int4 *tiles = nullptr;     // [P/64 + G]
+        int32_t *toff = nullptr;   // [G + 1] first tile of every group
+        int32_t *multi = nullptr;  // [G] groups of more than one tile
+        int n = 0, nmulti = 0;
+        std::vector<int4> host_tiles;  // sources of the uploads
+        std::vector<int32_t> host_toff, host_multi;
+    } ot, rt;
+    float *outer = nullptr;  // [P/64 + G][R][max(dp, hp, E)] tile sums of the adapter gradients
+    int P = 0, ntiles_tr = 0, tile_tr = 4;
 };
 
 struct gtmoe_layer {
@@ -1020,10 +1025,10 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
              [&] { return get(tw.pgroup, P); }, [&] { return get(tw.tiles_tr, P + L->G); },
              [&] { return get(tw.goff_router, (size_t)2); }, [&] { return get(tw.zero_bias, E); },
              [&] { return get(tw.partial, (size_t)tw.chunks * P * std::max(hp, dp)); },
-             [&] { return get(tw.otiles, P / lora_outer_tile_positions() + L->G); },
-             [&] { return get(tw.otoff, (size_t)L->G + 1); },
-             [&] { return get(tw.rtiles, (size_t)cap / lora_outer_tile_positions() + 1); },
-             [&] { return get(tw.rtoff, (size_t)2); },
+             [&] { return get(tw.ot.tiles, P / lora_outer_tile_positions() + L->G); },
+             [&] { return get(tw.ot.toff, (size_t)L->G + 1); }, [&] { return get(tw.ot.multi, (size_t)L->G); },
+             [&] { return get(tw.rt.tiles, (size_t)cap / lora_outer_tile_positions() + 1); },
+             [&] { return get(tw.rt.toff, (size_t)2); }, [&] { return get(tw.rt.multi, (size_t)1); },
              [&] { return get(tw.outer, (P / lora_outer_tile_positions() + L->G) * R * std::max({hp, dp, E})); }}) {
         rc = step();
         if (rc != GTMOE_OK) {
@@ -1038,8 +1043,7 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
 }
 
 LoraArgs lora_args(const AdapterSet &a, int P, const int32_t *pgroup, const int32_t *goff,
-                   const int4 *otiles = nullptr, const int32_t *otoff = nullptr, int notiles = 0,
-                   bool otile_single = false)
+                   const TrainWorkspace::OuterTiles *ot = nullptr)
 {
     LoraArgs l{};
     l.A = a.A;
@@ -1053,10 +1057,13 @@ LoraArgs lora_args(const AdapterSet &a, int P, const int32_t *pgroup, const int3
     l.P = P;
     l.pgroup = pgroup;
     l.goff = goff;
-    l.otiles = otiles;
-    l.otoff = otoff;
-    l.notiles = notiles;
-    l.otile_single = otile_single;
+    if (ot) {
+        l.otiles = ot->tiles;
+        l.otoff = ot->toff;
+        l.notiles = ot->n;
+        l.omulti = ot->multi;
+        l.nomulti = ot->nmulti;
+    }
     return l;
 }
 
@@ -1080,6 +1087,33 @@ RowsArgs rows_args(const DeviceMatrix &m, const float *in, int ld_in, const int3
     r.ld_out = ld_out;
     r.tiles = tiles;
     return r;
+}
+
+// Tiles of the adapter gradients over groups whose positions start at goff
+// (goff.size() - 1 groups), uploaded to `ot` (the host copies stay alive
+// until the stream has read them: the caller synchronizes before returning).
+int32_t upload_outer_tiles(gtmoe_context *ctx, const std::vector<int32_t> &goff, TrainWorkspace::OuterTiles &ot,
+                           hipStream_t s)
+{
+    const int G = (int)goff.size() - 1, n = lora_outer_tile_positions();
+    ot.host_tiles.clear();
+    ot.host_toff.assign(G + 1, 0);
+    ot.host_multi.clear();
+    for (int g = 0; g < G; ++g) {
+        ot.host_toff[g] = (int32_t)ot.host_tiles.size();
+        const int many = goff[g + 1] - goff[g] > n ? 1 : 0;
+        if (many) ot.host_multi.push_back(g);
+        for (int p = goff[g]; p < goff[g + 1]; p += n)
+            ot.host_tiles.push_back(make_int4(g, p, std::min(n, goff[g + 1] - p), many));
+    }
+    ot.host_toff[G] = (int32_t)ot.host_tiles.size();
+    ot.n = (int)ot.host_tiles.size();
+    ot.nmulti = (int)ot.host_multi.size();
+    HIP_TRY(ctx, hipMemcpyAsync(ot.tiles, ot.host_tiles.data(), sizeof(int4) * ot.n, hipMemcpyHostToDevice, s));
+    HIP_TRY(ctx, hipMemcpyAsync(ot.toff, ot.host_toff.data(), sizeof(int32_t) * (G + 1), hipMemcpyHostToDevice, s));
+    if (ot.nmulti)
+        HIP_TRY(ctx, hipMemcpyAsync(ot.multi, ot.host_multi.data(), sizeof(int32_t) * ot.nmulti, hipMemcpyHostToDevice, s));
+    return GTMOE_OK;
 }
 
 // Row chunks for the transposed product over `rows` rows: enough four-wave
@@ -1130,32 +1164,21 @@ int32_t adapter_forward(gtmoe_layer *L, int T, const double *inputs, const int64
     HIP_TRY(ctx, hipStreamSynchronize(s));
     const int P = goff[G];
     if (P != T * (S + k)) return fail(ctx, GTMOE_ERR_DEVICE, "dispatch placed %d positions, expected %d", P, T * (S + k));
-    std::vector<int32_t> pgroup(P), otoff(G + 1);
-    std::vector<int4> ttr, otr, rtr;
-    const int bt = rows_transposed_tile(P, G), ot = lora_outer_tile_positions();
+    std::vector<int32_t> pgroup(P);
+    std::vector<int4> ttr;
+    const int bt = rows_transposed_tile(P, G);
     for (int g = 0; g < G; ++g) {
         for (int p = goff[g]; p < goff[g + 1]; ++p) pgroup[p] = g;
         for (int p = goff[g]; p < goff[g + 1]; p += bt) ttr.push_back(make_int4(g, p, std::min(bt, goff[g + 1] - p), 0));
-        otoff[g] = (int32_t)otr.size();
-        for (int p = goff[g]; p < goff[g + 1]; p += ot) otr.push_back(make_int4(g, p, std::min(ot, goff[g + 1] - p), 0));
     }
-    otoff[G] = (int32_t)otr.size();
-    bool osingle = true;
-    for (int g = 0; g < G; ++g) osingle = osingle && otoff[g + 1] - otoff[g] <= 1;
-    for (int p = 0; p < T; p += ot) rtr.push_back(make_int4(0, p, std::min(ot, T - p), 0));
-    const int32_t rtoff[2] = {0, (int32_t)rtr.size()};
     HIP_TRY(ctx, hipMemcpyAsync(tw.pgroup, pgroup.data(), sizeof(int32_t) * P, hipMemcpyHostToDevice, s));
     HIP_TRY(ctx, hipMemcpyAsync(tw.tiles_tr, ttr.data(), sizeof(int4) * ttr.size(), hipMemcpyHostToDevice, s));
-    HIP_TRY(ctx, hipMemcpyAsync(tw.otiles, otr.data(), sizeof(int4) * otr.size(), hipMemcpyHostToDevice, s));
-    HIP_TRY(ctx, hipMemcpyAsync(tw.otoff, otoff.data(), sizeof(int32_t) * (G + 1), hipMemcpyHostToDevice, s));
-    HIP_TRY(ctx, hipMemcpyAsync(tw.rtiles, rtr.data(), sizeof(int4) * rtr.size(), hipMemcpyHostToDevice, s));
-    HIP_TRY(ctx, hipMemcpyAsync(tw.rtoff, rtoff, sizeof rtoff, hipMemcpyHostToDevice, s));
     tw.P = P;
     tw.ntiles_tr = (int)ttr.size();
     tw.tile_tr = bt;
-    tw.notiles = (int)otr.size();
-    tw.nrtiles = (int)rtr.size();
-    tw.osingle = osingle;
+    rc = upload_outer_tiles(ctx, goff, tw.ot, s);
+    if (rc == GTMOE_OK) rc = upload_outer_tiles(ctx, {0, T}, tw.rt, s);
+    if (rc != GTMOE_OK) return rc;
 
     // the bare products x W^T by the decode GEMV kernels (raw mode, over the
     // dispatch's slices), then the adapter terms and the biases
@@ -1252,7 +1275,7 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
     };
     RUN(ctx, s, "rows_transposed", transposed(L->down, tw.eg, d, tw.hgrad, hp));
     RUN(ctx, s, "lora_backward",
-        launch_lora_backward(lora_args(L->ad_down, P, tw.pgroup, w.goff, tw.otiles, tw.otoff, tw.notiles, tw.osingle), tw.eg, d,
+        launch_lora_backward(lora_args(L->ad_down, P, tw.pgroup, w.goff, &tw.ot), tw.eg, d,
                              tw.u_down, w.hidden32, hp, nullptr, tw.t, tw.hgrad, hp, L->ad_down.dA, L->ad_down.dB,
                              tw.outer, s));
     RUN(ctx, s, "swiglu_backward",
@@ -1266,7 +1289,7 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
                           Role{L->up, L->ad_up, tw.ugrad, tw.u_up, tw.dxu}}) {
         RUN(ctx, s, "rows_transposed", transposed(r.m, r.grad, hp, r.dx, dp));
         RUN(ctx, s, "lora_backward",
-            launch_lora_backward(lora_args(r.a, P, tw.pgroup, w.goff, tw.otiles, tw.otoff, tw.notiles, tw.osingle), r.grad, hp,
+            launch_lora_backward(lora_args(r.a, P, tw.pgroup, w.goff, &tw.ot), r.grad, hp,
                                  r.u, w.xf, dp, w.tok, tw.t, r.dx, dp, r.a.dA, r.a.dB, tw.outer, s));
     }
     RUN(ctx, s, "gather_input_grad", launch_gather_input_grad(tw.dxg, tw.dxu, dp, d, T, S, k, w.pos, tw.dx, s));
@@ -1276,8 +1299,7 @@ int32_t adapter_backward(gtmoe_layer *L, int T, const double *output_grads, doub
                                    tw.lgf, s));
         RUN(ctx, s, "router_input_grad", launch_router_input_grad(tw.lgf, T, E, L->router_w, dp, d, tw.dxr, dp, s));
         RUN(ctx, s, "lora_backward",
-            launch_lora_backward(lora_args(L->ad_router, T, nullptr, tw.goff_router, tw.rtiles, tw.rtoff, tw.nrtiles,
-                                           tw.nrtiles <= 1),
+            launch_lora_backward(lora_args(L->ad_router, T, nullptr, tw.goff_router, &tw.rt),
                                  tw.lgf, E, tw.u_router, w.xf, dp, nullptr, tw.t, tw.dxr, dp, L->ad_router.dA,
                                  L->ad_router.dB, tw.outer, s));
         RUN(ctx, s, "add_rows", launch_add_rows_f64(tw.dxr, dp, d, T, tw.dx, s));

@@ -137,12 +137,14 @@ struct LoraArgs {
     int R, kin, width, rows, G, P;
     const int32_t *pgroup, *goff;
     // tiles of at most lora_outer_tile_positions() positions of one group
-    // (group, first position, positions, 0), every group's in position
-    // order, and the first tile of every group (otoff[G + 1])
+    // (group, first position, positions, 1 if the group has more than one
+    // tile else 0), every group's in position order, the first tile of
+    // every group (otoff[G + 1]) and the groups of more than one tile
     const int4 *otiles;
     const int32_t *otoff;
     int notiles;
-    bool otile_single;  // no group has more than one tile
+    const int32_t *omulti;
+    int nomulti;
 };
 
 // Tokens per work slice of the GEMV path (the dispatch's tile size there).
@@ -266,7 +268,8 @@ hipError_t launch_lora_up_bias(const LoraArgs &a, const float *u, float *out, in
                                hipStream_t s);
 hipError_t launch_lora_up_bias_f64(const LoraArgs &a, const float *u, double *out, int ld_out, const double *bias,
                                    hipStream_t s);
-// scratch: a.notiles * a.R * max(a.rows, a.width) floats
+// scratch: a.notiles * a.R * max(a.rows, a.width) floats (unused when no
+// group has more than one tile)
 hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, const float *u, const float *in,
                                 int ld_in, const int32_t *in_tok, float *t, float *dx, int ld_dx, double *dA,
                                 double *dB, float *scratch, hipStream_t s);

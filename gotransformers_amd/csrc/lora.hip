@@ -399,17 +399,19 @@ __global__ __launch_bounds__(256) void lora_up_bias_kernel(LoraArgs a, const flo
 }
 
 // The adapter gradients are sums over each group's positions of outer
-// products: dB[g] += scale[g] * grad^T u and dA[g] += t^T in.  They run in
-// two steps.  lora_outer_kernel sums one tile of at most kOpPositions
-// positions of a group (tiles from the host, in position order):
-//   partial[tile][j][c] = sum over the tile's p of U[p][j] * V[row(p)][c]
-// for 16 ranks j (chunk blockIdx.z) and 64 columns c (blockIdx.x); wave w
-// takes positions p0 + w + 4 i, every lane keeps one column's 16 rank sums
-// (U's row is wave-uniform and comes through scalar loads), and the four
-// waves' sums are added in wave order through LDS.  lora_tiles_sum_kernel
-// then adds each group's tile partials in tile order, in float64, to the
-// accumulator; when every group is a single tile the outer kernel adds its
-// sums to the accumulator itself (each output has one writer).
+// products: dB[g] += scale[g] * grad^T u and dA[g] += t^T in.
+// lora_outer_kernel sums one tile of at most kOpPositions positions of a
+// group (tiles from the host, in position order):
+//   sum over the tile's p of U[p][j] * V[row(p)][c]
+// for 16 ranks j (chunk blockIdx.z) and 64 columns c (blockIdx.x).  The
+// tile's 16 ranks of U are staged in LDS (read back as wave-uniform
+// broadcasts), wave w takes positions p0 + w + 4 i with all sixteen of its
+// V loads issued together, every lane keeps one column's 16 rank sums, and
+// the four waves' sums are added in wave order through LDS.  A group of one
+// tile (descriptor .w == 0) adds its sums to the float64 accumulator
+// directly (each output has one writer); the tiles of larger groups write
+// partial[tile][j][c] and lora_tiles_sum_kernel adds them in tile order, in
+// float64, to the accumulator.
 constexpr int kOpPositions = 64;
 
 struct OuterArgs {
@@ -420,74 +422,89 @@ struct OuterArgs {
     int ld_v;
     const int32_t *v_row;  // V's row of every position, or null for the position itself
     int width;             // columns c
-    float *partial;        // [tiles][R][width], or null: add to dst directly
+    float *partial;        // [tiles][R][width] sums of the tiles of groups with more than one
     const float *scale;    // factor of group g, or null for 1
     double *dst;           // dst[g * gs + j * js + c * cs]
     long long gs, js, cs;
 };
 
-template <bool FULL>  // FULL: all 16 ranks of the chunk exist
-__device__ __forceinline__ void outer_tile(const float *__restrict__ U, int R, int j0, int p0, int m, int wave,
-                                           const float (&v)[16], float (&acc)[16])
-{
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float *u = U + (size_t)(p0 + min(wave + 4 * i, m - 1)) * R + j0;
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) acc[jj] = fmaf(FULL ? u[jj] : u[min(jj, R - 1 - j0)], v[i], acc[jj]);
-    }
-}
-
 __global__ __launch_bounds__(256) void lora_outer_kernel(OuterArgs a)
 {
     __shared__ float red[4][16][64];
+    __shared__ __attribute__((aligned(16))) float us[kOpPositions][16];
     const int4 td = a.tiles[blockIdx.y];
     const int g = td.x, p0 = td.y, m = td.z;
-    const float *__restrict__ U = a.U;
-    const float *__restrict__ V = a.V;
     const int R = a.R, width = a.width;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = blockIdx.x * 64 + lane, cc = min(c, width - 1);
     const int j0 = blockIdx.z * 16;
-    float v[16], acc[16];
+    // U rows of the tile, zero past the tile and past the rank (loads at
+    // clamped indices, all in flight together)
+    float uv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int i = threadIdx.x + 256 * e, q = i >> 4, jj = i & 15;
+        uv[e] = a.U[(size_t)(p0 + min(q, m - 1)) * R + min(j0 + jj, R - 1)];
+        if (q >= m || j0 + jj >= R) uv[e] = 0.f;
+    }
+    int row[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) row[i] = p0 + min(wave + 4 * i, m - 1);
+    if (a.v_row) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) row[i] = a.v_row[row[i]];
+    }
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = a.V[(size_t)row[i] * a.ld_v + cc];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int i = threadIdx.x + 256 * e;
+        us[i >> 4][i & 15] = uv[e];
+    }
+    __syncthreads();
+    float acc[16];
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) acc[jj] = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int k = min(wave + 4 * i, m - 1);
-        const int row = a.v_row ? a.v_row[p0 + k] : p0 + k;
-        const float x = V[(size_t)row * a.ld_v + cc];
-        v[i] = wave + 4 * i < m ? x : 0.f;  // positions past the tile add nothing
-        acc[i] = 0.f;
+        if (wave + 4 * i >= m) break;  // wave-uniform; positions past the tile add nothing
+        const float4 *u4 = reinterpret_cast<const float4 *>(us[wave + 4 * i]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float4 u = u4[e];
+            acc[4 * e] = fmaf(u.x, v[i], acc[4 * e]);
+            acc[4 * e + 1] = fmaf(u.y, v[i], acc[4 * e + 1]);
+            acc[4 * e + 2] = fmaf(u.z, v[i], acc[4 * e + 2]);
+            acc[4 * e + 3] = fmaf(u.w, v[i], acc[4 * e + 3]);
+        }
     }
-    if (R - j0 >= 16)
-        outer_tile<true>(U, R, j0, p0, m, wave, v, acc);
-    else
-        outer_tile<false>(U, R, j0, p0, m, wave, v, acc);
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) red[wave][jj][lane] = acc[jj];
     __syncthreads();
     // wave w finishes ranks 4 w .. 4 w + 3
     if (c >= width) return;
+    const double f = td.w == 0 && a.scale ? (double)a.scale[g] : 1.0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int jj = 4 * wave + e;
         if (j0 + jj >= R) break;
         const float t = ((red[0][jj][lane] + red[1][jj][lane]) + red[2][jj][lane]) + red[3][jj][lane];
-        if (a.partial) {
+        if (td.w)
             a.partial[((size_t)blockIdx.y * R + j0 + jj) * width + c] = t;
-        } else {
-            const double f = a.scale ? (double)a.scale[g] : 1.0;
+        else
             a.dst[(size_t)g * a.gs + (size_t)(j0 + jj) * a.js + (size_t)c * a.cs] += f * (double)t;
-        }
     }
 }
 
 // dst[g][j][c] (strides gs, js, cs) += factor * sum over the tiles
 // [toff[g], toff[g+1]) in order of partial[tile][j][c], factor = scale[g]
-// (or 1 without scales)
-__global__ __launch_bounds__(256) void lora_tiles_sum_kernel(OuterArgs a, const int32_t *__restrict__ toff)
+// (or 1 without scales), for the groups g = multi[blockIdx.z]
+__global__ __launch_bounds__(256) void lora_tiles_sum_kernel(OuterArgs a, const int32_t *__restrict__ toff,
+                                                             const int32_t *__restrict__ multi)
 {
-    const int c = blockIdx.x * 256 + threadIdx.x, j = blockIdx.y, g = blockIdx.z;
+    const int c = blockIdx.x * 256 + threadIdx.x, j = blockIdx.y, g = multi[blockIdx.z];
     if (c >= a.width) return;
     double sum = 0.0;
     for (int t = toff[g]; t < toff[g + 1]; ++t) sum += (double)a.partial[((size_t)t * a.R + j) * a.width + c];
@@ -495,15 +512,14 @@ __global__ __launch_bounds__(256) void lora_tiles_sum_kernel(OuterArgs a, const 
     a.dst[(size_t)g * a.gs + (size_t)j * a.js + (size_t)c * a.cs] += sum;
 }
 
-// dst += the sums of `o` over every group's tiles: one launch when no group
-// has more than one tile, else tile partials in scratch and their sum
-void launch_outer(OuterArgs o, int ntiles, int groups, bool single, const int32_t *toff, float *scratch,
-                  hipStream_t s)
+// dst += the sums of `o` over every group's tiles
+void launch_outer(OuterArgs o, const LoraArgs &a, float *scratch, hipStream_t s)
 {
-    o.partial = single ? nullptr : scratch;
-    hipLaunchKernelGGL(lora_outer_kernel, dim3((o.width + 63) / 64, ntiles, (o.R + 15) / 16), dim3(256), 0, s, o);
-    if (o.partial)
-        hipLaunchKernelGGL(lora_tiles_sum_kernel, dim3((o.width + 255) / 256, o.R, groups), dim3(256), 0, s, o, toff);
+    o.partial = scratch;
+    hipLaunchKernelGGL(lora_outer_kernel, dim3((o.width + 63) / 64, a.notiles, (o.R + 15) / 16), dim3(256), 0, s, o);
+    if (a.nomulti > 0)
+        hipLaunchKernelGGL(lora_tiles_sum_kernel, dim3((o.width + 255) / 256, o.R, a.nomulti), dim3(256), 0, s, o,
+                           a.otoff, a.omulti);
 }
 
 // t[p][j] = scale[g] * sum_n grad[p][n] * B[g][n][j]; one workgroup per
@@ -811,16 +827,17 @@ hipError_t launch_lora_backward(const LoraArgs &a, const float *grad, int ld_g, 
                                 double *dB, float *scratch, hipStream_t s)
 {
     if (a.P <= 0 || a.R <= 0) return hipSuccess;
-    if (a.notiles <= 0 || !a.otiles || !a.otoff || !scratch) return hipErrorInvalidValue;
+    if (a.notiles <= 0 || !a.otiles || !a.otoff || (a.nomulti > 0 && (!a.omulti || !scratch)))
+        return hipErrorInvalidValue;
     // dB += scale grad^T u: columns are B's rows n, the sums land at dB[g][n][j]
     launch_outer(OuterArgs{a.otiles, u, a.R, grad, ld_g, nullptr, a.rows, nullptr, a.scale, dB,
                            (long long)a.rows * a.R, 1LL, (long long)a.R},
-                 a.notiles, a.G, a.otile_single, a.otoff, scratch, s);
+                 a, scratch, s);
     hipLaunchKernelGGL(lora_t_kernel, dim3(a.P * ((a.R + kTRanks - 1) / kTRanks)), dim3(256), 0, s, a, grad, ld_g, t);
     // dA += t^T in: columns are the inputs i, the sums land at dA[g][j][i]
     launch_outer(OuterArgs{a.otiles, t, a.R, in, ld_in, in_tok, a.width, nullptr, nullptr, dA, (long long)a.R * a.kin,
                            (long long)a.kin, 1LL},
-                 a.notiles, a.G, a.otile_single, a.otoff, scratch, s);
+                 a, scratch, s);
     const int pp = (long long)((a.width + 255) / 256) * (a.P / 8) >= 1024 ? 8 : 1;
     hipLaunchKernelGGL(lora_dx_kernel, dim3((a.width + 255) / 256, (a.P + pp - 1) / pp), dim3(256), 0, s, a, t, dx,
                        ld_dx, pp);
