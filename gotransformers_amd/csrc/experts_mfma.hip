@@ -207,35 +207,25 @@ __device__ __forceinline__ void store_tile(const MfmaArgs &a, const uint16_t *os
 
 }  // namespace
 
-template <int PREC, bool GATEUP>
-__global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
+// One tile whose positions lie in its first MI 32-row blocks (M <= 32 MI):
+// the blocks past them are neither loaded nor multiplied.
+template <int PREC, bool GATEUP, int MI>
+__device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][BM][LDA], int g, int p0, int M,
+                                          int ntile)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDA];
-
-    const int j8 = blockIdx.x >> 3;
-    const int ntiles = *a.count;
-    const int per_xcd = (ntiles + 7) >> 3;
-    const int tile = (blockIdx.x & 7) * per_xcd + j8 / a.ntiles_n;
-    const int ntile = j8 % a.ntiles_n;
-    if (j8 / a.ntiles_n >= per_xcd || tile >= ntiles) return;
-    const int4 dsc = a.desc[tile];
-    const int g = dsc.x;
-    const int p0 = dsc.y;  // first position of the tile
-    const int M = dsc.z;   // positions in the tile
-
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, h = lane >> 5;
 
-    // activations: thread t -> rows t/8 + 32i (i < 4), 8 values at 8 (t % 8)
+    // activations: thread t -> rows t/8 + 32i (i < MI), 8 values at 8 (t % 8)
     // of the K step, so that eight lanes read a row's whole 128-byte piece
     // per load (a wave touches 8 cache lines per load, not 32 partly); rows
     // past the tile read past the buffer and get zeros
     const int ar = tid >> 3, ac = tid & 7;
     const __amdgpu_buffer_rsrc_t asrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(a.a), 0, (int)(a.a_rows * a.lda * 2), kRawBufferWord3);
-    uint32_t aoff[4];
+    uint32_t aoff[MI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MI; ++i) {
         const int r = ar + 32 * i;
         aoff[i] = r < M ? ((uint32_t)(GATEUP ? a.tok[p0 + r] : p0 + r) * (uint32_t)a.lda + ac * 8) * 2u : 0x80000000u;
     }
@@ -269,9 +259,9 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
         }
     }
 
-    floatx16 acc[4][2];
+    floatx16 acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -286,12 +276,12 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     // stage's loads alone, and a scheduling barrier keeps the refill of a
     // stage behind the instructions that consume it.
     const int nsteps = a.kp / BK;
-    uint4 av[2][4];
+    uint4 av[2][MI];
     BRaw<PREC> bq[2][2];  // [stage][column tile]
-    auto load_a = [&](uint4 (&v)[4], int step) {
+    auto load_a = [&](uint4 (&v)[MI], int step) {
         const int k0 = min(step, nsteps - 1) * BK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
             v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(asrc, aoff[i], k0 * 2, 0));
     };
     auto load_b = [&](BRaw<PREC> (&q)[2], int step) {
@@ -304,15 +294,16 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             load_scales<PREC>(q[j], bsrc[j], bvs[j], m);
         }
     };
-    auto store_a = [&](int buf, const uint4 (&v)[4]) {
+    auto store_a = [&](int buf, const uint4 (&v)[MI]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4 *>(&As[buf][ar + 32 * i][ac * 8]) = v[i];
+        for (int i = 0; i < MI; ++i) *reinterpret_cast<uint4 *>(&As[buf][ar + 32 * i][ac * 8]) = v[i];
     };
     // The K step is done in two halves (pair p = 0, 1: 16 MFMAs each, K
     // values of scale blocks 2p and 2p + 1).  While the MFMAs of one half run,
     // the same wave dequantizes the B operands of the next half, so the VALU
     // work hides under the matrix cores: the scheduling groups below ask for
-    // one MFMA, then four VALU instructions, in turn.
+    // one MFMA, then a share of the VALU instructions (four with all four
+    // row blocks), in turn.
     auto dequant_pair = [&](const BRaw<PREC> (&q)[2], int p, bf16x8 (&out)[2][2]) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -325,11 +316,11 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             // k-values of this MFMA step: lanes of half h carry values
             // 8s2..8s2+7 of block 2p + h (FP4: 2h + p) of the K step
             const int kk = 16 * (PREC == kFP4 ? 2 * h + p : 2 * p + h) + 8 * s2;
-            bf16x8 af[4];
+            bf16x8 af[MI];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][i * 32 + col][kk]);
+            for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][i * 32 + col][kk]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfp[j][s2], acc[i][j], 0, 0, 0);
@@ -338,11 +329,11 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     auto interleave = [&]() {
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the LDS reads of the A operands
+            __builtin_amdgcn_sched_group_barrier(0x100, MI, 0);  // the LDS reads of the A operands
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+            for (int m = 0; m < 2 * MI; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, (16 + MI - 1) / MI, 0);  // VALU
             }
         }
     };
@@ -410,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
                 return silu(gv) * uv;
             };
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; r += 2)
                     put(i, r, c,
@@ -431,7 +422,7 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             const float bd = n < a.n ? a.b0[(size_t)g * a.n + n] : 0.f;
             const int c = wave * 32 + col;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) put(i, r, c, pack_bf16(acc[i][j][r] + bd, acc[i][j][r + 1] + bd));
             __syncthreads();
@@ -439,6 +430,32 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
             if (j == 0) __syncthreads();  // the next pass rewrites the LDS tile
         }
     }
+}
+
+template <int PREC, bool GATEUP>
+__global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDA];
+
+    const int j8 = blockIdx.x >> 3;
+    const int ntiles = *a.count;
+    const int per_xcd = (ntiles + 7) >> 3;
+    const int tile = (blockIdx.x & 7) * per_xcd + j8 / a.ntiles_n;
+    const int ntile = j8 % a.ntiles_n;
+    if (j8 / a.ntiles_n >= per_xcd || tile >= ntiles) return;
+    const int4 dsc = a.desc[tile];
+    const int g = dsc.x;
+    const int p0 = dsc.y;  // first position of the tile
+    const int M = dsc.z;   // positions in the tile
+    // an expert's last tile is usually partly filled: multiply only the
+    // 32-row blocks that hold positions (fewer than three run as two: the
+    // dequantization, the same for any M, then bounds the time anyway)
+    if (M > 96)
+        gemm_tile<PREC, GATEUP, 4>(a, As, g, p0, M, ntile);
+    else if (M > 64)
+        gemm_tile<PREC, GATEUP, 3>(a, As, g, p0, M, ntile);
+    else
+        gemm_tile<PREC, GATEUP, 2>(a, As, g, p0, M, ntile);
 }
 
 int mfma_tile_m() { return BM; }
