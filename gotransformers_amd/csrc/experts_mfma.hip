@@ -49,7 +49,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int BM = 128;    // positions per tile
 constexpr int BN = 256;    // weight rows per tile (gate/up: 128 neurons x 2)
 constexpr int BK = 64;     // K per pipeline step (4 scale blocks)
-constexpr int LDA = BK + 8;  // LDS row stride in bf16 (144 bytes)
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -170,19 +169,21 @@ __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h
     return __builtin_bit_cast(bf16x8, o);
 }
 
-// The output tile in LDS: 128 rows of 128 bf16 columns, row stride OLD
-// (68 words: the rows m and m + 4 that one ds_write covers fall on disjoint
-// banks).
+// The output tile in LDS: two halves of 64 rows, one activation buffer each,
+// of 128 bf16 columns, row stride OLD (68 words: the rows m and m + 4 that
+// one ds_write covers fall on disjoint banks).  An activation buffer holds
+// one K step of the tile (128 rows of 128 bytes) or one output half.
 constexpr int OLD = 136;
-static_assert(BM * OLD <= 2 * BM * LDA, "the output tile fits in the activation buffers");
+constexpr int kBufBytes = 64 * OLD * 2 > BM * BK * 2 ? 64 * OLD * 2 : BM * BK * 2;
 
-// Rows [0, M) of the LDS output tile to out rows p0 + m; tile column c goes
-// to output column col_of(c) (groups of 8 tile columns map to 8 consecutive
-// output columns).  Thread t stores the 16-byte pieces t + 256 i (row
-// piece / 16, columns 8 (piece % 16) ..).  Widths or strides that are not
-// multiples of 8 columns take 2-byte stores.
+// Rows [0, M) of the LDS output tile (row m at os[m / 64] + (m % 64) OLD)
+// to out rows p0 + m; tile column c goes to output column col_of(c) (groups
+// of 8 tile columns map to 8 consecutive output columns).  Thread t stores
+// the 16-byte pieces t + 256 i (row piece / 16, columns 8 (piece % 16) ..).
+// Widths or strides that are not multiples of 8 columns take 2-byte stores.
 template <typename ColOf>
-__device__ __forceinline__ void store_tile(const MfmaArgs &a, const uint16_t *os, int p0, int M, ColOf col_of)
+__device__ __forceinline__ void store_tile(const MfmaArgs &a, const uint16_t *os0, const uint16_t *os1, int p0, int M,
+                                           ColOf col_of)
 {
     uint16_t *out = reinterpret_cast<uint16_t *>(a.out);
     const int tid = threadIdx.x;
@@ -192,42 +193,56 @@ __device__ __forceinline__ void store_tile(const MfmaArgs &a, const uint16_t *os
             const int piece = tid + 256 * i;
             const int m = piece >> 4, c = (piece & 15) * 8;
             const int n = col_of(c);
+            const uint16_t *os = i < BM * 8 / 256 ? os0 : os1;  // rows 16 i + tid / 16
             if (m < M && n < a.n)
                 *reinterpret_cast<uint4 *>(out + (size_t)(p0 + m) * a.ldo + n) =
-                    *reinterpret_cast<const uint4 *>(os + m * OLD + c);
+                    *reinterpret_cast<const uint4 *>(os + (m & 63) * OLD + c);
         }
     } else {
         for (int e = tid; e < BM * 128; e += 256) {
             const int m = e >> 7, c = e & 127;
             const int n = col_of(c);
-            if (m < M && n < a.n) out[(size_t)(p0 + m) * a.ldo + n] = os[m * OLD + c];
+            if (m < M && n < a.n) out[(size_t)(p0 + m) * a.ldo + n] = (m < 64 ? os0 : os1)[(m & 63) * OLD + c];
         }
     }
+}
+
+template <int S>
+__device__ __forceinline__ char *pick(char *b0, char *b1, char *b2)
+{
+    return S == 0 ? b0 : S == 1 ? b1 : b2;
 }
 
 }  // namespace
 
 // One tile whose positions lie in its first MI 32-row blocks (M <= 32 MI):
-// the blocks past them are neither loaded nor multiplied.
+// the blocks past them are neither loaded nor multiplied.  b0, b1, b2: the
+// three activation buffers (kBufBytes of LDS each, separate arrays, so that
+// the compiler tells their accesses apart).
 template <int PREC, bool GATEUP, int MI>
-__device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][BM][LDA], int g, int p0, int M,
+__device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1, char *b2, int g, int p0, int M,
                                           int ntile)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, h = lane >> 5;
 
-    // activations: thread t -> rows t/8 + 32i (i < MI), 8 values at 8 (t % 8)
-    // of the K step, so that eight lanes read a row's whole 128-byte piece
-    // per load (a wave touches 8 cache lines per load, not 32 partly); rows
-    // past the tile read past the buffer and get zeros
-    const int ar = tid >> 3, ac = tid & 7;
+    // activations go from memory straight into LDS (16-byte LDS-DMA loads,
+    // no registers): per K step, row block i < MI of the tile is four wave
+    // loads, wave w taking rows 32 i + 8 w .. + 7, lane l writing 16 bytes
+    // at row 32 i + 8 w + l / 8, slot l % 8 of the step's buffer.  A row is
+    // 128 bytes (64 bf16 of K); slot s of row R holds K values
+    // 8 (s ^ R % 8) .. + 7, so the 32 rows that one operand read takes fall
+    // on distinct banks.  Rows past M read past the buffer and get zeros.
     const __amdgpu_buffer_rsrc_t asrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(a.a), 0, (int)(a.a_rows * a.lda * 2), kRawBufferWord3);
+    const int arow = lane >> 3, achunk = (lane & 7) ^ arow;  // R % 8 == arow
     uint32_t aoff[MI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-        const int r = ar + 32 * i;
-        aoff[i] = r < M ? ((uint32_t)(GATEUP ? a.tok[p0 + r] : p0 + r) * (uint32_t)a.lda + ac * 8) * 2u : 0x80000000u;
+        const int r = 32 * i + 8 * wave + arow;
+        aoff[i] = r < M ? ((uint32_t)(GATEUP ? a.tok[p0 + r] : p0 + r) * (uint32_t)a.lda + achunk * 8) * 2u
+                        : 0x80000000u;
     }
 
     // weights: the wave's two column tiles (gate/up: the same 32 neurons of
@@ -267,22 +282,41 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // Software pipeline of distance 2: during step k the loads of step k+2
-    // are in flight (A into registers av[k % 2], B into bq[k % 2]) and A of
-    // step k+1 waits in av[(k+1) % 2] to be stored to LDS at the end of the
-    // step.  The loop is unrolled by two so the stage indices are constants;
-    // every load is issued unconditionally (steps past the end re-load the
-    // last step: cache hits, never used) so that the compiler waits for each
-    // stage's loads alone, and a scheduling barrier keeps the refill of a
-    // stage behind the instructions that consume it.
+    // Software pipeline: during step k the activations of step k + 2 are
+    // on their way into LDS buffer (k + 2) % 3 (buffer (k + 2) % 3 was read
+    // in step k - 1, before the barrier that ended it) and the weights of
+    // step k + NS into register stage k % NS (its pair 1 is dequantized at
+    // the start of step k): NS = 3 stages, or 2 for fp32 rows, whose stages
+    // are four times larger.  The loop is unrolled by three (six for two
+    // stages) so the buffer and stage indices are constants; every load is
+    // issued unconditionally (steps past the end re-load the last step:
+    // cache hits, never used), so that each step issues the same VMEM
+    // instructions in the same order: MI activation loads, then NB weight
+    // loads.  Step k ends once the activations of step k + 1 have landed:
+    // each wave waits until at most the VMEM instructions issued after its
+    // own loads of them are pending (2 NB + MI: one step's weights, then the
+    // activations and the weights of step k) and the barrier makes every
+    // wave's rows visible.  Scheduling barriers keep that order.
     const int nsteps = a.kp / BK;
-    uint4 av[2][MI];
-    BRaw<PREC> bq[2][2];  // [stage][column tile]
-    auto load_a = [&](uint4 (&v)[MI], int step) {
+    constexpr int NS = PREC == kFloat32 ? 2 : 3;
+    constexpr int UNROLL = NS == 3 ? 3 : 6;
+    BRaw<PREC> bq[NS][2];  // [stage][column tile]
+    constexpr int NB = PREC == kInt8 ? 6 : PREC == kFP4 ? 4 : 16;
+    constexpr int VM = 2 * NB + MI;
+    static_assert(VM < 64, "vmcnt holds six bits");
+    // s_waitcnt vmcnt(n) lgkmcnt(0), expcnt not waited for
+    constexpr auto vm_wait = [](int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); };
+    constexpr int kStepWait = vm_wait(VM);
+    // after the prologue's activations of step 0: the weights of step 1 and
+    // the activations of step 1, and with three stages the weights of step 2
+    constexpr int kPrologueWait = vm_wait(NS == 3 ? VM : NB + MI);
+    auto dma_a = [&](char *buf, int step) {
         const int k0 = min(step, nsteps - 1) * BK;
 #pragma unroll
         for (int i = 0; i < MI; ++i)
-            v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(asrc, aoff[i], k0 * 2, 0));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                asrc, (__attribute__((address_space(3))) void *)(buf + (32 * i + 8 * wave) * 128), 16, aoff[i],
+                k0 * 2, 0, 0);
     };
     auto load_b = [&](BRaw<PREC> (&q)[2], int step) {
         const int m = min(step, nsteps - 1);
@@ -294,9 +328,11 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
             load_scales<PREC>(q[j], bsrc[j], bvs[j], m);
         }
     };
-    auto store_a = [&](int buf, const uint4 (&v)[MI]) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i) *reinterpret_cast<uint4 *>(&As[buf][ar + 32 * i][ac * 8]) = v[i];
+    auto end_step = [&](auto wait_tag) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(decltype(wait_tag)::value);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
     };
     // The K step is done in two halves (pair p = 0, 1: 16 MFMAs each, K
     // values of scale blocks 2p and 2p + 1).  While the MFMAs of one half run,
@@ -310,15 +346,17 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) out[j][s2] = dequant_half<PREC>(q[j], p, s2);
     };
-    auto mfma_pair = [&](int buf, int p, const bf16x8 (&bfp)[2][2]) {
+    auto mfma_pair = [&](const char *buf, int p, const bf16x8 (&bfp)[2][2]) {
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             // k-values of this MFMA step: lanes of half h carry values
-            // 8s2..8s2+7 of block 2p + h (FP4: 2h + p) of the K step
-            const int kk = 16 * (PREC == kFP4 ? 2 * h + p : 2 * p + h) + 8 * s2;
+            // 8s2..8s2+7 of block 2p + h (FP4: 2h + p) of the K step, which
+            // is K chunk 2 block + s2, in slot chunk ^ (row % 8)
+            const int chunk = 2 * (PREC == kFP4 ? 2 * h + p : 2 * p + h) + s2;
+            const int so = 16 * (chunk ^ (col & 7));
             bf16x8 af[MI];
 #pragma unroll
-            for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][i * 32 + col][kk]);
+            for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(buf + (32 * i + col) * 128 + so);
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -332,57 +370,88 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
             __builtin_amdgcn_sched_group_barrier(0x100, MI, 0);  // the LDS reads of the A operands
 #pragma unroll
             for (int m = 0; m < 2 * MI; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // one MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, (16 + MI - 1) / MI, 0);  // VALU
             }
         }
     };
     bf16x8 bfa[2][2], bfb[2][2];  // B operands of the current and the next half step
-    // step k of the pipeline (ST = k % 2); bfa holds pair 0 of step k
-    auto step = [&](auto st_tag, int k) {
-        constexpr int ST = decltype(st_tag)::value;
-        // av[ST] went to LDS at the end of the previous step: its refill
-        // goes first, two whole steps ahead of its own store
-        load_a(av[ST], k + 2);
+    // step k of the pipeline (U = k % UNROLL); bfa holds pair 0 of step k.
+    // The last steps, after the loop, wait for all their loads instead: the
+    // compiler drops their weight loads (nothing reads them), which leaves
+    // fewer instructions behind the activations than the loop's count.
+    auto step = [&](auto u_tag, int k, auto wait_tag) {
+        constexpr int U = decltype(u_tag)::value;
+        constexpr int A0 = U % 3, A2 = (U + 2) % 3, B0 = U % NS, B1 = (U + 1) % NS;
+        const char *rd = pick<A0>(b0, b1, b2);
+        dma_a(pick<A2>(b0, b1, b2), k + 2);
         __builtin_amdgcn_sched_barrier(0);
-        mfma_pair(ST, 0, bfa);
-        dequant_pair(bq[ST], 1, bfb);
+        mfma_pair(rd, 0, bfa);
+        dequant_pair(bq[B0], 1, bfb);
         interleave();
         __builtin_amdgcn_sched_barrier(0);
-        load_b(bq[ST], k + 2);
-        mfma_pair(ST, 1, bfb);
-        dequant_pair(bq[ST ^ 1], 0, bfa);  // pair 0 of step k + 1 (past the end: unused)
+        load_b(bq[B0], k + NS);
+        mfma_pair(rd, 1, bfb);
+        dequant_pair(bq[B1], 0, bfa);  // pair 0 of step k + 1 (past the end: unused)
         interleave();
-        __builtin_amdgcn_sched_barrier(0);
-        // past the last step this stores a re-load nobody reads (the
-        // epilogue reuses the buffers only after the barrier below)
-        store_a(ST ^ 1, av[ST ^ 1]);
-        __syncthreads();
+        end_step(wait_tag);
     };
+    const std::integral_constant<int, kStepWait> loop_wait;
+    const std::integral_constant<int, (7 << 4)> full_wait;  // vmcnt(0) lgkmcnt(0)
 
-    load_a(av[0], 0);
+    // prologue: after the activations of step 1 come as many VMEM
+    // instructions as after those of step k + 1 in the loop (with three
+    // stages the weights of step 2, with two those of step 1)
     load_b(bq[0], 0);
-    load_a(av[1], 1);
-    load_b(bq[1], 1);
-    store_a(0, av[0]);
-    dequant_pair(bq[0], 0, bfa);
-    __syncthreads();
-    int k = 0;
-    for (; k + 1 < nsteps; k += 2) {
-        step(std::integral_constant<int, 0>{}, k);
-        step(std::integral_constant<int, 1>{}, k + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    dma_a(b0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NS == 3) {
+        load_b(bq[1], 1);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_a(b1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(bq[NS - 1], 2);
+    } else {
+        dma_a(b1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(bq[1], 1);
     }
-    if (k < nsteps) step(std::integral_constant<int, 0>{}, k);
+    __builtin_amdgcn_sched_barrier(0);
+    dequant_pair(bq[0], 0, bfa);
+    end_step(std::integral_constant<int, kPrologueWait>{});
+    int k = 0;
+    for (; k + UNROLL <= nsteps; k += UNROLL) {
+        step(std::integral_constant<int, 0>{}, k, loop_wait);
+        step(std::integral_constant<int, 1>{}, k + 1, loop_wait);
+        step(std::integral_constant<int, 2>{}, k + 2, loop_wait);
+        if constexpr (UNROLL == 6) {
+            step(std::integral_constant<int, 3>{}, k + 3, loop_wait);
+            step(std::integral_constant<int, 4>{}, k + 4, loop_wait);
+            step(std::integral_constant<int, 5>{}, k + 5, loop_wait);
+        }
+    }
+    if (k < nsteps) step(std::integral_constant<int, 0>{}, k, full_wait);
+    if (k + 1 < nsteps) step(std::integral_constant<int, 1>{}, k + 1, full_wait);
+    if constexpr (UNROLL == 6) {
+        if (k + 2 < nsteps) step(std::integral_constant<int, 2>{}, k + 2, full_wait);
+        if (k + 3 < nsteps) step(std::integral_constant<int, 3>{}, k + 3, full_wait);
+        if (k + 4 < nsteps) step(std::integral_constant<int, 4>{}, k + 4, full_wait);
+    }
+    // the loads past the last step land before any wave reuses the buffers
+    end_step(full_wait);
 
     // epilogue: the tile's bf16 outputs are put in LDS (free now: every wave
-    // is past its last read of the activations) and leave in 16-byte stores
-    // of whole row pieces.  Lane holds column (lane & 31) of each 32x32 tile,
-    // rows 8*(r/4) + 4*(lane/32) + r%4 for accumulator register r; rows past
-    // the tile's M are computed from zero activations and not stored.
-    uint16_t *os = &As[0][0][0];
+    // is past its last read of the activations and every load has landed)
+    // and leave in 16-byte stores of whole row pieces.  Lane holds column
+    // (lane & 31) of each 32x32 tile, rows 8*(r/4) + 4*(lane/32) + r%4 for
+    // accumulator register r; rows past the tile's M are computed from zero
+    // activations and not stored.  Row block i goes to half i / 2.
+    uint16_t *os0 = reinterpret_cast<uint16_t *>(b0), *os1 = reinterpret_cast<uint16_t *>(b1);
     const int rq = h * 4;
     auto put = [&](int i, int r, int c, uint32_t pair) {  // registers r, r + 1 (rows m, m + 1)
-        const int m = i * 32 + 8 * (r >> 2) + rq + (r & 3);
+        uint16_t *os = i < 2 ? os0 : os1;
+        const int m = (i & 1) * 32 + 8 * (r >> 2) + rq + (r & 3);
         os[m * OLD + c] = (uint16_t)pair;
         os[(m + 1) * OLD + c] = (uint16_t)(pair >> 16);
     };
@@ -412,7 +481,7 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
         else emit_all(std::false_type{});
         __syncthreads();
         // tile column c is hidden column ntile * 128 + c
-        store_tile(a, os, p0, M, [&](int c) { return ntile * (BN / 2) + c; });
+        store_tile(a, os0, os1, p0, M, [&](int c) { return ntile * (BN / 2) + c; });
     } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -426,7 +495,7 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) put(i, r, c, pack_bf16(acc[i][j][r] + bd, acc[i][j][r + 1] + bd));
             __syncthreads();
-            store_tile(a, os, p0, M, [&](int c) { return ntile * BN + (c >> 5) * 64 + j * 32 + (c & 31); });
+            store_tile(a, os0, os1, p0, M, [&](int c) { return ntile * BN + (c >> 5) * 64 + j * 32 + (c & 31); });
             if (j == 0) __syncthreads();  // the next pass rewrites the LDS tile
         }
     }
@@ -435,7 +504,9 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, uint16_t (&As)[2][B
 template <int PREC, bool GATEUP>
 __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDA];
+    __shared__ __attribute__((aligned(16))) char buf0[kBufBytes];
+    __shared__ __attribute__((aligned(16))) char buf1[kBufBytes];
+    __shared__ __attribute__((aligned(16))) char buf2[kBufBytes];
 
     const int j8 = blockIdx.x >> 3;
     const int ntiles = *a.count;
@@ -451,11 +522,11 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
     // 32-row blocks that hold positions (fewer than three run as two: the
     // dequantization, the same for any M, then bounds the time anyway)
     if (M > 96)
-        gemm_tile<PREC, GATEUP, 4>(a, As, g, p0, M, ntile);
+        gemm_tile<PREC, GATEUP, 4>(a, buf0, buf1, buf2, g, p0, M, ntile);
     else if (M > 64)
-        gemm_tile<PREC, GATEUP, 3>(a, As, g, p0, M, ntile);
+        gemm_tile<PREC, GATEUP, 3>(a, buf0, buf1, buf2, g, p0, M, ntile);
     else
-        gemm_tile<PREC, GATEUP, 2>(a, As, g, p0, M, ntile);
+        gemm_tile<PREC, GATEUP, 2>(a, buf0, buf1, buf2, g, p0, M, ntile);
 }
 
 int mfma_tile_m() { return BM; }
