@@ -173,71 +173,85 @@ __global__ __launch_bounds__(256) void router_small_kernel(const float *__restri
     if (lane == 0) logits[(size_t)t * E + e] = (double)acc + bias[e];
 }
 
-// Many tokens: fp32 matrix cores.  A workgroup computes 32 tokens x 32
-// experts with v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation);
-// its four waves take a quarter of K each and add their partial tiles
-// through LDS.  Lane l supplies row l%32 (token resp. expert) at k-offset
+// Many tokens: fp32 matrix cores.  A workgroup computes 32 tokens x 32 NE
+// experts with v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation),
+// so a token row is read once for NE expert tiles; its NW waves take an
+// NW-th of K each and add their partial tiles through LDS in wave order.
+// Lane l supplies row l%32 (token resp. expert of each tile) at k-offset
 // 8*(l/32) + s of every 16-value step for the 8 chained instructions s, so a
-// lane's operands are two float4 loads per step.  Rows past T or E read the
+// lane's operands are two float4 loads per row and step; the next step's
+// loads are in flight while a step multiplies.  Rows past T or E read the
 // last valid row and are not written.
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+constexpr long long kRouterWaves = 2048;  // two waves per SIMD of 256 CUs
 
-__global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ x, int ldx, int T, int kp,
-                                                          const float *__restrict__ w, int ldw,
-                                                          const double *__restrict__ bias, int E,
-                                                          double *__restrict__ logits,
-                                                          const float *__restrict__ row_scale)
+template <int NE, int NW>
+__global__ __launch_bounds__(64 * NW) void router_mfma_kernel(const float *__restrict__ x, int ldx, int T, int kp,
+                                                              const float *__restrict__ w, int ldw,
+                                                              const double *__restrict__ bias, int E,
+                                                              double *__restrict__ logits,
+                                                              const float *__restrict__ row_scale)
 {
-    __shared__ float red[4][16][64];
+    __shared__ float red[NW][16 * NE][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
+    const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32 * NE;
     const int r = lane & 31, h = lane >> 5;
     const float *xr = x + (size_t)min(t0 + r, T - 1) * ldx + 8 * h;
-    const float *wr = w + (size_t)min(e0 + r, E - 1) * ldw + 8 * h;
-    const int n16 = kp / 16;
-    const int k0 = wave * n16 / 4, k1 = (wave + 1) * n16 / 4;
-    floatx16 acc;
+    const float *wr[NE];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    for (int j = 0; j < NE; ++j) wr[j] = w + (size_t)min(e0 + 32 * j + r, E - 1) * ldw + 8 * h;
+    const int n16 = kp / 16;
+    const int k0 = wave * n16 / NW, k1 = (wave + 1) * n16 / NW;
+    floatx16 acc[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[j][i] = 0.f;
     // operands of step kb + 1 load while step kb multiplies
-    float4 xa, xb, wa, wb;
-    if (k0 < k1) {
-        xa = *reinterpret_cast<const float4 *>(xr + k0 * 16);
-        xb = *reinterpret_cast<const float4 *>(xr + k0 * 16 + 4);
-        wa = *reinterpret_cast<const float4 *>(wr + k0 * 16);
-        wb = *reinterpret_cast<const float4 *>(wr + k0 * 16 + 4);
-    }
-    for (int kb = k0; kb < k1; ++kb) {
-        float4 nxa = xa, nxb = xb, nwa = wa, nwb = wb;
-        if (kb + 1 < k1) {
-            nxa = *reinterpret_cast<const float4 *>(xr + (kb + 1) * 16);
-            nxb = *reinterpret_cast<const float4 *>(xr + (kb + 1) * 16 + 4);
-            nwa = *reinterpret_cast<const float4 *>(wr + (kb + 1) * 16);
-            nwb = *reinterpret_cast<const float4 *>(wr + (kb + 1) * 16 + 4);
+    float4 xa, xb, wa[NE], wb[NE];
+    auto load = [&](float4 &pa, float4 &pb, float4 (&qa)[NE], float4 (&qb)[NE], int kb) {
+        pa = *reinterpret_cast<const float4 *>(xr + kb * 16);
+        pb = *reinterpret_cast<const float4 *>(xr + kb * 16 + 4);
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            qa[j] = *reinterpret_cast<const float4 *>(wr[j] + kb * 16);
+            qb[j] = *reinterpret_cast<const float4 *>(wr[j] + kb * 16 + 4);
         }
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, wa.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, wa.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.z, wa.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.w, wa.w, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.x, wb.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.y, wb.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.z, wb.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.w, wb.w, acc, 0, 0, 0);
+    };
+    if (k0 < k1) load(xa, xb, wa, wb, k0);
+    for (int kb = k0; kb < k1; ++kb) {
+        float4 nxa, nxb, nwa[NE], nwb[NE];
+        load(nxa, nxb, nwa, nwb, min(kb + 1, k1 - 1));  // past the last step: a re-load, not used
+        const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int j = 0; j < NE; ++j) {
+                const float ws = s < 4 ? (&wa[j].x)[s] : (&wb[j].x)[s - 4];
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[s], ws, acc[j], 0, 0, 0);
+            }
         xa = nxa;
         xb = nxb;
-        wa = nwa;
-        wb = nwb;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            wa[j] = nwa[j];
+            wb[j] = nwb[j];
+        }
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
-    __syncthreads();
-    // accumulator register i of lane l is token row 8*(i/4) + 4*(l/32) + i%4,
-    // expert column l%32; wave v finishes registers 4v..4v+3
+    for (int j = 0; j < NE; ++j)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = 4 * wave + j;
-        const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), e = e0 + r;
-        float v = red[0][i][lane] + red[1][i][lane] + red[2][i][lane] + red[3][i][lane];
+        for (int i = 0; i < 16; ++i) red[wave][16 * j + i][lane] = acc[j][i];
+    __syncthreads();
+    // accumulator register i of tile j in lane l is token row
+    // 8*(i/4) + 4*(l/32) + i%4, expert 32 j + l%32; wave q finishes the
+    // registers 16 j + i = q, q + NW, ...
+    for (int ji = wave; ji < 16 * NE; ji += NW) {
+        const int j = ji >> 4, i = ji & 15;
+        const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), e = e0 + 32 * j + r;
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) v += red[q][ji][lane];
         if (t < T && e < E) {
             if (row_scale) v = row_scale[t] * v;
             logits[(size_t)t * E + e] = (double)v + bias[e];
@@ -257,9 +271,24 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
                            row_scale);
     } else {
         const int kp = (d + 63) / 64 * 64;
-        dim3 grid((T + 31) / 32, (E + 31) / 32);
-        hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
-                           row_scale);
+        // two expert tiles per workgroup (each token row read half as
+        // often) when the grid still holds two waves per SIMD of the 256
+        // CUs, with four waves over K if that is enough, else eight; one
+        // tile and four waves otherwise
+        const long long tiles2 = (long long)((T + 31) / 32) * ((E + 63) / 64);
+        if (E > 32 && tiles2 * 8 >= kRouterWaves) {
+            dim3 grid((T + 31) / 32, (E + 63) / 64);
+            if (tiles2 * 4 >= kRouterWaves)
+                hipLaunchKernelGGL((router_mfma_kernel<2, 4>), grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E,
+                                   logits, row_scale);
+            else
+                hipLaunchKernelGGL((router_mfma_kernel<2, 8>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E,
+                                   logits, row_scale);
+        } else {
+            dim3 grid((T + 31) / 32, (E + 31) / 32);
+            hipLaunchKernelGGL((router_mfma_kernel<1, 4>), grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E,
+                               logits, row_scale);
+        }
     }
     return hipGetLastError();
 }
