@@ -232,11 +232,16 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     // loads, wave w taking rows 32 i + 8 w .. + 7, lane l writing 16 bytes
     // at row 32 i + 8 w + l / 8, slot l % 8 of the step's buffer.  A row is
     // 128 bytes (64 bf16 of K); slot s of row R holds K values
-    // 8 (s ^ R % 8) .. + 7, so the 32 rows that one operand read takes fall
-    // on distinct banks.  Rows past M read past the buffer and get zeros.
+    // 8 (s ^ (R / 2) % 8) .. + 7.  The LDS has 64 four-byte banks and serves
+    // a 16-byte read 16 lanes at a time: rows R and R + 1 fall on opposite
+    // halves of the banks and the swizzle spreads the 8 rows of each parity
+    // among a 16-row run over the 8 slots, so an operand read (16 rows, one
+    // K chunk) touches every bank once.  Rows past M read past the buffer
+    // and get zeros.
     const __amdgpu_buffer_rsrc_t asrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(a.a), 0, (int)(a.a_rows * a.lda * 2), kRawBufferWord3);
-    const int arow = lane >> 3, achunk = (lane & 7) ^ arow;  // R % 8 == arow
+    // (R / 2) % 8 == (4 (w % 2) + l / 16) for this lane's rows R
+    const int arow = lane >> 3, achunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
     uint32_t aoff[MI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
@@ -351,9 +356,9 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
         for (int s2 = 0; s2 < 2; ++s2) {
             // k-values of this MFMA step: lanes of half h carry values
             // 8s2..8s2+7 of block 2p + h (FP4: 2h + p) of the K step, which
-            // is K chunk 2 block + s2, in slot chunk ^ (row % 8)
+            // is K chunk 2 block + s2, in slot chunk ^ (row / 2) % 8
             const int chunk = 2 * (PREC == kFP4 ? 2 * h + p : 2 * p + h) + s2;
-            const int so = 16 * (chunk ^ (col & 7));
+            const int so = 16 * (chunk ^ ((col >> 1) & 7));
             bf16x8 af[MI];
 #pragma unroll
             for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(buf + (32 * i + col) * 128 + so);
