@@ -12,17 +12,18 @@
 // Four waves split the columns: each wave owns all 128 positions x 64
 // columns (4 x 2 MFMA tiles of 32 x 32; for gate/up its two column tiles are
 // gate and up of the same 32 neurons, so both values of a neuron land in
-// the same lane).  The activations go through LDS (double-buffered, K steps
-// of 64) and are read by all four waves; each weight value is loaded and
-// dequantized exactly once per workgroup, by the wave that uses it,
-// straight from the panel layout into MFMA operand registers: lane l holds
-// column l%32 and, for each pair of 16-value MFMA steps, one whole scale
-// block (block 2p + l/32 of the K step; FP4: 2(l/32) + p, so that its two
-// blocks of a step are one 16-byte unit), whose first and second halves feed
-// the two steps.  The activations are read from LDS in the same permuted K
-// order.  Global loads run two K steps ahead of the MFMAs, and the epilogue
-// stages the tile's bf16 outputs in LDS so that they leave in 16-byte row
-// pieces.
+// the same lane).  The activations reach LDS by LDS-DMA loads (three
+// buffers, K steps of 64, two steps ahead) and are read by all four waves;
+// each weight value is loaded and dequantized exactly once per workgroup, by
+// the wave that uses it, straight from the panel layout into MFMA operand
+// registers (three register stages, three steps ahead): lane l holds column
+// l%32 and, for each pair of 16-value MFMA steps, one whole scale block
+// (block 2p + l/32 of the K step; FP4: 2(l/32) + p, so that its two blocks
+// of a step are one 16-byte unit), whose first and second halves feed the
+// two steps.  The activations are read from LDS in the same permuted K
+// order.  A tile multiplies only the 32-row blocks that hold positions, and
+// the epilogue stages the tile's bf16 outputs in LDS so that they leave in
+// 16-byte row pieces.
 //
 // Tiles: the m-tiles of all groups (the dispatch kernel wrote their count
 // and a (group, first position, positions) descriptor per tile; blocks past
