@@ -179,11 +179,12 @@ __global__ __launch_bounds__(256) void router_small_kernel(const float *__restri
 // NW-th of K each and add their partial tiles through LDS in wave order.
 // Lane l supplies row l%32 (token resp. expert of each tile) at k-offset
 // 8*(l/32) + s of every 16-value step for the 8 chained instructions s, so a
-// lane's operands are two float4 loads per row and step; the next step's
-// loads are in flight while a step multiplies.  Rows past T or E read the
-// last valid row and are not written.
+// lane's operands are two float4 loads per row and step; the loads of the
+// next kRouterAhead steps are in flight while a step multiplies.  Rows past
+// T or E read the last valid row and are not written.
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr long long kRouterWaves = 2048;  // two waves per SIMD of 256 CUs
+constexpr int kRouterAhead = 3;            // steps whose loads are in flight
 
 template <int NE, int NW>
 __global__ __launch_bounds__(64 * NW) void router_mfma_kernel(const float *__restrict__ x, int ldx, int T, int kp,
@@ -207,35 +208,40 @@ __global__ __launch_bounds__(64 * NW) void router_mfma_kernel(const float *__res
     for (int j = 0; j < NE; ++j)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[j][i] = 0.f;
-    // operands of step kb + 1 load while step kb multiplies
-    float4 xa, xb, wa[NE], wb[NE];
-    auto load = [&](float4 &pa, float4 &pb, float4 (&qa)[NE], float4 (&qb)[NE], int kb) {
-        pa = *reinterpret_cast<const float4 *>(xr + kb * 16);
-        pb = *reinterpret_cast<const float4 *>(xr + kb * 16 + 4);
+    // a ring of kRouterAhead steps' operands: step kb's loads are issued
+    // kRouterAhead steps before it multiplies (past the last step the ring
+    // re-loads that step, unused)
+    struct Ops {
+        float4 xa, xb, wa[NE], wb[NE];
+    };
+    auto load = [&](Ops &o, int kb) {
+        o.xa = *reinterpret_cast<const float4 *>(xr + kb * 16);
+        o.xb = *reinterpret_cast<const float4 *>(xr + kb * 16 + 4);
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
-            qa[j] = *reinterpret_cast<const float4 *>(wr[j] + kb * 16);
-            qb[j] = *reinterpret_cast<const float4 *>(wr[j] + kb * 16 + 4);
+            o.wa[j] = *reinterpret_cast<const float4 *>(wr[j] + kb * 16);
+            o.wb[j] = *reinterpret_cast<const float4 *>(wr[j] + kb * 16 + 4);
         }
     };
-    if (k0 < k1) load(xa, xb, wa, wb, k0);
-    for (int kb = k0; kb < k1; ++kb) {
-        float4 nxa, nxb, nwa[NE], nwb[NE];
-        load(nxa, nxb, nwa, nwb, min(kb + 1, k1 - 1));  // past the last step: a re-load, not used
-        const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    Ops ring[kRouterAhead];
+    if (k0 < k1) {
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+        for (int i = 0; i < kRouterAhead; ++i) load(ring[i], min(k0 + i, k1 - 1));
+    }
+    for (int kb = k0; kb < k1; kb += kRouterAhead) {
 #pragma unroll
-            for (int j = 0; j < NE; ++j) {
-                const float ws = s < 4 ? (&wa[j].x)[s] : (&wb[j].x)[s - 4];
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[s], ws, acc[j], 0, 0, 0);
-            }
-        xa = nxa;
-        xb = nxb;
+        for (int i = 0; i < kRouterAhead; ++i) {
+            if (kb + i >= k1) break;  // wave-uniform
+            Ops &o = ring[i];
+            const float xs[8] = {o.xa.x, o.xa.y, o.xa.z, o.xa.w, o.xb.x, o.xb.y, o.xb.z, o.xb.w};
 #pragma unroll
-        for (int j = 0; j < NE; ++j) {
-            wa[j] = nwa[j];
-            wb[j] = nwb[j];
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int j = 0; j < NE; ++j) {
+                    const float ws = s < 4 ? (&o.wa[j].x)[s] : (&o.wb[j].x)[s - 4];
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[s], ws, acc[j], 0, 0, 0);
+                }
+            load(o, min(kb + i + kRouterAhead, k1 - 1));
         }
     }
 #pragma unroll
