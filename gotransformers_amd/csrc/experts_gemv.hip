@@ -82,6 +82,11 @@ __device__ __forceinline__ uint32_t comp(const uint4 &v)
     return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
 }
 
+__device__ __forceinline__ uint32_t comp_rt(const uint4 &v, int i)
+{
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 __device__ __forceinline__ s16x4 as_s16x4(uint32_t lo, uint32_t hi)
 {
     const u32x2 v = {lo, hi};
@@ -605,6 +610,198 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
     }
 }
 
+// One token (T = 1, self-dispatching): the k routed slots' and the shared
+// experts' rows spread over the whole GPU.  A workgroup takes R rows of one
+// group (R divides the 64-row panel) and all of K; lane l of each of its 4
+// waves owns row l % R and unit phase l / R, so a load of the wave reads R
+// rows' 16-byte units side by side (R x 16 contiguous bytes per phase).
+// Phase p of the workgroup takes units p, p + 4 * 64 / R, ... of its rows.
+// The token row is staged once in LDS as fp32.  Per 16-value block: the
+// codes times the token values, summed in order with fp32 FMAs, then times
+// the block's scale into the lane's sum (the order of lowprecision/rows.go:
+// 207-257 within a block); the lanes' sums are added across phases and
+// waves.  Same epilogues as gemv_kernel.
+template <int PREC, bool GATEUP, int R>
+__global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
+{
+    constexpr int MATS = GATEUP ? 2 : 1;
+    constexpr int PH = 64 / R;       // unit phases per wave
+    constexpr int STRIDE = 4 * PH;   // units between a lane's units
+    constexpr int VPU = PREC == kInt8 ? 16 : 32;  // values per 16-byte unit
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    float *xs = reinterpret_cast<float *>(lds);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int y = blockIdx.y;  // shared expert y < S, else routed slot y - S
+    const int n0 = blockIdx.x * R;
+    const int K = a.nblocks * 16;
+    // the input row (the token, or this slot's hidden row) is requested
+    // first: it does not depend on the routing
+    const int in_row = GATEUP ? 0 : y;  // hidden rows: shared experts, then the routed slots
+    const int out_row = y;
+    const float4 *xin = reinterpret_cast<const float4 *>(a.in + (size_t)in_row * a.ld_in);
+    float4 xv[4];  // K <= 4096: at most four float4 per thread
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (tid + 256 * i < K / 4) xv[i] = xin[tid + 256 * i];
+    int g = y;
+    float wgt = 1.0f;
+    if (y >= a.S) {
+        g = a.S + a.chosen[y - a.S];
+        wgt = a.gates32[y - a.S];
+    }
+    g = __builtin_amdgcn_readfirstlane(g);
+    const int nunits = a.row_bytes / 16;
+    const int r = lane % R;
+    const int n = n0 + r;
+    const int panel = n0 >> 6, prow = (n0 & 63) + r;
+
+    PanelSrc src[MATS];
+    {
+        const size_t wpanel = (size_t)panel * 64 * a.row_bytes;
+        const int wbytes = 64 * a.row_bytes;
+        const size_t spanel = (size_t)panel * 64 * a.nblocks;
+        const int sbytes = 64 * a.nblocks * 4;
+#pragma unroll
+        for (int m = 0; m < MATS; ++m) {
+            const void *w = m == 0 ? a.w0 : a.w1;
+            const float *sc = m == 0 ? a.s0 : a.s1;
+            src[m].codes = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<char *>(reinterpret_cast<const char *>(w)) + (size_t)g * a.w_group_stride + wpanel, 0,
+                wbytes, kRawBufferWord3);
+            src[m].scales = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(sc) + (size_t)g * a.s_group_stride + spanel, 0, sbytes, kRawBufferWord3);
+        }
+    }
+    constexpr int UB = 4;  // units of a lane in flight together
+    float sum[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) sum[m] = 0.f;
+    const int ulanes = nunits / STRIDE;  // units per lane (the launcher checks the division)
+
+    // unit u = U0 + q of the lane: U0 = wave PH + j STRIDE (uniform, a
+    // multiple of 4) and q = lane / R; its first scale block b = u BPU sits
+    // at (b / 4) 1024 + (b % 4) 4 + row 16 in the panel's scales
+    constexpr int BPU = VPU / 16;  // scale blocks per unit
+    const int q = lane / R;
+    const uint32_t cvo = (uint32_t)prow * 16u + (uint32_t)q * 1024u;
+    const uint32_t svo = (uint32_t)prow * 16u + (uint32_t)((q * BPU) >> 2) * 1024u + (uint32_t)((q * BPU) & 3) * 4u;
+    for (int j0 = 0; j0 < ulanes; j0 += UB) {
+        uint4 c[UB][MATS];
+        float sc[UB][MATS][BPU];
+#pragma unroll
+        for (int i = 0; i < UB; ++i) {
+            // past the lane's last unit: its last unit again (never used)
+            const int U0 = wave * PH + min(j0 + i, ulanes - 1) * STRIDE;
+#pragma unroll
+            for (int m = 0; m < MATS; ++m) {
+                c[i][m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src[m].codes, cvo,
+                                                                                         U0 * 1024, 0));
+                const int soff = (U0 * BPU / 4) * 1024;
+                if constexpr (BPU == 1) {
+                    sc[i][m][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src[m].scales, svo,
+                                                                                                soff, 0));
+                } else {
+                    const float2 v = __builtin_bit_cast(
+                        float2, __builtin_amdgcn_raw_buffer_load_b64(src[m].scales, svo, soff, 0));
+                    sc[i][m][0] = v.x;
+                    sc[i][m][1] = v.y;
+                }
+            }
+        }
+        if (j0 == 0) {
+            // the input row into LDS (K fp32 values, K a multiple of 64)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (tid + 256 * i < K / 4) reinterpret_cast<float4 *>(xs)[tid + 256 * i] = xv[i];
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < UB; ++i) {
+            if (j0 + i >= ulanes) break;  // wave-uniform
+            const int u = wave * PH + (j0 + i) * STRIDE + q;
+            const float4 *xv = reinterpret_cast<const float4 *>(xs + u * VPU);
+#pragma unroll
+            for (int blk = 0; blk < BPU; ++blk) {
+                float xb[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v = xv[blk * 4 + q];
+                    xb[4 * q] = v.x;
+                    xb[4 * q + 1] = v.y;
+                    xb[4 * q + 2] = v.z;
+                    xb[4 * q + 3] = v.w;
+                }
+#pragma unroll
+                for (int m = 0; m < MATS; ++m) {
+                    float acc = 0.f;
+                    if constexpr (PREC == kInt8) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const uint32_t d = comp_rt(c[i][m], q);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc = fmaf((float)(int)(int8_t)(d >> (8 * e)), xb[4 * q + e], acc);
+                        }
+                    } else {
+                        // FP4: block blk is dwords 2 blk, 2 blk + 1; each byte
+                        // holds two values, the even one in the low nibble
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {
+                            const uint32_t d = comp_rt(c[i][m], 2 * blk + q);
+                            const f32x2 f[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0),
+                                                __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1),
+                                                __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2),
+                                                __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3)};
+#pragma unroll
+                            for (int sel = 0; sel < 4; ++sel) {
+                                acc = fmaf(f[sel].x, xb[8 * q + 2 * sel], acc);
+                                acc = fmaf(f[sel].y, xb[8 * q + 2 * sel + 1], acc);
+                            }
+                        }
+                    }
+                    sum[m] = fmaf(acc, sc[i][m][blk], sum[m]);
+                }
+            }
+        }
+    }
+    // across the phases of the wave, then across the waves in wave order
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int off = R; off < 64; off <<= 1) sum[m] += __shfl_xor(sum[m], off);
+    __syncthreads();  // every read of the staged row is done
+    float *red = xs;  // [4][MATS][R]
+    if (lane < R)
+#pragma unroll
+        for (int m = 0; m < MATS; ++m) red[(wave * MATS + m) * R + lane] = sum[m];
+    __syncthreads();
+    if (wave != 0 || lane >= R || n >= a.rows) return;
+    float v[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) {
+        float t = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < 4; ++wv) t += red[(wv * MATS + m) * R + lane];
+        v[m] = t;
+    }
+    const float b0 = a.b0[(size_t)g * a.rows + n];
+    if constexpr (GATEUP) {
+        float gv = v[0] + b0;
+        float uv = v[1] + a.b1[(size_t)g * a.rows + n];
+        if (a.clamp > 0.f) {
+            gv = fminf(gv, a.clamp);                   // ClampedSiLU: x > L -> silu(L)
+            uv = fminf(fmaxf(uv, -a.clamp), a.clamp);  // ClampedLinear
+        }
+        a.out[(size_t)out_row * a.ld_out + n] = silu(gv) * uv;
+    } else if (a.final_out) {
+        // at most two contributions per output row (see gemv_kernel)
+        __hip_atomic_fetch_add(a.final_out + n, wgt * (v[0] + b0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        a.out[(size_t)out_row * a.ld_out + n] = v[0] + b0;
+    }
+}
+
 namespace {
 
 // LDS: the staged tokens (2 x 2 bytes per k-value and token) or the
@@ -662,10 +859,41 @@ hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
     return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
 }
 
+template <bool GATEUP, int PREC, int R>
+hipError_t launch_one_token(const GemvArgs &a, hipStream_t s)
+{
+    const size_t lds = (size_t)a.nblocks * 16 * sizeof(float);  // the token row; >= the reduction's 4 x 2 x R
+    const dim3 grid((a.rows + R - 1) / R, a.S + a.k);
+    hipLaunchKernelGGL((gemv1_kernel<PREC, GATEUP, R>), grid, dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+// One token of a layer wide enough that the general kernel runs eight waves
+// over a panel (at least 16 chunks of K): the single-token kernel, with R =
+// 16 rows per workgroup when that still gives 256 workgroups, else 8.  Int8
+// and FP4 rows whose 16-byte units divide evenly among a workgroup's unit
+// phases.  Returns false (nothing launched) otherwise.
+template <bool GATEUP>
+bool launch_single_token(const GemvArgs &a, int precision, hipStream_t s, hipError_t &e)
+{
+    if (!a.self_dispatch || a.T != 1 || a.raw || (precision != kInt8 && precision != kFP4)) return false;
+    if (a.nblocks / Chunk<kInt8>::CB < 16 || a.nblocks * 16 > 4096) return false;
+    const int nunits = a.row_bytes / 16;
+    const int R = (long long)(a.rows / 16) * (a.S + a.k) >= 256 ? 16 : 8;
+    if (a.row_bytes % 16 != 0 || nunits % (4 * (64 / R)) != 0) return false;
+    if (precision == kInt8)
+        e = R == 16 ? launch_one_token<GATEUP, kInt8, 16>(a, s) : launch_one_token<GATEUP, kInt8, 8>(a, s);
+    else
+        e = R == 16 ? launch_one_token<GATEUP, kFP4, 16>(a, s) : launch_one_token<GATEUP, kFP4, 8>(a, s);
+    return true;
+}
+
 template <bool GATEUP>
 hipError_t launch_any(const GemvArgs &a, int precision, int max_slices, hipStream_t s)
 {
     if (max_slices <= 0) return hipSuccess;
+    hipError_t e1 = hipSuccess;
+    if (launch_single_token<GATEUP>(a, precision, s, e1)) return e1;
     // the input rows are read through a buffer resource with 32-bit offsets
     if (a.in_rows <= 0 || a.in_rows * a.ld_in * 4 > 0x7fffffffLL) return hipErrorInvalidValue;
     switch (precision) {
