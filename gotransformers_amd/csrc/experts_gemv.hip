@@ -640,10 +640,11 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
     const int in_row = GATEUP ? 0 : y;  // hidden rows: shared experts, then the routed slots
     const int out_row = y;
     const float4 *xin = reinterpret_cast<const float4 *>(a.in + (size_t)in_row * a.ld_in);
-    float4 xv[4];  // K <= 4096: at most four float4 per thread
+    // K <= 4096: at most four float4 per thread, loaded unconditionally (the
+    // index clamped; the extra copies are not stored) so they stay in registers
+    float4 xv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (tid + 256 * i < K / 4) xv[i] = xin[tid + 256 * i];
+    for (int i = 0; i < 4; ++i) xv[i] = xin[min(tid + 256 * i, K / 4 - 1)];
     int g = y;
     float wgt = 1.0f;
     if (y >= a.S) {
@@ -686,12 +687,13 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
     const int q = lane / R;
     const uint32_t cvo = (uint32_t)prow * 16u + (uint32_t)q * 1024u;
     const uint32_t svo = (uint32_t)prow * 16u + (uint32_t)((q * BPU) >> 2) * 1024u + (uint32_t)((q * BPU) & 3) * 4u;
-    for (int j0 = 0; j0 < ulanes; j0 += UB) {
-        uint4 c[UB][MATS];
-        float sc[UB][MATS][BPU];
+    uint4 c[UB][MATS];
+    float sc[UB][MATS][BPU];
+    // the lane's units j0 .. j0 + UB - 1 (past its last unit: the last unit
+    // again, never used)
+    auto load_units = [&](int j0) {
 #pragma unroll
         for (int i = 0; i < UB; ++i) {
-            // past the lane's last unit: its last unit again (never used)
             const int U0 = wave * PH + min(j0 + i, ulanes - 1) * STRIDE;
 #pragma unroll
             for (int m = 0; m < MATS; ++m) {
@@ -709,54 +711,55 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
                 }
             }
         }
-        if (j0 == 0) {
-            // the input row into LDS (K fp32 values, K a multiple of 64)
+    };
+    load_units(0);
+    // the input row into LDS (K fp32 values, K a multiple of 64)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (tid + 256 * i < K / 4) reinterpret_cast<float4 *>(xs)[tid + 256 * i] = xv[i];
-            __syncthreads();
-        }
+    for (int i = 0; i < 4; ++i)
+        if (tid + 256 * i < K / 4) reinterpret_cast<float4 *>(xs)[tid + 256 * i] = xv[i];
+    __syncthreads();
+    for (int j0 = 0;;) {
 #pragma unroll
         for (int i = 0; i < UB; ++i) {
             if (j0 + i >= ulanes) break;  // wave-uniform
             const int u = wave * PH + (j0 + i) * STRIDE + q;
-            const float4 *xv = reinterpret_cast<const float4 *>(xs + u * VPU);
+            const float4 *xq = reinterpret_cast<const float4 *>(xs + u * VPU);
 #pragma unroll
             for (int blk = 0; blk < BPU; ++blk) {
                 float xb[16];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 v = xv[blk * 4 + q];
-                    xb[4 * q] = v.x;
-                    xb[4 * q + 1] = v.y;
-                    xb[4 * q + 2] = v.z;
-                    xb[4 * q + 3] = v.w;
+                for (int h = 0; h < 4; ++h) {
+                    const float4 v = xq[blk * 4 + h];
+                    xb[4 * h] = v.x;
+                    xb[4 * h + 1] = v.y;
+                    xb[4 * h + 2] = v.z;
+                    xb[4 * h + 3] = v.w;
                 }
 #pragma unroll
                 for (int m = 0; m < MATS; ++m) {
                     float acc = 0.f;
                     if constexpr (PREC == kInt8) {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const uint32_t d = comp_rt(c[i][m], q);
+                        for (int h = 0; h < 4; ++h) {
+                            const uint32_t d = comp_rt(c[i][m], h);
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
-                                acc = fmaf((float)(int)(int8_t)(d >> (8 * e)), xb[4 * q + e], acc);
+                                acc = fmaf((float)(int)(int8_t)(d >> (8 * e)), xb[4 * h + e], acc);
                         }
                     } else {
                         // FP4: block blk is dwords 2 blk, 2 blk + 1; each byte
                         // holds two values, the even one in the low nibble
 #pragma unroll
-                        for (int q = 0; q < 2; ++q) {
-                            const uint32_t d = comp_rt(c[i][m], 2 * blk + q);
+                        for (int h = 0; h < 2; ++h) {
+                            const uint32_t d = comp_rt(c[i][m], 2 * blk + h);
                             const f32x2 f[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0),
                                                 __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1),
                                                 __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2),
                                                 __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3)};
 #pragma unroll
                             for (int sel = 0; sel < 4; ++sel) {
-                                acc = fmaf(f[sel].x, xb[8 * q + 2 * sel], acc);
-                                acc = fmaf(f[sel].y, xb[8 * q + 2 * sel + 1], acc);
+                                acc = fmaf(f[sel].x, xb[8 * h + 2 * sel], acc);
+                                acc = fmaf(f[sel].y, xb[8 * h + 2 * sel + 1], acc);
                             }
                         }
                     }
@@ -764,6 +767,9 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
                 }
             }
         }
+        j0 += UB;
+        if (j0 >= ulanes) break;
+        load_units(j0);
     }
     // across the phases of the wave, then across the waves in wave order
 #pragma unroll
