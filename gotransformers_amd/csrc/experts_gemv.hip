@@ -610,19 +610,20 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
     }
 }
 
-// One token (T = 1, self-dispatching): the k routed slots' and the shared
-// experts' rows spread over the whole GPU.  A workgroup takes R rows of one
-// group (R divides the 64-row panel) and all of K; lane l of each of its 4
-// waves owns row l % R and unit phase l / R, so a load of the wave reads R
-// rows' 16-byte units side by side (R x 16 contiguous bytes per phase).
-// Phase p of the workgroup takes units p, p + 4 * 64 / R, ... of its rows.
-// The token row is staged once in LDS as fp32.  Per 16-value block: the
-// codes times the token values, summed in order with fp32 FMAs, then times
-// the block's scale into the lane's sum (the order of lowprecision/rows.go:
-// 207-257 within a block); the lanes' sums are added across phases and
-// waves.  Same epilogues as gemv_kernel.
+// A few tokens (T <= kFewTokens, self-dispatching): only k T routed
+// (token, slot) pairs and S T shared (expert, token) pairs have work, so
+// each pair's rows are spread over the whole GPU.  A workgroup takes R rows
+// of one pair (R divides the 64-row panel) and all of K; lane l of each of
+// its 4 waves owns row l % R and unit phase l / R, so a load of the wave
+// reads R rows' 16-byte units side by side (R x 16 contiguous bytes per
+// phase).  Phase p of the workgroup takes units p, p + 4 * 64 / R, ... of
+// its rows.  The pair's input row is staged once in LDS as fp32.  Per
+// 16-value block: the codes times the input values, summed in order with
+// fp32 FMAs, then times the block's scale into the lane's sum (the order of
+// lowprecision/rows.go:207-257 within a block); the lanes' sums are added
+// across phases and waves.  Same epilogues as gemv_kernel.
 template <int PREC, bool GATEUP, int R>
-__global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
+__global__ __launch_bounds__(256) void gemv_few_kernel(GemvArgs a)
 {
     constexpr int MATS = GATEUP ? 2 : 1;
     constexpr int PH = 64 / R;       // unit phases per wave
@@ -632,12 +633,17 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
     float *xs = reinterpret_cast<float *>(lds);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int y = blockIdx.y;  // shared expert y < S, else routed slot y - S
+    // token t = blockIdx.z; blockIdx.y = shared expert s < S (row s T + t
+    // of the self-dispatch layout), else routed slot j = blockIdx.y - S
+    // (entry t k + j, row S T + t k + j).  The input row (the token, or the
+    // pair's hidden row) is requested first: it does not depend on the
+    // routing.
+    const int t = blockIdx.z, yy = blockIdx.y;
     const int n0 = blockIdx.x * R;
     const int K = a.nblocks * 16;
-    // the input row (the token, or this slot's hidden row) is requested
-    // first: it does not depend on the routing
-    const int in_row = GATEUP ? 0 : y;  // hidden rows: shared experts, then the routed slots
+    const int entry = t * a.k + yy - a.S;  // routed pairs only
+    const int y = yy < a.S ? yy * a.T + t : a.S * a.T + entry;
+    const int in_row = GATEUP ? t : y;
     const int out_row = y;
     const float4 *xin = reinterpret_cast<const float4 *>(a.in + (size_t)in_row * a.ld_in);
     // K <= 4096: at most four float4 per thread, loaded unconditionally (the
@@ -645,11 +651,11 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
     float4 xv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) xv[i] = xin[min(tid + 256 * i, K / 4 - 1)];
-    int g = y;
+    int g = yy;
     float wgt = 1.0f;
-    if (y >= a.S) {
-        g = a.S + a.chosen[y - a.S];
-        wgt = a.gates32[y - a.S];
+    if (yy >= a.S) {
+        g = a.S + a.chosen[entry];
+        wgt = a.gates32[entry];
     }
     g = __builtin_amdgcn_readfirstlane(g);
     const int nunits = a.row_bytes / 16;
@@ -802,7 +808,8 @@ __global__ __launch_bounds__(256) void gemv1_kernel(GemvArgs a)
         a.out[(size_t)out_row * a.ld_out + n] = silu(gv) * uv;
     } else if (a.final_out) {
         // at most two contributions per output row (see gemv_kernel)
-        __hip_atomic_fetch_add(a.final_out + n, wgt * (v[0] + b0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(a.final_out + (size_t)t * a.rows + n, wgt * (v[0] + b0), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     } else {
         a.out[(size_t)out_row * a.ld_out + n] = v[0] + b0;
     }
@@ -865,32 +872,39 @@ hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
     return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
 }
 
+// Up to this many tokens the few-token kernel runs: it streams an expert's
+// weights once per (token, slot) pair, where gemv_kernel streams them once per
+// slice of up to 8 tokens, and measured faster up to 6 tokens (C2 and a C5
+// block; about even at 8).
+constexpr int kFewTokens = 6;
+
 template <bool GATEUP, int PREC, int R>
-hipError_t launch_one_token(const GemvArgs &a, hipStream_t s)
+hipError_t launch_few(const GemvArgs &a, hipStream_t s)
 {
     const size_t lds = (size_t)a.nblocks * 16 * sizeof(float);  // the token row; >= the reduction's 4 x 2 x R
-    const dim3 grid((a.rows + R - 1) / R, a.S + a.k);
-    hipLaunchKernelGGL((gemv1_kernel<PREC, GATEUP, R>), grid, dim3(256), lds, s, a);
+    const dim3 grid((a.rows + R - 1) / R, a.S + a.k, a.T);
+    hipLaunchKernelGGL((gemv_few_kernel<PREC, GATEUP, R>), grid, dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
-// One token of a layer wide enough that the general kernel runs eight waves
-// over a panel (at least 16 chunks of K): the single-token kernel, with R =
-// 16 rows per workgroup when that still gives 256 workgroups, else 8.  Int8
-// and FP4 rows whose 16-byte units divide evenly among a workgroup's unit
+// A few tokens through a layer wide enough that gemv_kernel runs eight waves
+// over a panel (at least 16 chunks of K): the few-token kernel, with R = 16
+// rows per workgroup when that still gives 256 workgroups, else 8.  Int8 and
+// FP4 rows whose 16-byte units divide evenly among a workgroup's unit
 // phases.  Returns false (nothing launched) otherwise.
 template <bool GATEUP>
-bool launch_single_token(const GemvArgs &a, int precision, hipStream_t s, hipError_t &e)
+bool launch_few_tokens(const GemvArgs &a, int precision, hipStream_t s, hipError_t &e)
 {
-    if (!a.self_dispatch || a.T != 1 || a.raw || (precision != kInt8 && precision != kFP4)) return false;
+    if (!a.self_dispatch || a.T < 1 || a.T > kFewTokens || a.raw || (precision != kInt8 && precision != kFP4))
+        return false;
     if (a.nblocks / Chunk<kInt8>::CB < 16 || a.nblocks * 16 > 4096) return false;
     const int nunits = a.row_bytes / 16;
-    const int R = (long long)(a.rows / 16) * (a.S + a.k) >= 256 ? 16 : 8;
+    const int R = (long long)(a.rows / 16) * (a.S + a.k) * a.T >= 256 ? 16 : 8;
     if (a.row_bytes % 16 != 0 || nunits % (4 * (64 / R)) != 0) return false;
     if (precision == kInt8)
-        e = R == 16 ? launch_one_token<GATEUP, kInt8, 16>(a, s) : launch_one_token<GATEUP, kInt8, 8>(a, s);
+        e = R == 16 ? launch_few<GATEUP, kInt8, 16>(a, s) : launch_few<GATEUP, kInt8, 8>(a, s);
     else
-        e = R == 16 ? launch_one_token<GATEUP, kFP4, 16>(a, s) : launch_one_token<GATEUP, kFP4, 8>(a, s);
+        e = R == 16 ? launch_few<GATEUP, kFP4, 16>(a, s) : launch_few<GATEUP, kFP4, 8>(a, s);
     return true;
 }
 
@@ -899,7 +913,7 @@ hipError_t launch_any(const GemvArgs &a, int precision, int max_slices, hipStrea
 {
     if (max_slices <= 0) return hipSuccess;
     hipError_t e1 = hipSuccess;
-    if (launch_single_token<GATEUP>(a, precision, s, e1)) return e1;
+    if (launch_few_tokens<GATEUP>(a, precision, s, e1)) return e1;
     // the input rows are read through a buffer resource with 32-bit offsets
     if (a.in_rows <= 0 || a.in_rows * a.ld_in * 4 > 0x7fffffffLL) return hipErrorInvalidValue;
     switch (precision) {

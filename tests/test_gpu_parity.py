@@ -170,27 +170,38 @@ def test_c2_int8_decode(ctx, T):
     assert e <= FP32_TOL
 
 
-@pytest.mark.parametrize("name,cfg,prec", [
-    ("C5 block, 16 experts", dict(d=2048, h=1024, E=16, k=4, S=1), FP4),
-    ("C2 shape", dict(d=1024, h=2048, E=16, k=2, S=0), FP4),
-    ("clamped, one shared", dict(d=512, h=512, E=4, k=2, S=1, clamp=0.3, std=0.05), INT8),
-])
-def test_single_token_decode(ctx, name, cfg, prec):
-    """One token through a layer at least 512 values wide runs the
-    single-token expert kernels (the rows of the routed slots and shared
-    experts spread over the whole GPU, 8 or 16 rows per workgroup); the
-    result must match the oracle under the device's routing, as the
-    many-token kernels' do."""
-    say(f"single token {name}")
+FEW = {
+    "C5 block, 16 experts": (dict(d=2048, h=1024, E=16, k=4, S=1), FP4),
+    "C2 shape": (dict(d=1024, h=2048, E=16, k=2, S=0), FP4),
+    "clamped, one shared": (dict(d=512, h=512, E=4, k=2, S=1, clamp=0.3, std=0.05), INT8),
+}
+
+
+@pytest.mark.parametrize("name", list(FEW))
+def test_few_token_decode(ctx, name):
+    """Up to six tokens through a layer at least 512 values wide run the
+    few-token expert kernels (each (token, slot) pair's and each (shared
+    expert, token) pair's rows spread over the whole GPU, 8 or 16 rows per
+    workgroup); the results must match the oracle under the device's
+    routing, as the many-token kernels' do, at one token and at six (one
+    layer object, so both calls also share its workspace)."""
+    cfg, prec = FEW[name]
     spec = make_moe(gt.encode_rows, precision=prec, seed=21, **cfg)
-    x = np.random.default_rng(22).normal(size=(1, cfg["d"]))
-    y, r, used = run_layer(ctx, spec, x, gt.PATH_AUTO)
-    assert used == gt.PATH_FP32
-    check_routing(r.chosen, spec, x, cfg["k"], f"single token {name}")
-    ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates, threads=8)
-    e = rel_err(y, ref.outputs)
-    say(f"single token {name} max rel err {e:.3e}")
-    assert e <= FP32_TOL
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        for T in (1, 6):
+            say(f"few tokens {name} T={T}")
+            x = np.random.default_rng(22 + T).normal(size=(T, cfg["d"]))
+            y = m.forward(x, None, path=gt.PATH_AUTO)
+            r = m.last_routing()
+            assert m.last_path == gt.PATH_FP32
+            check_routing(r.chosen, spec, x, cfg["k"], f"few tokens {name} T={T}")
+            ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates, threads=8)
+            e = rel_err(y, ref.outputs)
+            say(f"few tokens {name} T={T} max rel err {e:.3e}")
+            assert e <= FP32_TOL
+    finally:
+        m.destroy()
 
 
 @pytest.mark.parametrize("name,cfg,prec,T", [
