@@ -178,6 +178,9 @@ struct Workspace {
     uint16_t *hidden16 = nullptr;  // [P][hp] bf16
     float *slot_out = nullptr;    // [P][d] fp32 (fp32 path) or bf16 (MFMA path)
     int32_t *chunk_cnt = nullptr;  // [chunks][E] scratch of the many-token dispatch
+    // a layer's own workspace only (not the no-allocation forward's area):
+    int32_t *part_cnt = nullptr;   // [cap] arrival counts of a token's routing workgroups (kept zero)
+    float *xalt = nullptr;         // [min(cap, kMaxSplitRouteTokens)][d] a stack's second residual buffer
     float *inv = nullptr;          // [T] inverse RMS of rows the previous stack layer's combine normalised
 };
 
@@ -368,9 +371,11 @@ double decoded_value(const gtmoe_rows *r, int row, int i)
 
 // The buffers of a forward for `cap` tokens laid out from `base` (256-byte
 // aligned parts); returns the bytes they take.  With base null only the size
-// is computed.  Without host staging the float64 rows of the host-API calls
-// and the stack-only buffers (a host-API stack's residual, the rows' inverse
-// RMS) are left out (single-layer device forwards only).
+// is computed.  Without host staging the float64 rows of the host-API calls,
+// the stack-only buffers (a host-API stack's residual, the rows' inverse
+// RMS, the second residual buffer) and the split routing's arrival counts
+// are left out (single-layer device forwards only; their routing then runs
+// one workgroup per token).
 size_t layout_workspace(const gtmoe_layer *L, int cap, bool host_staging, char *base, Workspace &w)
 {
     const size_t P = (size_t)cap * (L->S + L->k);
@@ -393,7 +398,8 @@ size_t layout_workspace(const gtmoe_layer *L, int cap, bool host_staging, char *
         {(void **)&w.tok, P * 4},                       {(void **)&w.hidden32, P * L->hp * 4},
         {(void **)&w.hidden16, P * L->hp * 2},          {(void **)&w.slot_out, P * L->d * 4},
         {(void **)&w.chunk_cnt, (size_t)dispatch_chunks(cap) * L->E * 4},
-        {(void **)&w.inv, hs * cap * 4},
+        {(void **)&w.inv, hs * cap * 4},               {(void **)&w.part_cnt, hs * cap * 4},
+        {(void **)&w.xalt, hs * std::min(cap, kMaxSplitRouteTokens) * L->d * 4},
     };
     size_t off = 0;
     for (const Part &p : parts) {
@@ -480,7 +486,8 @@ struct PendingCombine {
 // Otherwise: convert or RMSNorm into ws.xf / ws.xb, router and top-k (or hash
 // routing), then the dispatch.  token_ids: device pointer (hash routing).
 int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t *token_ids, int path, hipStream_t s,
-                          float *zero_out = nullptr, const PendingCombine *pend = nullptr, bool prenormed = false)
+                          float *zero_out = nullptr, const PendingCombine *pend = nullptr, bool prenormed = false,
+                          float *x_out = nullptr)
 {
     gtmoe_context *ctx = L->ctx;
     Workspace &w = L->ws;
@@ -528,7 +535,11 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         f.tile_off = w.tile_off;
         f.tile_desc = w.tile_desc;
         f.zero_out = zero_out;
-        if (pend) {  // x is the fp32 residual stream, updated in place first
+        // split routing where the workspace has the arrival counts
+        f.parts = w.part_cnt ? route_fused_parts(T, L->E, hash) : 1;
+        f.part_cnt = w.part_cnt;
+        f.x_out = x_out;
+        if (pend) {  // x is the fp32 residual stream, combined first (into x_out, or in place)
             f.pend_slot = pend->slot;
             f.pend_pos = pend->pos;
             f.pend_gates = pend->gates;
@@ -1862,6 +1873,10 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
     PendingCombine pending{};
     bool have_pending = false;
     bool prenormed = false;  // this layer's norm was done by the previous layer's combine
+    // Where the residual stream is: x, or, after a routing launch whose
+    // workgroups split a token's experts (and so could not combine in
+    // place), the first layer's second buffer.  Every combine kernel writes x.
+    float *cur = x;
     for (int l = 0; l < n_layers; ++l) {
         gtmoe_layer *L = layers[l];
         const int path = choose_path(L, T, flags);
@@ -1874,8 +1889,16 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
             continue;
         }
         Workspace &w = L->ws;
-        rc = prepare_and_route(L, T, Inputs{x, false, true}, ids, path, s, nullptr, have_pending ? &pending : nullptr,
-                               prenormed);
+        // a pending combine goes to the fused routing launch (it fits, or
+        // nothing would be pending); with split routing it writes the other
+        // residual buffer
+        // (split routing needs T <= kMaxSplitRouteTokens, the rows xalt holds)
+        float *out = nullptr;
+        if (have_pending && w.part_cnt && route_fused_parts(T, L->E, L->desc.use_hash_routing != 0) > 1)
+            out = cur == x ? layers[0]->ws.xalt : x;
+        rc = prepare_and_route(L, T, Inputs{cur, false, true}, ids, path, s, nullptr,
+                               have_pending ? &pending : nullptr, prenormed, out);
+        if (out) cur = out;
         have_pending = false;
         prenormed = false;
         if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
@@ -1899,12 +1922,14 @@ static int32_t stack_run(gtmoe_layer *const *layers, int32_t n_layers, int32_t T
             cn.ldb = N->dp;
             cn.inv = N->ws.inv;
             RUN(ctx, s, "combine_norm",
-                launch_combine(T, L->d, L->S, L->k, w.slot_out, true, pos, w.gates32, x, x, nullptr, s, cn));
+                launch_combine(T, L->d, L->S, L->k, w.slot_out, true, pos, w.gates32, cur, x, nullptr, s, cn));
             prenormed = true;
+            cur = x;
         } else {
             RUN(ctx, s, "combine",
-                launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, pos, w.gates32, x, x, nullptr,
-                               s));
+                launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, pos, w.gates32, cur, x,
+                               nullptr, s));
+            cur = x;
         }
         mark_forward(L, T, path, s);
     }

@@ -199,13 +199,25 @@ struct FusedArgs {
     int4 *tile_desc;
     float *zero_out;  // [T][d] rows zeroed by the token's workgroup, or nullptr
     // The previous stack layer's combine, done here before anything else
-    // (x is then float and updated in place): x[t] += shared rows + gate *
-    // routed slot rows, in the combine kernel's order and arithmetic.
+    // (x is then float): x[t] + shared rows + gate * routed slot rows, in the
+    // combine kernel's order and arithmetic, written to x_out (or in place
+    // when x_out is null, allowed with one part only).
     const float *pend_slot;    // that layer's fp32 slot outputs, or nullptr: nothing pending
     const int32_t *pend_pos;   // its pos table, or nullptr: slot rows at S*T + t*k + i
     const float *pend_gates;   // [T][k]
     int pend_S, pend_k;
+    float *x_out;
+    // parts > 1: each token's experts are split over that many workgroups,
+    // which publish their logits and count themselves in part_cnt[t] (kept
+    // zero between launches); the last to arrive runs the top-k.
+    int parts;
+    int32_t *part_cnt;
 };
+
+// Workgroups per token of the few-token routing: more than one only for
+// batches of up to kMaxSplitRouteTokens tokens and at least 32 experts.
+constexpr int kMaxSplitRouteTokens = 256;
+int route_fused_parts(int T, int E, bool hash);
 
 // Launchers (each returns the hipError_t of its launch).
 hipError_t launch_convert_inputs_f64(const double *x, int T, int d, float *xf, int ldf, uint16_t *xb, int ldb,

@@ -8,6 +8,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace gtmoe {
 
 // ---------------------------------------------------------------------------
@@ -819,19 +821,39 @@ __device__ __forceinline__ float4 in4(const double *row, int i)
 // (rows whose width is not a multiple of 4 re-read the input).  The small
 // operands (router and balance biases, norm weights) are loaded at the start
 // so that their latency overlaps the row's.
+//
+// With a.parts = P > 1 (few tokens, many experts) each token has P
+// workgroups, part p taking experts [p ceil(E/P), (p + 1) ceil(E/P)), so
+// that the router's rows are read by P CUs at once: every part prepares the
+// row (the pending combine and the norm, in registers), but only part 0
+// writes the combined residual row (to a.x_out, never in place: the other
+// parts still read the old row), the prepared row and the zeroed output
+// row.  Wave 0 of each part publishes its logits to a.logits and counts the
+// part in a.part_cnt[t]; the part that arrives last runs the top-k over all
+// of them and resets the count.  No part waits for another.  The logits
+// travel as agent-scope atomic stores and loads, which the hardware performs
+// at the device's point of coherence (write-through, past the XCD's L2), and
+// the count is incremented only once those stores are acknowledged
+// (s_waitcnt vmcnt(0)).  A release/acquire pair would give the same ordering
+// through a whole-L2 write-back per workgroup and an L2 invalidation per
+// token; measured, that cost more than the split saved.
 template <typename InT, bool NORM, bool HASH, int EPL, int NX>
 __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
     __shared__ double lg[kMaxExperts];
     __shared__ __attribute__((aligned(16))) float comb[NX * 256];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int t = blockIdx.x;
+    const int P = a.parts;
+    const int t = blockIdx.x / P, part = blockIdx.x - t * P;
+    const int epp = (a.E + P - 1) / P;
+    const int eb = part * epp, ee = min(a.E, eb + epp);  // this part's experts
     const InT *xr = reinterpret_cast<const InT *>(a.x) + (size_t)t * a.d;
     const bool vec = (a.d & 3) == 0;
 
     if constexpr (sizeof(InT) == 4) {
         if (a.pend_slot) {  // the previous layer's combine (combine_kernel's arithmetic)
-            float *x = const_cast<float *>(reinterpret_cast<const float *>(xr));
+            const float *xin_row = reinterpret_cast<const float *>(xr);
+            float *x = a.x_out ? a.x_out + (size_t)t * a.d : const_cast<float *>(xin_row);
             // the routed rows and gates of this token (at most 8; slots past
             // pend_k re-read slot 0 and are not added), all requested before
             // the adds, which keep the reference's order
@@ -848,14 +870,14 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
                 float v8[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v8[i] = row[i][c];
-                const float xc = x[c];
+                const float xc = xin_row[c];
                 float acc = 0.f;
                 for (int s = 0; s < a.pend_S; ++s) acc += a.pend_slot[((size_t)s * a.T + t) * a.d + c];
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     if (i < a.pend_k) acc = fmaf(g[i], v8[i], acc);
                 const float v = xc + acc;
-                x[c] = v;
+                if (part == 0) x[c] = v;
                 comb[c] = v;
             }
             __syncthreads();
@@ -867,7 +889,7 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     double bias_l = 0.0;
     double bal[EPL];
     if (!HASH) {
-        if (wave + 16 * lane < a.E) bias_l = a.bias[wave + 16 * lane];
+        if (eb + wave + 16 * lane < ee) bias_l = a.bias[eb + wave + 16 * lane];
         if (wave == 0) load_balance<EPL>(a.balance, a.E, lane, bal);
     }
     float4 nv = make_float4(1.f, 1.f, 1.f, 1.f);
@@ -903,9 +925,9 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     }
 
     if (!HASH) {
-        for (int e0 = wave; e0 < a.E; e0 += 32) {
+        for (int e0 = eb + wave; e0 < ee; e0 += 32) {
             const int e1 = e0 + 16;
-            const bool two = e1 < a.E;
+            const bool two = e1 < ee;
             const float *w0 = a.w + (size_t)e0 * a.kp;
             const float *w1 = a.w + (size_t)(two ? e1 : e0) * a.kp;
             float d0 = 0.f, d1 = 0.f;
@@ -929,8 +951,8 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
                 d0 += __shfl_xor(d0, off);
                 d1 += __shfl_xor(d1, off);
             }
-            // e0 = wave + 16 (2 it), e1 = e0 + 16: lanes 2 it and 2 it + 1
-            const int j0 = (e0 - wave) / 16;
+            // e0 = eb + wave + 16 (2 it), e1 = e0 + 16: lanes 2 it and 2 it + 1
+            const int j0 = (e0 - eb - wave) / 16;
             const double b0 = __shfl(bias_l, j0), b1 = __shfl(bias_l, j0 + 1);
             if (lane == 0) {
                 lg[e0] = (double)(d0 * inv) + b0;
@@ -938,8 +960,9 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
             }
         }
     }
-    // prepared row
-    if (vec) {
+    // prepared row (part 0)
+    if (part != 0) {
+    } else if (vec) {
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
             const int i = 4 * lane + 256 * j;
@@ -971,24 +994,42 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
             if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
         }
     }
-    if (a.zero_out)
+    if (a.zero_out && part == 0)
         for (int i = threadIdx.x; i < a.d; i += 1024) a.zero_out[(size_t)t * a.d + i] = 0.f;
     __syncthreads();
-    if (wave == 0) {
-        if (HASH) {
-            if (lane == 0) hash_token(a.ids, t, a.E, a.k, a.chosen, a.gates, a.gates32, nullptr);
-        } else {
-            topk_token<EPL>(lg, t, a.E, a.k, bal, lane, a.chosen, a.gates, a.gates32, nullptr);
-        }
+    if (wave != 0) return;
+    if (HASH) {
+        if (lane == 0) hash_token(a.ids, t, a.E, a.k, a.chosen, a.gates, a.gates32, nullptr);
+        return;
     }
+    if (P > 1) {
+        double *row = a.logits + (size_t)t * a.E;
+        for (int e = eb + lane; e < ee; e += 64)
+            __hip_atomic_store(row + e, lg[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): the stores are acknowledged
+        int prior = 0;
+        if (lane == 0) prior = __hip_atomic_fetch_add(a.part_cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__shfl(prior, 0) != P - 1) return;  // not the last part
+        for (int e = lane; e < a.E; e += 64) lg[e] = __hip_atomic_load(row + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_store(a.part_cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    topk_token<EPL>(lg, t, a.E, a.k, bal, lane, a.chosen, a.gates, a.gates32, nullptr);
 }
 
 bool fused_route_fits(int T, int k, int kp) { return T >= 1 && T * k <= kFusedMaxTK && T <= 1024 && kp <= 4096; }
 
+// Parts per token: enough workgroups for every CU (256), at least 16
+// experts per part, at most 8 parts; one for hash routing.
+int route_fused_parts(int T, int E, bool hash)
+{
+    if (hash || T <= 0 || T > kMaxSplitRouteTokens) return 1;
+    return std::max(1, std::min({(256 + T - 1) / T, E / 16, 8}));
+}
+
 template <typename InT, bool NORM, int NX>
 static hipError_t launch_token_nx(const FusedArgs &a, bool hash, hipStream_t s)
 {
-    dim3 grid(a.T);
+    dim3 grid(a.T * a.parts);
     if (hash) hipLaunchKernelGGL((route_token_kernel<InT, NORM, true, 1, NX>), grid, dim3(1024), 0, s, a);
     else if (a.E <= 64) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 1, NX>), grid, dim3(1024), 0, s, a);
     else if (a.E <= 128) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 2, NX>), grid, dim3(1024), 0, s, a);
@@ -1009,6 +1050,10 @@ static hipError_t launch_token_typed(const FusedArgs &a, bool hash, hipStream_t 
 hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, bool dispatch, hipStream_t s)
 {
     if (!fused_route_fits(a.T, a.k, a.kp)) return hipErrorInvalidValue;
+    // more than one part needs the arrival counts, and a pending combine
+    // then must not be written in place
+    if (a.parts < 1 || (a.parts > 1 && (hash || !a.part_cnt || (a.pend_slot && (!a.x_out || a.x_out == a.x)))))
+        return hipErrorInvalidValue;
     hipError_t e;
     if (input_f64) e = a.norm ? launch_token_typed<double, true>(a, hash, s) : launch_token_typed<double, false>(a, hash, s);
     else e = a.norm ? launch_token_typed<float, true>(a, hash, s) : launch_token_typed<float, false>(a, hash, s);
