@@ -76,11 +76,15 @@ def test_graph_forward_replays_equal_eager(ctx, T, path, S):
     assert rel_err(eager0, ref.outputs) <= tol
 
 
-@pytest.mark.parametrize("T,path", [(8, gt.PATH_FP32), (96, gt.PATH_BF16)])
-def test_graph_stack_replays_equal_eager(ctx, T, path):
-    say(f"graph stack T={T} path={path}")
+# E = 64 at T = 8: the routing splits each token's experts over several
+# workgroups (arrival counts that reset themselves, replay after replay) and
+# the residual alternates between x and a second buffer; four layers end
+# with the last combine reading the second buffer.
+@pytest.mark.parametrize("T,path,E,nl", [(8, gt.PATH_FP32, 6, 3), (96, gt.PATH_BF16, 6, 3), (8, gt.PATH_FP32, 64, 4)])
+def test_graph_stack_replays_equal_eager(ctx, T, path, E, nl):
+    say(f"graph stack T={T} path={path} E={E} layers={nl}")
     d = 128
-    specs = [make_moe(gt.encode_rows, d=d, h=192, E=6, k=2, S=1, precision=FP4, seed=30 + i) for i in range(3)]
+    specs = [make_moe(gt.encode_rows, d=d, h=192, E=E, k=2, S=1, precision=FP4, seed=30 + i) for i in range(nl)]
     rng = np.random.default_rng(31)
     x0 = rng.standard_normal((T, d))
     layers = [gt.MixtureOfExperts.from_spec(ctx, s) for s in specs]
