@@ -267,6 +267,153 @@ __global__ __launch_bounds__(64 * NW) void router_mfma_kernel(const float *__res
     }
 }
 
+// Many tokens, staged through LDS: a workgroup computes 32 tokens x 32 NE
+// experts with v_mfma_f32_32x32x2_f32 as router_mfma_kernel does, but the
+// token and router rows reach LDS in 64-value chunks by 16-byte LDS-DMA
+// loads (four rows of 256 bytes per wave load, so each load reads whole
+// cache lines), four chunk buffers, three chunks in flight ahead of the one
+// multiplied.  The 16-byte slots of row R are XOR-swizzled by R % 16, so
+// that the operand reads (32 rows, one slot each) touch every bank once per
+// 16 lanes.  Wave w multiplies slots 2w and 2w + 1 of every chunk (lane l:
+// row l % 32, slot 2w + l / 32, the slot's four values over four chained
+// MFMAs); the waves' partial tiles are added in wave order at the end.  Rows
+// past T or E read the last valid row and are not written.
+constexpr long long kRouterStagedWgs = 256;  // one workgroup per CU at least
+constexpr int kRawBufferWord3 = 0x00020000;  // descriptor word 3 for raw (untyped) buffer access on CDNA
+
+template <int NE>
+constexpr int router_lds_buf()
+{
+    return 32 * 256 + 32 * NE * 256;  // a chunk's token rows and router rows
+}
+
+// (the body is a device function: its LDS-DMA address casts have no host
+// form, and the kernel's host-side stub is only emitted for a body without)
+template <int NE>
+__device__ __forceinline__ void router_lds_body(const float *__restrict__ x, int ldx, int T, int kp,
+                                                const float *__restrict__ w, int ldw, const double *__restrict__ bias,
+                                                int E, double *__restrict__ logits, const float *__restrict__ row_scale,
+                                                char *s0, char *s1, char *s2, char *s3)
+{
+    constexpr int NW = 8;
+    constexpr int XB = 32 * 256;            // a chunk's token rows
+    constexpr int BUF = router_lds_buf<NE>();
+    constexpr int PER_WAVE = 16 * NE * 64;  // floats of a wave's partial tiles
+    static_assert(2 * PER_WAVE * 4 <= BUF, "two waves' partial tiles per chunk buffer");
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32 * NE;
+    const int nchunks = kp / 64;
+
+    // DMA: wave w loads rows 4w .. 4w + 3 of the token tile and of each
+    // expert tile; lane l takes row 4w + l / 16 and writes LDS slot l % 16
+    // of it, which holds the row's 16-byte slot (l % 16) ^ (row % 16)
+    const __amdgpu_buffer_rsrc_t xsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x), 0, (int)((long long)T * ldx * 4), kRawBufferWord3);
+    const __amdgpu_buffer_rsrc_t wsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(w), 0, (int)((long long)E * ldw * 4), kRawBufferWord3);
+    const int rl = 4 * wave + (lane >> 4);
+    const int sw = ((lane & 15) ^ (rl & 15)) * 16;  // bytes into the chunk
+    const uint32_t xvo = (uint32_t)min(t0 + rl, T - 1) * (uint32_t)ldx * 4u + (uint32_t)sw;
+    uint32_t wvo[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j) wvo[j] = (uint32_t)min(e0 + 32 * j + rl, E - 1) * (uint32_t)ldw * 4u + (uint32_t)sw;
+    auto dma = [&](char *buf, int chunk) {
+        const int so = min(chunk, nchunks - 1) * 256;  // past the last chunk: the last again, never read
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xsrc, (__attribute__((address_space(3))) void *)(buf + 4 * wave * 256),
+                                                 16, xvo, so, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NE; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wsrc, (__attribute__((address_space(3))) void *)(buf + XB + (32 * j + 4 * wave) * 256), 16, wvo[j], so,
+                0, 0);
+    };
+    // operand reads: row r = l % 32, slot c = 2 wave + l / 32
+    const int r = lane & 31, c = 2 * wave + (lane >> 5);
+    const int ro = r * 256 + ((c ^ (r & 15)) * 16);
+    floatx16 acc[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[j][i] = 0.f;
+    auto compute = [&](const char *buf) {
+        const float4 xv = *reinterpret_cast<const float4 *>(buf + ro);
+        float4 wv[NE];
+#pragma unroll
+        for (int j = 0; j < NE; ++j) wv[j] = *reinterpret_cast<const float4 *>(buf + XB + j * 32 * 256 + ro);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < NE; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32((&xv.x)[s], (&wv[j].x)[s], acc[j], 0, 0, 0);
+    };
+    // chunk i's loads are done once at most the two later chunks' are in flight
+    constexpr int kDma = 1 + NE;
+    constexpr int kWait = (2 * kDma & 15) | (((2 * kDma) >> 4) << 14) | (7 << 4);  // vmcnt(2 kDma) lgkmcnt(0)
+    auto step = [&](char *cur, char *ahead, int i) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kWait);
+        __builtin_amdgcn_s_barrier();  // every wave's part of chunk i is in; chunk i - 1 is read
+        __builtin_amdgcn_sched_barrier(0);
+        dma(ahead, i + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(cur);
+    };
+    dma(s0, 0);
+    dma(s1, 1);
+    dma(s2, 2);
+    for (int i = 0; i < nchunks; i += 4) {  // nchunks is a multiple of 4 (the launcher checks)
+        step(s0, s3, i);
+        step(s1, s0, i + 1);
+        step(s2, s1, i + 2);
+        step(s3, s2, i + 3);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the loads past the last chunk have landed too
+    __syncthreads();                // and every read of the chunk buffers is done
+    // the waves' partial tiles, two per chunk buffer
+    auto part = [&](int q) -> float * {
+        char *b = q < 2 ? s0 : q < 4 ? s1 : q < 6 ? s2 : s3;
+        return reinterpret_cast<float *>(b) + (q & 1) * PER_WAVE;
+    };
+    {
+        float *mine = part(wave);
+#pragma unroll
+        for (int j = 0; j < NE; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mine[(16 * j + i) * 64 + lane] = acc[j][i];
+    }
+    __syncthreads();
+    // accumulator register i of tile j in lane l is token row
+    // 8*(i/4) + 4*(l/32) + i%4, expert 32 j + l%32; wave q finishes the
+    // registers 16 j + i = q, q + NW, ...
+    const int h = lane >> 5;
+    for (int ji = wave; ji < 16 * NE; ji += NW) {
+        const int j = ji >> 4, i = ji & 15;
+        const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), e = e0 + 32 * j + r;
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) v += part(q)[ji * 64 + lane];
+        if (t < T && e < E) {
+            if (row_scale) v = row_scale[t] * v;
+            logits[(size_t)t * E + e] = (double)v + bias[e];
+        }
+    }
+}
+
+template <int NE>
+__global__ __launch_bounds__(512) void router_lds_kernel(const float *__restrict__ x, int ldx, int T, int kp,
+                                                         const float *__restrict__ w, int ldw,
+                                                         const double *__restrict__ bias, int E,
+                                                         double *__restrict__ logits,
+                                                         const float *__restrict__ row_scale)
+{
+    // four separate arrays, so that the compiler tracks the loads into each
+    __shared__ __attribute__((aligned(16))) char s0[router_lds_buf<NE>()];
+    __shared__ __attribute__((aligned(16))) char s1[router_lds_buf<NE>()];
+    __shared__ __attribute__((aligned(16))) char s2[router_lds_buf<NE>()];
+    __shared__ __attribute__((aligned(16))) char s3[router_lds_buf<NE>()];
+    router_lds_body<NE>(x, ldx, T, kp, w, ldw, bias, E, logits, row_scale, s0, s1, s2, s3);
+}
+
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
                          double *logits, hipStream_t s, const float *row_scale)
 {
@@ -284,7 +431,18 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
         // CUs, with four waves over K if that is enough, else eight; one
         // tile and four waves otherwise
         const long long tiles2 = (long long)((T + 31) / 32) * ((E + 63) / 64);
-        if (E > 32 && tiles2 * 8 >= kRouterWaves) {
+        const long long tiles1 = (long long)((T + 31) / 32) * ((E + 31) / 32);
+        const bool staged = kp % 256 == 0 && (long long)T * ldx * 4 <= 0x7fffffffLL &&
+                            (long long)E * ldw * 4 <= 0x7fffffffLL;
+        if (staged && E > 32 && tiles2 >= kRouterStagedWgs) {
+            dim3 grid((T + 31) / 32, (E + 63) / 64);
+            hipLaunchKernelGGL((router_lds_kernel<2>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
+                               row_scale);
+        } else if (staged && tiles1 >= kRouterStagedWgs) {
+            dim3 grid((T + 31) / 32, (E + 31) / 32);
+            hipLaunchKernelGGL((router_lds_kernel<1>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
+                               row_scale);
+        } else if (E > 32 && tiles2 * 8 >= kRouterWaves) {
             dim3 grid((T + 31) / 32, (E + 63) / 64);
             if (tiles2 * 4 >= kRouterWaves)
                 hipLaunchKernelGGL((router_mfma_kernel<2, 4>), grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E,
