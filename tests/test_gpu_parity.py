@@ -174,6 +174,7 @@ FEW = {
     "C5 block, 16 experts": (dict(d=2048, h=1024, E=16, k=4, S=1), FP4),
     "C2 shape": (dict(d=1024, h=2048, E=16, k=2, S=0), FP4),
     "clamped, one shared": (dict(d=512, h=512, E=4, k=2, S=1, clamp=0.3, std=0.05), INT8),
+    "hashed, two shared": (dict(d=512, h=1024, E=8, k=3, S=2, use_hash=True), FP4),
 }
 
 
@@ -191,11 +192,18 @@ def test_few_token_decode(ctx, name):
     try:
         for T in (1, 6):
             say(f"few tokens {name} T={T}")
-            x = np.random.default_rng(22 + T).normal(size=(T, cfg["d"]))
-            y = m.forward(x, None, path=gt.PATH_AUTO)
+            rng = np.random.default_rng(22 + T)
+            x = rng.normal(size=(T, cfg["d"]))
+            ids = rng.integers(0, 5000, T) if cfg.get("use_hash") else None
+            y = m.forward(x, ids, path=gt.PATH_AUTO)
             r = m.last_routing()
             assert m.last_path == gt.PATH_FP32
-            check_routing(r.chosen, spec, x, cfg["k"], f"few tokens {name} T={T}")
+            if ids is None:
+                check_routing(r.chosen, spec, x, cfg["k"], f"few tokens {name} T={T}")
+            else:
+                assert np.array_equal(r.chosen, oracle.hash_route(ids, cfg["E"], cfg["k"]).chosen)
+            # the dispatch tables, built on request, agree with the oracle's
+            assert np.array_equal(m.last_expert_load(), oracle.dispatch(r.chosen, cfg["E"]).load)
             ref = oracle.moe_forward_routed(spec, x, r.chosen, r.gates, threads=8)
             e = rel_err(y, ref.outputs)
             say(f"few tokens {name} T={T} max rel err {e:.3e}")
