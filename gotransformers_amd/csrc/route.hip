@@ -806,12 +806,15 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
     dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, tile_desc, sh);
 }
 
-// Many tokens: chunks of 256 tokens (4 waves) per workgroup.
+// Many tokens: chunks of kChunk tokens per workgroup.
 //   count:   per-chunk, per-expert counts            -> chunk_cnt[c][e]
 //   scan:    one workgroup: per-expert totals, offsets, the group tables, and
 //            every chunk's starting position per expert -> chunk_cnt[c][e]
 //   scatter: per chunk, wave ranks + the chunk's base  -> rows, pos, tok
-constexpr int kChunk = 256;
+// 128 tokens per chunk: twice the workgroups of 256 for a shorter
+// per-workgroup chain (C3 dispatch 16.5 → 15.6 µs); every placement
+// workgroup reads all chunks' counts, so the chunks are not made smaller
+constexpr int kChunk = 128;
 
 __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(const int32_t *__restrict__ chosen, int T, int k, int E,
                                                                 int32_t *__restrict__ chunk_cnt)
@@ -876,15 +879,17 @@ __global__ __launch_bounds__(1024) void dispatch_place_kernel(const int32_t *__r
     block_exclusive_scan(sh.cnt, sh.base, E, sh.wave_sums, &sh.total);
     if (c == 0) write_group_tables(T, k, E, S, bm, sh, load, offsets, goff, tok, tile_off, tile_desc);
 
-    // ranks inside the chunk: wave w covers token-wave w/4 and the experts
-    // e = w%4 (mod 4)
-    const int tw = wave >> 2, sub = wave & 3;
+    // ranks inside the chunk: the 16 waves cover the chunk's kChunk / 64
+    // token-waves, kSubsets waves per token-wave; wave w covers token-wave
+    // w / kSubsets and the experts e = w % kSubsets (mod kSubsets)
+    constexpr int kSubsets = 16 / (kChunk / 64);
+    const int tw = wave / kSubsets, sub = wave % kSubsets;
     const int tl = tw * 64 + lane;
     const int t = c * kChunk + tl;
     int ce[kMaxK];
 #pragma unroll
     for (int i = 0; i < kMaxK; ++i) ce[i] = (t < T && i < k) ? chosen[(size_t)t * k + i] : -1;
-    for (int e = sub; e < E; e += 4) {
+    for (int e = sub; e < E; e += kSubsets) {
         int match = -1;
 #pragma unroll
         for (int i = 0; i < kMaxK; ++i)
