@@ -56,11 +56,13 @@ struct ChunkRegs {
     float s[MATS][Chunk<PREC>::CB];
 };
 
-// Chunks in flight per wave (register ring).
+// Chunks in flight per wave (register ring): three for FP4 gate/up, whose
+// chunks are half the bytes of Int8's (C5 decode gate/up 1183 -> 1158 us per
+// step), two otherwise (a third chunk measured slower for Int8).
 template <int PREC, int MATS, int NQ>
 constexpr int ring_depth()
 {
-    return 2;
+    return PREC == kFP4 && MATS == 2 ? 3 : 2;
 }
 
 // One weight matrix's panel as buffer resources: the panel's codes (64 rows
