@@ -215,7 +215,7 @@ struct FusedArgs {
 };
 
 // Workgroups per token of the few-token routing: more than one only for
-// batches of up to kMaxSplitRouteTokens tokens and at least 32 experts.
+// batches of up to kMaxSplitRouteTokens tokens and at least 64 experts.
 constexpr int kMaxSplitRouteTokens = 256;
 int route_fused_parts(int T, int E, bool hash);
 

@@ -1181,12 +1181,14 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 
 bool fused_route_fits(int T, int k, int kp) { return T >= 1 && T * k <= kFusedMaxTK && T <= 1024 && kp <= 4096; }
 
-// Parts per token: enough workgroups for every CU (256), at least 16
-// experts per part, at most 8 parts; one for hash routing.
+// Parts per token: up to 128 workgroups in all, at least 32 experts per
+// part, at most 8 parts; one for hash routing.  Every part repeats the
+// token's combine and norm, so fewer, larger parts won: at C5 decode (T=64,
+// E=64) 2 parts took 421 us of routing per step, 4 parts 438, 8 parts 592.
 int route_fused_parts(int T, int E, bool hash)
 {
     if (hash || T <= 0 || T > kMaxSplitRouteTokens) return 1;
-    return std::max(1, std::min({(256 + T - 1) / T, E / 16, 8}));
+    return std::max(1, std::min({(128 + T - 1) / T, E / 32, 8}));
 }
 
 template <typename InT, bool NORM, int NX>
