@@ -302,6 +302,10 @@ int32_t alloc_matrix(gtmoe_context *ctx, DeviceMatrix &m, int precision, int row
         const size_t sb = (size_t)groups * m.group_scales() * sizeof(float);
         HIP_TRY(ctx, hipMalloc(&m.scales, sb));
         HIP_TRY(ctx, hipMemset(m.scales, 0, sb));
+    } else {
+        const size_t hb = (size_t)groups * m.group_bf16_bytes();
+        HIP_TRY(ctx, hipMalloc(&m.bf16, hb));
+        HIP_TRY(ctx, hipMemset(m.bf16, 0, hb));
     }
     const size_t bb = (size_t)groups * rows * sizeof(float);
     HIP_TRY(ctx, hipMalloc(&m.biases, bb));
@@ -314,9 +318,11 @@ void free_matrix(DeviceMatrix &m)
     if (m.values) (void)hipFree(m.values);
     if (m.scales) (void)hipFree(m.scales);
     if (m.biases) (void)hipFree(m.biases);
+    if (m.bf16) (void)hipFree(m.bf16);
     m.values = nullptr;
     m.scales = nullptr;
     m.biases = nullptr;
+    m.bf16 = nullptr;
 }
 
 // Check a Rows snapshot like RowsFromSnapshot (lowprecision/rows.go:172-203).
@@ -697,6 +703,12 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s, float *final
         a.out = w.hidden16;
         a.ldo = L->hp;
         a.clamp = (float)L->desc.clamp_limit;
+        if (L->gate.precision == kFloat32) {  // Float32 experts: their rows' bf16 copies
+            a.w0 = L->gate.bf16;
+            a.w1 = L->up.bf16;
+            a.w_group_stride = (long long)L->gate.group_bf16_bytes();
+            a.row_bytes = L->gate.bf16_row_bytes();
+        }
         L->last_mfma[0] = a;
         L->last_max_tiles = max_tiles;
         L->relaunch_ready = true;
@@ -719,6 +731,11 @@ int32_t run_experts(gtmoe_layer *L, int T, int path, hipStream_t s, float *final
         b.desc = w.tile_desc;
         b.out = w.slot_out;
         b.ldo = L->d;
+        if (L->down.precision == kFloat32) {
+            b.w0 = L->down.bf16;
+            b.w_group_stride = (long long)L->down.group_bf16_bytes();
+            b.row_bytes = L->down.bf16_row_bytes();
+        }
         L->last_mfma[1] = b;
         RUN(ctx, s, "mfma_down", launch_mfma_down(b, L->down.precision, max_tiles, s));
     }
@@ -1538,6 +1555,11 @@ int32_t gtmoe_upload_rows(gtmoe_layer *L, int32_t role, int32_t index, const gtm
     }
     HIP_TRY(ctx, hipMemcpy((char *)m.values + (size_t)group * m.group_value_bytes(), vals.data(), vals.size(),
                            hipMemcpyHostToDevice));
+    if (m.precision == kFloat32) {  // and the group's bf16 copy for the prefill GEMM
+        HIP_TRY(ctx, launch_bf16_rows((char *)m.values + (size_t)group * m.group_value_bytes(),
+                                      (char *)m.bf16 + (size_t)group * m.group_bf16_bytes(), m.rows_p, m.kp, nullptr));
+        HIP_TRY(ctx, hipStreamSynchronize(nullptr));
+    }
     if (m.precision != kFloat32) {
         const int src_blocks = (m.width + 15) / 16;
         std::vector<float> sc(m.group_scales(), 0.f);

@@ -63,8 +63,13 @@ struct DeviceMatrix {
     void *values = nullptr;
     float *scales = nullptr;
     float *biases = nullptr;
+    // Float32 experts only: the rows rounded to bf16 (nearest even), in the
+    // same panel layout with 8 values per 16-byte unit, for the prefill GEMM
+    void *bf16 = nullptr;
     size_t group_value_bytes() const { return (size_t)rows_p * row_bytes; }
     size_t group_scales() const { return (size_t)rows_p * nblocks; }
+    int bf16_row_bytes() const { return kp * 2; }
+    size_t group_bf16_bytes() const { return (size_t)rows_p * bf16_row_bytes(); }
 };
 
 // Arguments of the expert GEMV kernels (fp32 path).
@@ -245,6 +250,8 @@ hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, in
                            int32_t *tile_off, int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s);
 hipError_t launch_gemv_gateup(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
 hipError_t launch_gemv_down(const GemvArgs &a, int precision, int max_slices, hipStream_t s);
+// The bf16 copy of Float32 rows (panel layout): rows_p rows of kp values.
+hipError_t launch_bf16_rows(const void *rows_f32, void *rows_bf16, int rows_p, int kp, hipStream_t s);
 hipError_t launch_mfma_gateup(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 hipError_t launch_mfma_down(const MfmaArgs &a, int precision, int max_tiles, hipStream_t s);
 int mfma_tile_m();

@@ -80,7 +80,7 @@ struct BRaw<kFP4> {
 };
 template <>
 struct BRaw<kFloat32> {
-    uint4 q[2][4];
+    uint4 q[2][2];  // Float32 experts: the block's 16 values from the rows' bf16 copy
 };
 
 // descriptor word 3 for raw (untyped) buffer access on CDNA
@@ -109,11 +109,12 @@ __device__ __forceinline__ void load_block(BRaw<PREC> &r, int i, const GroupSrc 
         // unit 2m + h (blocks 4m + 2h and 4m + 2h + 1); vo carries h * 1024
         if (p == 0) r.u = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, 2 * m * 1024, 0));
     } else {
-        // units 4b .. 4b + 3; vo carries 4h * 1024
+        // Float32 experts read their rows' bf16 copy (8 values per unit):
+        // units 2b, 2b + 1; vo carries 2h * 1024
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 2; ++u)
             r.q[i][u] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, ((4 * m + 2 * p) * 4 + u) * 1024, 0));
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(src.codes, vo, ((4 * m + 2 * p) * 2 + u) * 1024, 0));
     }
 }
 
@@ -161,11 +162,9 @@ __device__ __forceinline__ bf16x8 dequant_half(const BRaw<PREC> &r, int i, int h
         o[2] = pack_bf16(f2[0] * s, f2[1] * s);
         o[3] = pack_bf16(f3[0] * s, f3[1] * s);
     } else {
-        const uint4 a = r.q[i][2 * h], b = r.q[i][2 * h + 1];
-        o[0] = pack_bf16(__uint_as_float(a.x), __uint_as_float(a.y));
-        o[1] = pack_bf16(__uint_as_float(a.z), __uint_as_float(a.w));
-        o[2] = pack_bf16(__uint_as_float(b.x), __uint_as_float(b.y));
-        o[3] = pack_bf16(__uint_as_float(b.z), __uint_as_float(b.w));
+        // already bf16 (the fp32 rows rounded to nearest even at upload, as
+        // pack_bf16 rounds): no arithmetic
+        return __builtin_bit_cast(bf16x8, r.q[i][h]);
     }
     return __builtin_bit_cast(bf16x8, o);
 }
@@ -269,7 +268,7 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
         const uint32_t rowoff = (uint32_t)(n / 64) * 64u * (uint32_t)a.row_bytes + (uint32_t)(n % 64) * 16u;
         if constexpr (PREC == kInt8) bvo[j] = rowoff + h * 1024u;
         else if constexpr (PREC == kFP4) bvo[j] = rowoff + h * 1024u;
-        else bvo[j] = rowoff + h * 4096u;
+        else bvo[j] = rowoff + h * 2048u;
         if constexpr (PREC != kFloat32) {
             bsrc[j].scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(sc) + (size_t)g * a.s_group_stride, 0,
                                                              (int)(a.s_group_stride * 4), kRawBufferWord3);
@@ -292,9 +291,10 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     // on their way into LDS buffer (k + 2) % 3 (buffer (k + 2) % 3 was read
     // in step k - 1, before the barrier that ended it) and the weights of
     // step k + NS into register stage k % NS (its pair 1 is dequantized at
-    // the start of step k): NS = 3 stages, or 2 for fp32 rows, whose stages
-    // are four times larger.  The loop is unrolled by three (six for two
-    // stages) so the buffer and stage indices are constants; every load is
+    // the start of step k): NS = 3 stages, or 2 for Float32 experts, whose
+    // bf16 rows make stages a third larger than Int8's codes and scales.
+    // The loop is unrolled by three (six for two stages) so the buffer and
+    // stage indices are constants; every load is
     // issued unconditionally (steps past the end re-load the last step:
     // cache hits, never used), so that each step issues the same VMEM
     // instructions in the same order: MI activation loads, then NB weight
@@ -307,7 +307,7 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     constexpr int NS = PREC == kFloat32 ? 2 : 3;
     constexpr int UNROLL = NS == 3 ? 3 : 6;
     BRaw<PREC> bq[NS][2];  // [stage][column tile]
-    constexpr int NB = PREC == kInt8 ? 6 : PREC == kFP4 ? 4 : 16;
+    constexpr int NB = PREC == kInt8 ? 6 : PREC == kFP4 ? 4 : 8;
     constexpr int VM = 2 * NB + MI;
     static_assert(VM < 64, "vmcnt holds six bits");
     // s_waitcnt vmcnt(n) lgkmcnt(0), expcnt not waited for
@@ -536,6 +536,35 @@ __global__ __launch_bounds__(256, 2) void mfma_gemm_kernel(MfmaArgs a)
 }
 
 int mfma_tile_m() { return BM; }
+
+// One 16-byte unit of the bf16 copy per thread: fp32 units 2u and 2u + 1 of
+// a row (8 values), rounded as pack_bf16 rounds.  Threads run down the rows
+// of a unit, so reads and writes are contiguous within each panel.
+__global__ __launch_bounds__(256) void bf16_rows_kernel(const char *__restrict__ src, char *__restrict__ dst,
+                                                        int rows_p, int kp)
+{
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int units = kp / 8;
+    if (idx >= (long long)rows_p * units) return;
+    const int r = (int)(idx % rows_p), u = (int)(idx / rows_p);
+    const uint4 a = *reinterpret_cast<const uint4 *>(src + panel_unit_offset(r, 2 * u, kp * 4));
+    const uint4 b = *reinterpret_cast<const uint4 *>(src + panel_unit_offset(r, 2 * u + 1, kp * 4));
+    uint4 o;
+    o.x = pack_bf16(__uint_as_float(a.x), __uint_as_float(a.y));
+    o.y = pack_bf16(__uint_as_float(a.z), __uint_as_float(a.w));
+    o.z = pack_bf16(__uint_as_float(b.x), __uint_as_float(b.y));
+    o.w = pack_bf16(__uint_as_float(b.z), __uint_as_float(b.w));
+    *reinterpret_cast<uint4 *>(dst + panel_unit_offset(r, u, kp * 2)) = o;
+}
+
+hipError_t launch_bf16_rows(const void *rows_f32, void *rows_bf16, int rows_p, int kp, hipStream_t s)
+{
+    if (rows_p <= 0 || kp <= 0 || kp % 8 != 0) return hipErrorInvalidValue;
+    const long long n = (long long)rows_p * (kp / 8);
+    hipLaunchKernelGGL(bf16_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const char *>(rows_f32), static_cast<char *>(rows_bf16), rows_p, kp);
+    return hipGetLastError();
+}
 
 namespace {
 
