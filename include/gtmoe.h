@@ -75,7 +75,9 @@ typedef struct gtmoe_layer_desc {
     int32_t shared_experts;     /* S >= 0 */
     int32_t routed_experts;     /* E in [1, 256] */
     int32_t experts_per_token;  /* k in [1, min(E, 8)] */
-    int32_t precision;          /* expert weights: GTMOE_FLOAT32, GTMOE_INT8 or GTMOE_FP4 */
+    int32_t precision;          /* expert weights: GTMOE_FLOAT32, GTMOE_INT8 or GTMOE_FP4
+                                   (FLOAT32 rows also keep a bf16 copy on the device, for the
+                                   many-token path: 6 bytes per weight in all) */
     int32_t use_hash_routing;   /* MixtureOfExperts.UseHashRouting */
     int32_t reserved;
     double clamp_limit;         /* > 0: clamped SwiGLU (feedforward.NewClampedSwiGLU); 0: SwiGLU */
