@@ -586,14 +586,17 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
     } else if (in.f64) {
         RUN(ctx, s, "convert_inputs",
             launch_convert_inputs_f64((const double *)in.x, T, L->d, xf, L->dp, xb, L->dp, s));
-    } else {
+    } else if (xf != nullptr || hash) {
         RUN(ctx, s, "convert_inputs",
             launch_convert_inputs_f32((const float *)in.x, T, L->d, xf, L->dp, xb, L->dp, s));
     }
+    // an fp32 input read in place by the router: the router writes its bf16 rows
+    uint16_t *router_xb = xf == nullptr && !in.f64 && !in.norm && !hash ? xb : nullptr;
     if (hash) {
         RUN(ctx, s, "hash_route", launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
     } else {
-        RUN(ctx, s, "router", launch_router(xr, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s));
+        RUN(ctx, s, "router", launch_router(xr, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s,
+                                            nullptr, router_xb, L->dp));
         RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
     }
     RUN(ctx, s, "dispatch",

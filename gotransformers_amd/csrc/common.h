@@ -232,9 +232,12 @@ hipError_t launch_convert_inputs_f32(const float *x, int T, int d, float *xf, in
 hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *xf, int ldf, uint16_t *xb, int ldb,
                           hipStream_t s);
 // row_scale (optional, [T]): each row's logits are scale * dot + bias (the
-// inverse RMS of a row whose norm weights are folded into w).
+// inverse RMS of a row whose norm weights are folded into w).  xb (optional,
+// rows of ldb >= d bf16 values, x unpadded: ldx == d, d % 64 == 0): also
+// write x as bf16, as the input conversion would.
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
-                         double *logits, hipStream_t s, const float *row_scale = nullptr);
+                         double *logits, hipStream_t s, const float *row_scale = nullptr, uint16_t *xb = nullptr,
+                         int ldb = 0);
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
                        double *gates, float *gates32, hipStream_t s);
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,

@@ -9,6 +9,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace gtmoe {
 
@@ -287,13 +288,28 @@ constexpr int router_lds_buf()
     return 32 * 256 + 32 * NE * 256;  // a chunk's token rows and router rows
 }
 
+// Four floats as bf16 (nearest even), packed in 8 bytes (the rounding of
+// the input conversion's bf16 rows).
+__device__ __forceinline__ uint2 router_bf16x4(float4 v)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){v.x, v.y}, bf16x2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){v.z, v.w}, bf16x2)));
+}
+
 // (the body is a device function: its LDS-DMA address casts have no host
 // form, and the kernel's host-side stub is only emitted for a body without)
-template <int NE>
+// CONV: the workgroup also writes its 32 token rows as bf16 (xb, rows of
+// ldb values): each lane reads back the 16 bytes its own DMA put in LDS (row
+// 4 w + l / 16, the row's slot (l % 16) ^ (row % 16)), so the 16 lanes of a
+// row store one contiguous 128-byte run of it, after the chunk's products.
+template <int NE, bool CONV>
 __device__ __forceinline__ void router_lds_body(const float *__restrict__ x, int ldx, int T, int kp,
                                                 const float *__restrict__ w, int ldw, const double *__restrict__ bias,
                                                 int E, double *__restrict__ logits, const float *__restrict__ row_scale,
-                                                char *s0, char *s1, char *s2, char *s3)
+                                                uint16_t *__restrict__ xb, int ldb, char *s0, char *s1, char *s2,
+                                                char *s3)
 {
     constexpr int NW = 8;
     constexpr int XB = 32 * 256;            // a chunk's token rows
@@ -330,13 +346,19 @@ __device__ __forceinline__ void router_lds_body(const float *__restrict__ x, int
     // operand reads: row r = l % 32, slot c = 2 wave + l / 32
     const int r = lane & 31, c = 2 * wave + (lane >> 5);
     const int ro = r * 256 + ((c ^ (r & 15)) * 16);
+    // rows past T hold row T - 1 (the DMA clamps the row): their lanes store
+    // the same bits to row T - 1, so every wave issues every chunk's store
+    uint2 *xbo = CONV ? reinterpret_cast<uint2 *>(xb + (size_t)min(t0 + rl, T - 1) * ldb + sw / 4) : nullptr;
+    const int own = 4 * wave * 256 + 16 * lane;  // this lane's DMA slot in a chunk buffer
     floatx16 acc[NE];
 #pragma unroll
     for (int j = 0; j < NE; ++j)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[j][i] = 0.f;
-    auto compute = [&](const char *buf) {
+    auto compute = [&](const char *buf, int i) {
         const float4 xv = *reinterpret_cast<const float4 *>(buf + ro);
+        float4 xo;
+        if constexpr (CONV) xo = *reinterpret_cast<const float4 *>(buf + own);
         float4 wv[NE];
 #pragma unroll
         for (int j = 0; j < NE; ++j) wv[j] = *reinterpret_cast<const float4 *>(buf + XB + j * 32 * 256 + ro);
@@ -345,27 +367,40 @@ __device__ __forceinline__ void router_lds_body(const float *__restrict__ x, int
 #pragma unroll
             for (int j = 0; j < NE; ++j)
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32((&xv.x)[s], (&wv[j].x)[s], acc[j], 0, 0, 0);
+        if constexpr (CONV) xbo[16 * i] = router_bf16x4(xo);  // columns 64 i + sw / 4 .. + 3
     };
-    // chunk i's loads are done once at most the two later chunks' are in flight
+    // chunk i's loads are done once at most the two later chunks' are in
+    // flight, and (CONV) the stores of up to three earlier chunks: vector
+    // memory operations are counted in issue order, a chunk's store after its
+    // products, so step i waits for vmcnt(2 kDma + min(i, 3))
     constexpr int kDma = 1 + NE;
-    constexpr int kWait = (2 * kDma & 15) | (((2 * kDma) >> 4) << 14) | (7 << 4);  // vmcnt(2 kDma) lgkmcnt(0)
-    auto step = [&](char *cur, char *ahead, int i) {
+    auto step = [&](char *cur, char *ahead, int i, auto stores) {
+        constexpr int n = 2 * kDma + (CONV ? decltype(stores)::value : 0);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(kWait);
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));  // vmcnt(n) lgkmcnt(0)
         __builtin_amdgcn_s_barrier();  // every wave's part of chunk i is in; chunk i - 1 is read
         __builtin_amdgcn_sched_barrier(0);
         dma(ahead, i + 3);
         __builtin_amdgcn_sched_barrier(0);
-        compute(cur);
+        compute(cur, i);
     };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
     dma(s0, 0);
     dma(s1, 1);
     dma(s2, 2);
-    for (int i = 0; i < nchunks; i += 4) {  // nchunks is a multiple of 4 (the launcher checks)
-        step(s0, s3, i);
-        step(s1, s0, i + 1);
-        step(s2, s1, i + 2);
-        step(s3, s2, i + 3);
+    // nchunks is a multiple of 4 (the launcher checks)
+    step(s0, s3, 0, S0{});
+    step(s1, s0, 1, S1{});
+    step(s2, s1, 2, S2{});
+    step(s3, s2, 3, S3{});
+    for (int i = 4; i < nchunks; i += 4) {
+        step(s0, s3, i, S3{});
+        step(s1, s0, i + 1, S3{});
+        step(s2, s1, i + 2, S3{});
+        step(s3, s2, i + 3, S3{});
     }
     __builtin_amdgcn_s_waitcnt(0);  // the loads past the last chunk have landed too
     __syncthreads();                // and every read of the chunk buffers is done
@@ -404,21 +439,33 @@ __global__ __launch_bounds__(512) void router_lds_kernel(const float *__restrict
                                                          const float *__restrict__ w, int ldw,
                                                          const double *__restrict__ bias, int E,
                                                          double *__restrict__ logits,
-                                                         const float *__restrict__ row_scale)
+                                                         const float *__restrict__ row_scale,
+                                                         uint16_t *__restrict__ xb, int ldb)
 {
     // four separate arrays, so that the compiler tracks the loads into each
     __shared__ __attribute__((aligned(16))) char s0[router_lds_buf<NE>()];
     __shared__ __attribute__((aligned(16))) char s1[router_lds_buf<NE>()];
     __shared__ __attribute__((aligned(16))) char s2[router_lds_buf<NE>()];
     __shared__ __attribute__((aligned(16))) char s3[router_lds_buf<NE>()];
-    router_lds_body<NE>(x, ldx, T, kp, w, ldw, bias, E, logits, row_scale, s0, s1, s2, s3);
+    // the first expert tile of each token tile writes the bf16 rows
+    if (xb != nullptr && blockIdx.y == 0)
+        router_lds_body<NE, true>(x, ldx, T, kp, w, ldw, bias, E, logits, row_scale, xb, ldb, s0, s1, s2, s3);
+    else
+        router_lds_body<NE, false>(x, ldx, T, kp, w, ldw, bias, E, logits, row_scale, nullptr, 0, s0, s1, s2, s3);
 }
 
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
-                         double *logits, hipStream_t s, const float *row_scale)
+                         double *logits, hipStream_t s, const float *row_scale, uint16_t *xb, int ldb)
 {
     if (T <= 0) return hipSuccess;
+    // xb (optional): the bf16 copy of the rows, written by the staged kernel
+    // as it reads them, else by the input conversion first
+    if (xb != nullptr && (ldx != d || d % 64 != 0 || ldb < d)) return hipErrorInvalidValue;
+    auto convert_first = [&]() -> hipError_t {
+        return xb ? launch_convert_inputs_f32(x, T, d, nullptr, 0, xb, ldb, s) : hipSuccess;
+    };
     if (T <= 256) {
+        if (hipError_t e = convert_first()) return e;
         // rows are zero-padded to a multiple of 64 values
         const int kp = (d + 63) / 64 * 64;
         dim3 grid((T * E + 3) / 4);
@@ -437,12 +484,16 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
         if (staged && E > 32 && tiles2 >= kRouterStagedWgs) {
             dim3 grid((T + 31) / 32, (E + 63) / 64);
             hipLaunchKernelGGL((router_lds_kernel<2>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
-                               row_scale);
+                               row_scale, xb, ldb);
+            return hipGetLastError();
         } else if (staged && tiles1 >= kRouterStagedWgs) {
             dim3 grid((T + 31) / 32, (E + 31) / 32);
             hipLaunchKernelGGL((router_lds_kernel<1>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
-                               row_scale);
-        } else if (E > 32 && tiles2 * 8 >= kRouterWaves) {
+                               row_scale, xb, ldb);
+            return hipGetLastError();
+        }
+        if (hipError_t e = convert_first()) return e;
+        if (E > 32 && tiles2 * 8 >= kRouterWaves) {
             dim3 grid((T + 31) / 32, (E + 63) / 64);
             if (tiles2 * 4 >= kRouterWaves)
                 hipLaunchKernelGGL((router_mfma_kernel<2, 4>), grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E,

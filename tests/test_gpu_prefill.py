@@ -251,6 +251,48 @@ def test_device_buffers_off_16_byte_alignment(ctx, path, T):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("T,E", [(4100, 64), (8200, 128), (1100, 8)])
+def test_fp32_rows_converted_by_the_router(ctx, T, E):
+    """fp32 device rows on the bf16 path, read in place by the router: at
+    4100 tokens x 64 experts and 8200 x 128 the staged router writes the
+    bf16 rows itself (one and two expert tiles per workgroup, a last token
+    tile part-filled); at 1100 x 8 the rows are converted first.  Two calls
+    with different rows (a row left unwritten would keep the first call's
+    values), each against the float64-input forward of the same values,
+    whose rows go through the separate conversion, and the oracle on a
+    sample."""
+    import torch
+    say(f"fp32 rows converted by the router, T={T} E={E}")
+    d = 256
+    spec = make_moe(gt.encode_rows, d=d, h=64, E=E, k=2, S=1, precision=FP4, seed=41, std=0.2, bias_std=0.05)
+    rng = np.random.default_rng(42)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        for call in range(2):
+            x = rng.uniform(-1, 1, (T, d)).astype(np.float32)
+            xa = torch.from_numpy(x).cuda()
+            ya = torch.full((T, d), float("nan"), device="cuda")
+            torch.cuda.synchronize()
+            m.forward_device(T, xa.data_ptr(), ya.data_ptr(), path=gt.PATH_BF16)
+            torch.cuda.synchronize()
+            assert m.last_path == gt.PATH_BF16
+            y = ya.cpu().numpy().astype(np.float64)
+            r = m.last_routing()
+            y64 = m.forward(x.astype(np.float64), path=gt.PATH_BF16)
+            r64 = m.last_routing()
+            assert np.array_equal(r.chosen, r64.chosen), call
+            e = float(np.max(np.abs(y - y64)) / np.max(np.abs(y64)))
+            say(f"[T={T} E={E} call {call}] max rel diff to the float64-input forward {e:.3e}")
+            assert e <= 1e-6, (call, e)
+            sample = np.sort(rng.choice(T, 16, replace=False))
+            sample[-1] = T - 1
+            ref = oracle.moe_forward_routed(spec, x[sample].astype(np.float64), r.chosen[sample], r.gates[sample],
+                                            threads=16)
+            assert rel_err(y[sample], ref.outputs) <= BF16_TOL
+    finally:
+        m.destroy()
+
+
 @pytest.mark.parametrize("d,hash_mid", [(128, False), (128, True), (96, False)])
 def test_bf16_stack_norm_done_by_the_combine(ctx, d, hash_mid):
     """A bf16 stack past the fused routing (T*k > 2048).  With d a multiple of
