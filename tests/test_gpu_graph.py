@@ -27,12 +27,15 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
 
 
-@pytest.mark.parametrize("T,path,S", [(16, gt.PATH_FP32, 1), (1, gt.PATH_FP32, 1), (64, gt.PATH_BF16, 1),
-                                      (16, gt.PATH_FP32, 0), (3, gt.PATH_FP32, 0)])
-def test_graph_forward_replays_equal_eager(ctx, T, path, S):
-    # S = 0 with top-2: the combine is folded into the down kernel
-    say(f"graph forward T={T} path={path} S={S}")
-    spec = make_moe(gt.encode_rows, d=256, h=512, E=8, k=2, S=S, precision=INT8, seed=21)
+@pytest.mark.parametrize("T,path,S,E", [(16, gt.PATH_FP32, 1, 8), (1, gt.PATH_FP32, 1, 8), (64, gt.PATH_BF16, 1, 8),
+                                        (16, gt.PATH_FP32, 0, 8), (3, gt.PATH_FP32, 0, 8),
+                                        (4100, gt.PATH_BF16, 1, 64)])
+def test_graph_forward_replays_equal_eager(ctx, T, path, S, E):
+    # S = 0 with top-2: the combine is folded into the down kernel; 4100
+    # tokens x 64 experts: the staged router writes the bf16 rows, the
+    # dispatch runs per chunk of tokens
+    say(f"graph forward T={T} path={path} S={S} E={E}")
+    spec = make_moe(gt.encode_rows, d=256, h=512, E=E, k=2, S=S, precision=INT8, seed=21)
     rng = np.random.default_rng(22)
     x0 = rng.standard_normal((T, 256))
     x1 = rng.standard_normal((T, 256))
@@ -71,9 +74,10 @@ def test_graph_forward_replays_equal_eager(ctx, T, path, S):
             assert np.array_equal(yg.cpu().numpy(), eager1)
     finally:
         m.destroy()
-    ref = oracle.moe_forward_routed(spec, x0, r0.chosen, r0.gates)
+    sample = np.arange(T) if T <= 256 else np.sort(rng.choice(T, 32, replace=False))
+    ref = oracle.moe_forward_routed(spec, x0[sample], r0.chosen[sample], r0.gates[sample])
     tol = 1e-4 if path == gt.PATH_FP32 else 2e-2
-    assert rel_err(eager0, ref.outputs) <= tol
+    assert rel_err(eager0[sample], ref.outputs) <= tol
 
 
 # E = 64 at T = 8: the routing splits each token's experts over several
