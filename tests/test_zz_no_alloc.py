@@ -51,9 +51,13 @@ def test_noalloc_matches_forward_device(ctx, path):
     # scratch area must hold as zeros)
     a_spec = make_moe(gt.encode_rows, d=1024, h=2048, E=16, k=2, S=0, precision=INT8, seed=70)
     b_spec = make_moe(gt.encode_rows, d=100, h=90, E=6, k=3, S=1, precision=FP4, seed=71, std=0.1, bias_std=0.02)
+    # many tokens over 64 experts: routed by the staged router (which, on the
+    # bf16 path, writes the bf16 rows into the area) and dispatched per chunk
+    c_spec = make_moe(gt.encode_rows, d=256, h=64, E=64, k=2, S=1, precision=FP4, seed=74, std=0.2, bias_std=0.05)
     rng = np.random.default_rng(72)
     a = gt.MixtureOfExperts.from_spec(ctx, a_spec)
     b = gt.MixtureOfExperts.from_spec(ctx, b_spec)
+    c = gt.MixtureOfExperts.from_spec(ctx, c_spec)
     tol = 1e-4 if path == gt.PATH_FP32 else 2e-2
     try:
         # two calls in a row on one layer, the second smaller, then the other
@@ -67,6 +71,17 @@ def test_noalloc_matches_forward_device(ctx, path):
             e = rel_err(yb, ref.outputs)
             say(f"[d={spec.vector_size} T={T}] equal to forward_device; max rel err vs oracle {e:.2e}")
             assert e <= tol
+        for T in (4100, 1500):
+            x = rng.standard_normal((T, 256))
+            ya, yb, r = both(c, x, path)
+            assert np.all(np.isfinite(ya))
+            assert np.array_equal(ya, yb), (256, T)
+            sample = np.sort(rng.choice(T, 24, replace=False))
+            ref = oracle.moe_forward_routed(c_spec, x[sample].astype(np.float32).astype(np.float64),
+                                            r.chosen[sample], r.gates[sample])
+            e = rel_err(yb[sample], ref.outputs)
+            say(f"[d=256 E=64 T={T}] equal to forward_device; max rel err vs oracle on a sample {e:.2e}")
+            assert e <= tol
         # the call keeps no routing state on the layer
         with pytest.raises(gt.GtmoeError) as info:
             b.last_routing()
@@ -74,6 +89,7 @@ def test_noalloc_matches_forward_device(ctx, path):
     finally:
         a.destroy()
         b.destroy()
+        c.destroy()
 
 
 def test_noalloc_refuses_sizes_beyond_the_scratch_area(ctx):
