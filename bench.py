@@ -27,8 +27,11 @@ kernel sources it was measured on are the ones built now (null otherwise).
 
 `detail.workloads` repeats the measurement, without CPU baseline, for the
 other configurations: the decode chunk of the same stack (T=64), one Int8
-decode layer (d=1024, 16 experts, top-2, h=2048) at T=1, 8 and 32 with four
-weight copies used round-robin (504 MB, beyond the 256 MB Infinity Cache),
+decode layer (d=1024, 16 experts, top-2, h=2048) at T=1, 8 and 32, each
+rotating over enough resident weight copies that the gate/up bytes of the
+experts a step can activate, times the copies, come to at least 768 MB (three
+times the 256 MB Infinity Cache; 77 copies at T=1, 10 at T=8 and T=32), so
+every step and every relaunch reads its weights from HBM,
 one FP4 prefill layer (d=1024, 64+1 experts, top-6, h=512, T=4096) and one
 Int8 prefill layer with Zipf(1.2) router-bias skew (d=2048, 128 experts,
 top-8, h=768, T=16384).  --workload picks another headline; --no-detail
@@ -59,12 +62,33 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 MFMA_FP32_PEAK_TFLOPS = 157.3
 
 WORKLOADS = {
-    "c2": dict(d=1024, E=16, k=2, h=2048, S=0, prec="int8", T=32, layers=1, copies=4, seed=0),
+    "c2": dict(d=1024, E=16, k=2, h=2048, S=0, prec="int8", T=32, layers=1, copies=None, seed=0),
     "c3": dict(d=1024, E=64, k=6, h=512, S=1, prec="fp4", T=4096, layers=1, copies=1, seed=3),
     "c4": dict(d=2048, E=128, k=8, h=768, S=0, prec="int8", T=16384, layers=1, copies=1, seed=4, zipf=0.6),
     "c5d": dict(d=2048, E=64, k=4, h=1024, S=1, prec="fp4", T=64, layers=24, copies=1, seed=5, sets=4),
     "c5p": dict(d=2048, E=64, k=4, h=1024, S=1, prec="fp4", T=8192, layers=24, copies=1, seed=5, sets=4),
 }
+
+
+# Single-layer decode workloads rotate over this many bytes of the experts a
+# step can activate (three times the 256 MB Infinity Cache), so that no step
+# and no relaunch finds its weights in the cache.
+CACHE_DEFEAT_BYTES = 768 << 20
+
+
+def weight_copies(c):
+    """Resident weight copies a workload rotates over: one for stacks (every
+    layer has its own copy) and prefill layers (every expert is read per
+    step, bytes far beyond the cache); for a decode layer enough copies that
+    the gate/up bytes of the min(T*k, E) + S experts a step can activate,
+    times the copies, reach CACHE_DEFEAT_BYTES."""
+    if c.get("copies"):
+        return c["copies"]
+    if c["layers"] > 1 or c["T"] * c["k"] > 8 * c["E"]:
+        return 1
+    active = min(c["T"] * c["k"], c["E"]) + c["S"]
+    per_copy = active * 2 * expert_bytes(c, c["h"], c["d"])
+    return max(4, -(-CACHE_DEFEAT_BYTES // per_copy))
 
 
 def weight_bytes_per_value(prec):
@@ -433,7 +457,16 @@ def summary(key, c, r):
             "kernel_achieved": roof["achieved"], "kernel_frac": roof["frac"], "traffic": roof["traffic"],
             "step_achieved": roof["step_achieved"], "step_frac": roof["step_frac"], "unit": roof["unit"],
             "kernel_ms_per_step": r["kernel_ms_per_step"],
-            "active_experts_layer0": int(np.count_nonzero(r["loads"][0]))}
+            "active_experts_layer0": int(np.count_nonzero(r["loads"][0])),
+            "weight_copies": c["copies"], "rotated_gateup_weight_bytes": rotated_bytes(c, r)}
+
+
+def rotated_bytes(c, r):
+    """Gate/up weight bytes of the active experts over every resident copy
+    or layer the steps and relaunch bursts rotate through (each layer's
+    realised routing)."""
+    per_layer = [(int(np.count_nonzero(l)) + c["S"]) * 2 * expert_bytes(c, c["h"], c["d"]) for l in r["loads"]]
+    return int(sum(per_layer) * c["copies"])
 
 
 def run_detail(gt, torch, ctx, stream, keys, shared, args):
@@ -444,6 +477,7 @@ def run_detail(gt, torch, ctx, stream, keys, shared, args):
         c = dict(WORKLOADS[key])
         if tokens:
             c["T"] = tokens
+        c["copies"] = weight_copies(c)
         reuse = shared.get(c.get("seed"), None) if key in ("c5d", "c5p") else None
         layers = reuse if reuse is not None else build_layers(gt, ctx, c, make_specs(gt, c))
         steps = 50 if c["layers"] > 1 or c["T"] * c["k"] > 8 * c["E"] else 200
@@ -494,6 +528,7 @@ def main():
     c = dict(WORKLOADS[key])
     if args.tokens:
         c["T"] = args.tokens
+    c["copies"] = weight_copies(c)
     if args.adapters:
         if c["layers"] != 1:
             print("--adapters measures a single layer (c2, c3 or c4)", file=sys.stderr)
@@ -549,7 +584,7 @@ def main():
         "config": {"workload": workload_name(key, c), "tokens": T, "d_model": d, "routed_experts": c["E"],
                    "shared_experts": c["S"], "top_k": c["k"], "expert_hidden": c["h"],
                    "expert_weights": f"{c['prec']} per-16 fp32 scales", "layers_per_step": c["layers"],
-                   "weight_copies": c["copies"],
+                   "weight_copies": c["copies"], "rotated_gateup_weight_bytes": rotated_bytes(c, r),
                    "path": "fp32 dequant-GEMV" if decode else "bf16 MFMA grouped GEMM",
                    "hip_graph": bool(args.graph), "step_timing": "median of per-step HIP event pairs"},
         "roofline": r["roofline"],
