@@ -525,6 +525,146 @@ __device__ __forceinline__ bool better(double s1, int e1, double s2, int e2)
     return s1 > s2 || (s1 == s2 && e1 < e2);
 }
 
+// sort.SliceStable(candidates, score descending) of mixtureofexperts.go:106,
+// step for step, for a row with NaN scores: Go's stable sort (package sort:
+// insertion sort of blocks of 20, then SymMerge of neighbouring runs of 20,
+// 40, 80, ... -- Kim & Kutzner, 2004), with less(i, j) = s[c[i]] > s[c[j]].
+// With scores that are totally ordered every stable sort gives the order the
+// arg-max rounds of topk_token find; NaN compares neither greater nor less
+// than anything, and the order the reference leaves then depends on exactly
+// which comparisons and swaps its sort makes, so those are repeated here.
+// One lane runs it over the candidate list c[0..n) in LDS (the scores s[] in
+// LDS too); SymMerge's two recursive calls work on disjoint ranges, so they
+// are kept on an explicit stack (stk, 3 ints per entry; the recursion is at
+// most ceil(log2 n) <= 8 deep for n <= 256, so 32 entries never fill).
+constexpr int kSortStack = 32;
+
+struct GoSort {
+    int *c;
+    const double *s;
+    __device__ bool less(int i, int j) const { return s[c[i]] > s[c[j]]; }
+    __device__ void swap(int i, int j) const
+    {
+        const int t = c[i];
+        c[i] = c[j];
+        c[j] = t;
+    }
+    __device__ void insertion(int a, int b) const
+    {
+        for (int i = a + 1; i < b; ++i)
+            for (int j = i; j > a && less(j, j - 1); --j) swap(j, j - 1);
+    }
+    __device__ void swap_range(int a, int b, int n) const
+    {
+        for (int i = 0; i < n; ++i) swap(a + i, b + i);
+    }
+    __device__ void rotate(int a, int m, int b) const
+    {
+        int i = m - a, j = b - m;
+        while (i != j) {
+            if (i > j) {
+                swap_range(m - i, m, j);
+                i -= j;
+            } else {
+                swap_range(m - i, m + j - i, i);
+                j -= i;
+            }
+        }
+        swap_range(m - i, m, i);
+    }
+    __device__ void sym_merge(int a0, int m0, int b0, int *stk) const
+    {
+        int sp = 0;
+        stk[0] = a0;
+        stk[1] = m0;
+        stk[2] = b0;
+        sp = 1;
+        while (sp > 0) {
+            --sp;
+            const int a = stk[3 * sp], m = stk[3 * sp + 1], b = stk[3 * sp + 2];
+            if (m - a == 1) {
+                int i = m, j = b;
+                while (i < j) {
+                    const int h = (int)((unsigned)(i + j) >> 1);
+                    if (less(h, a)) i = h + 1;
+                    else j = h;
+                }
+                for (int k = a; k < i - 1; ++k) swap(k, k + 1);
+                continue;
+            }
+            if (b - m == 1) {
+                int i = a, j = m;
+                while (i < j) {
+                    const int h = (int)((unsigned)(i + j) >> 1);
+                    if (!less(m, h)) i = h + 1;
+                    else j = h;
+                }
+                for (int k = m; k > i; --k) swap(k, k - 1);
+                continue;
+            }
+            const int mid = (int)((unsigned)(a + b) >> 1);
+            const int n = mid + m;
+            int start, r;
+            if (m > mid) {
+                start = n - b;
+                r = mid;
+            } else {
+                start = a;
+                r = m;
+            }
+            const int p = n - 1;
+            while (start < r) {
+                const int cc = (int)((unsigned)(start + r) >> 1);
+                if (!less(p - cc, cc)) start = cc + 1;
+                else r = cc;
+            }
+            const int end = n - start;
+            if (start < m && m < end) rotate(start, m, end);
+            if (mid < end && end < b && sp < kSortStack) {
+                stk[3 * sp] = mid;
+                stk[3 * sp + 1] = end;
+                stk[3 * sp + 2] = b;
+                ++sp;
+            }
+            if (a < start && start < mid && sp < kSortStack) {
+                stk[3 * sp] = a;
+                stk[3 * sp + 1] = start;
+                stk[3 * sp + 2] = mid;
+                ++sp;
+            }
+        }
+    }
+    __device__ void stable(int n, int *stk) const
+    {
+        int block = 20, a = 0, b = block;
+        while (b <= n) {
+            insertion(a, b);
+            a = b;
+            b += block;
+        }
+        insertion(a, n);
+        while (block < n) {
+            a = 0;
+            b = 2 * block;
+            while (b <= n) {
+                sym_merge(a, a + block, b, stk);
+                a = b;
+                b += 2 * block;
+            }
+            if (a + block < n) sym_merge(a, a + block, n, stk);
+            block *= 2;
+        }
+    }
+};
+
+// LDS a top-k wave needs for a row with NaN scores: the scores, the
+// candidate list and the merge stack.
+struct TopkScratch {
+    double *score;  // [kMaxExperts]
+    int *cand;      // [kMaxExperts]
+    int *stk;       // [3 * kSortStack]
+};
+
 // The balance biases of experts lane + 64 j (0 past E).
 template <int EPL>
 __device__ __forceinline__ void load_balance(const double *__restrict__ balance, int E, int lane, double (&bal)[EPL])
@@ -535,13 +675,13 @@ __device__ __forceinline__ void load_balance(const double *__restrict__ balance,
 
 // Top-k of one token by one wave (EPL experts per lane; bal[j] is the
 // balance bias of expert lane + 64 j, loaded ahead by the caller).  Writes
-// chosen, gates (float64 and fp32) for token t, and the chosen list to
-// `chosen_copy` when given.
+// chosen and gates (float64 and fp32) for token t; scr: LDS of the wave, used
+// only when a score is NaN.
 template <int EPL>
 __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row, int t, int E, int k,
                                            const double (&bal)[EPL], int lane, int32_t *__restrict__ chosen,
                                            double *__restrict__ gates, float *__restrict__ gates32,
-                                           int32_t *chosen_copy)
+                                           const TopkScratch &scr)
 {
     double a[EPL], sc[EPL];
     bool taken[EPL];
@@ -557,40 +697,60 @@ __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row,
             sc[j] = -INFINITY;
         }
     }
-    for (int r = 0; r < k; ++r) {
-        double bs = -INFINITY;
-        int be = 0x7fffffff;
+    bool nan = false;
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const int e = lane + 64 * j;
-            if (e < E && !taken[j] && better(sc[j], e, bs, be)) {
-                bs = sc[j];
-                be = e;
-            }
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            const double os = __shfl_xor(bs, off);
-            const int oe = __shfl_xor(be, off);
-            if (better(os, oe, bs, be)) {
-                bs = os;
-                be = oe;
-            }
-        }
-        if (be == 0x7fffffff) {
-            // Only NaN scores remain (NaN never compares better): take the
-            // lowest unchosen expert so the outputs stay in range.
-            int lowest = 0x7fffffff;
+    for (int j = 0; j < EPL; ++j) nan = nan || (lane + 64 * j < E && sc[j] != sc[j]);
+    if (__ballot(nan) == 0) {
+        // totally ordered scores: k rounds of wave arg-max in the order
+        // (score descending, expert ascending), the first k of any stable sort
+        for (int r = 0; r < k; ++r) {
+            double bs = -INFINITY;
+            int be = 0x7fffffff;
 #pragma unroll
             for (int j = 0; j < EPL; ++j) {
                 const int e = lane + 64 * j;
-                if (e < E && !taken[j] && e < lowest) lowest = e;
+                if (e < E && !taken[j] && better(sc[j], e, bs, be)) {
+                    bs = sc[j];
+                    be = e;
+                }
             }
-            for (int off = 32; off > 0; off >>= 1) lowest = min(lowest, __shfl_xor(lowest, off));
-            be = lowest;
-        }
+            for (int off = 32; off > 0; off >>= 1) {
+                const double os = __shfl_xor(bs, off);
+                const int oe = __shfl_xor(be, off);
+                if (better(os, oe, bs, be)) {
+                    bs = os;
+                    be = oe;
+                }
+            }
 #pragma unroll
-        for (int j = 0; j < EPL; ++j)
-            if (lane + 64 * j == be) taken[j] = true;
+            for (int j = 0; j < EPL; ++j)
+                if (lane + 64 * j == be) taken[j] = true;
+        }
+    } else {
+        // NaN scores: the reference's sort, repeated by lane 0
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            if (e < E) {
+                scr.score[e] = sc[j];
+                scr.cand[e] = e;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS stores are done
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) GoSort{scr.cand, scr.score}.stable(E, scr.stk);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int i = 0; i < k; ++i) {
+            const int ce = scr.cand[i];
+#pragma unroll
+            for (int j = 0; j < EPL; ++j)
+                if (lane + 64 * j == ce) taken[j] = true;
+        }
     }
     // chosen experts in ascending order, with their affinities
     int list_e[kMaxK];
@@ -623,7 +783,6 @@ __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row,
             chosen[(size_t)t * k + i] = list_e[i];
             gates[(size_t)t * k + i] = g;
             gates32[(size_t)t * k + i] = (float)g;
-            if (chosen_copy) chosen_copy[t * k + i] = list_e[i];
         }
     }
 }
@@ -633,12 +792,16 @@ __global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ lo
                                                    const double *__restrict__ balance, int32_t *__restrict__ chosen,
                                                    double *__restrict__ gates, float *__restrict__ gates32)
 {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ double score[4][kMaxExperts];
+    __shared__ int cand[4][kMaxExperts];
+    __shared__ int stk[4][3 * kSortStack];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
     if (t >= T) return;  // wave-uniform
     double bal[EPL];
     load_balance<EPL>(balance, E, lane, bal);
-    topk_token<EPL>(logits + (size_t)t * E, t, E, k, bal, lane, chosen, gates, gates32, nullptr);
+    topk_token<EPL>(logits + (size_t)t * E, t, E, k, bal, lane, chosen, gates, gates32,
+                    TopkScratch{score[wave], cand[wave], stk[wave]});
 }
 
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
@@ -660,7 +823,7 @@ hipError_t launch_topk(const double *logits, int T, int E, int k, const double *
 // Ids are checked non-negative by the host before launch.
 __device__ __forceinline__ void hash_token(const int64_t *__restrict__ ids, int t, int E, int k,
                                            int32_t *__restrict__ chosen, double *__restrict__ gates,
-                                           float *__restrict__ gates32, int32_t *chosen_copy)
+                                           float *__restrict__ gates32)
 {
     const unsigned long long first =
         ((unsigned long long)ids[t] * 2654435761ULL + 12345ULL) % (unsigned long long)E;
@@ -670,7 +833,6 @@ __device__ __forceinline__ void hash_token(const int64_t *__restrict__ ids, int 
         chosen[(size_t)t * k + i] = e;
         gates[(size_t)t * k + i] = g;
         gates32[(size_t)t * k + i] = (float)g;
-        if (chosen_copy) chosen_copy[t * k + i] = e;
     }
 }
 
@@ -679,7 +841,7 @@ __global__ void hash_route_kernel(const int64_t *__restrict__ ids, int T, int E,
 {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T) return;
-    hash_token(ids, t, E, k, chosen, gates, gates32, nullptr);
+    hash_token(ids, t, E, k, chosen, gates, gates32);
 }
 
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates, float *gates32,
@@ -1055,6 +1217,8 @@ template <typename InT, bool NORM, bool HASH, int EPL, int NX>
 __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
     __shared__ double lg[kMaxExperts];
+    __shared__ int cand[kMaxExperts];  // the top-k's candidate list and merge stack (NaN rows)
+    __shared__ int stk[3 * kSortStack];
     __shared__ __attribute__((aligned(16))) float comb[NX * 256];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int P = a.parts;
@@ -1213,21 +1377,33 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     __syncthreads();
     if (wave != 0) return;
     if (HASH) {
-        if (lane == 0) hash_token(a.ids, t, a.E, a.k, a.chosen, a.gates, a.gates32, nullptr);
+        if (lane == 0) hash_token(a.ids, t, a.E, a.k, a.chosen, a.gates, a.gates32);
         return;
     }
     if (P > 1) {
+        // The hand-off rests on the hardware, not on the memory model's
+        // release/acquire (which costs a write-back and an invalidation of
+        // the whole L2 of the XCD): agent-scope stores and loads are
+        // performed at the device's point of coherence, past the L2 of any
+        // one XCD (write-through), so a store that vmcnt(0) has seen
+        // acknowledged is visible to every later agent-scope load on the
+        // device.  The two asm statements keep the compiler's side in order:
+        // each clobbers memory, so no store moves below the wait, and no load
+        // of the logits moves above the count that tells this part it is the
+        // last.
         double *row = a.logits + (size_t)t * a.E;
         for (int e = eb + lane; e < ee; e += 64)
             __hip_atomic_store(row + e, lg[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): the stores are acknowledged
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stores are acknowledged
         int prior = 0;
         if (lane == 0) prior = __hip_atomic_fetch_add(a.part_cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__shfl(prior, 0) != P - 1) return;  // not the last part
+        asm volatile("" ::: "memory");
         for (int e = lane; e < a.E; e += 64) lg[e] = __hip_atomic_load(row + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (lane == 0) __hip_atomic_store(a.part_cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    topk_token<EPL>(lg, t, a.E, a.k, bal, lane, a.chosen, a.gates, a.gates32, nullptr);
+    // the logits in lg are read before a NaN row's scores overwrite them
+    topk_token<EPL>(lg, t, a.E, a.k, bal, lane, a.chosen, a.gates, a.gates32, TopkScratch{lg, cand, stk});
 }
 
 bool fused_route_fits(int T, int k, int kp) { return T >= 1 && T * k <= kFusedMaxTK && T <= 1024 && kp <= 4096; }

@@ -77,6 +77,7 @@ def lib():
         L.gtmoe_oracle_dot_row.restype = dbl
         L.gtmoe_oracle_layer_forward.argtypes = [C.POINTER(_Layer), C.c_int, P, C.c_int, P]
         L.gtmoe_oracle_route_from_logits.argtypes = [C.c_int, C.c_int, C.c_int, P, P, P, P, P]
+        L.gtmoe_oracle_go_stable_order.argtypes = [C.c_int, P, P]
         L.gtmoe_oracle_hash_route.argtypes = [C.c_int, C.c_int, C.c_int, P, P, P]
         L.gtmoe_oracle_hash_route.restype = C.c_int
         L.gtmoe_oracle_dispatch.argtypes = [C.c_int, C.c_int, C.c_int, P, P, P, P]
@@ -254,6 +255,16 @@ def route_from_logits(logits, k, balance_biases=None):
     lib().gtmoe_oracle_route_from_logits(T, E, k, logits.ctypes.data, bb.ctypes.data, chosen.ctypes.data,
                                          gates.ctypes.data, aff.ctypes.data)
     return SimpleNamespace(chosen=chosen, gates=gates, affinities=aff)
+
+
+def go_stable_order(scores):
+    """The candidate order sort.SliceStable(candidates, score descending)
+    leaves (mixtureofexperts.go:106), Go's block insertion sort and SymMerge
+    step for step; any order of NaN scores included."""
+    s = _c(scores, np.float64)
+    order = np.empty(len(s), np.int32)
+    lib().gtmoe_oracle_go_stable_order(len(s), s.ctypes.data, order.ctypes.data)
+    return order
 
 
 def hash_route(token_ids, experts, k):

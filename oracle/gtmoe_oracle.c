@@ -471,23 +471,141 @@ void gtmoe_oracle_expert_forward(const gtmoe_oracle_expert *e, int tokens, const
 /* Routing                                                                     */
 /* ------------------------------------------------------------------------- */
 
+/* sort.SliceStable(candidates, less) of mixtureofexperts.go:106, with
+ * less(i, j) = score(candidates[i]) > score(candidates[j]).  Go's stable sort
+ * (package sort, stable_func and its helpers insertionSort_func,
+ * symMerge_func, rotate_func, swapRange_func; Go 1.27 as go.mod pins it)
+ * insertion-sorts blocks of 20 and then merges neighbouring blocks of 20,
+ * 40, 80, ... with SymMerge (Kim & Kutzner, 2004).  For scores that are
+ * totally ordered every stable sort gives the same order; with NaN scores
+ * (no NaN compares greater, or less, than anything) the order is whatever
+ * this sequence of comparisons and swaps leaves, so it is followed step for
+ * step.  Candidate positions are swapped, as the reference's Swapper does. */
+typedef struct {
+    int *c;
+    const double *s;
+} cand_sort;
+
+static int cs_less(const cand_sort *d, int i, int j) { return d->s[d->c[i]] > d->s[d->c[j]]; }
+
+static void cs_swap(const cand_sort *d, int i, int j)
+{
+    int t = d->c[i];
+    d->c[i] = d->c[j];
+    d->c[j] = t;
+}
+
+static void cs_insertion(const cand_sort *d, int a, int b)
+{
+    for (int i = a + 1; i < b; i++)
+        for (int j = i; j > a && cs_less(d, j, j - 1); j--) cs_swap(d, j, j - 1);
+}
+
+static void cs_swap_range(const cand_sort *d, int a, int b, int n)
+{
+    for (int i = 0; i < n; i++) cs_swap(d, a + i, b + i);
+}
+
+/* the blocks [a, m) and [m, b) exchanged */
+static void cs_rotate(const cand_sort *d, int a, int m, int b)
+{
+    int i = m - a, j = b - m;
+    while (i != j) {
+        if (i > j) {
+            cs_swap_range(d, m - i, m, j);
+            i -= j;
+        } else {
+            cs_swap_range(d, m - i, m + j - i, i);
+            j -= i;
+        }
+    }
+    cs_swap_range(d, m - i, m, i);
+}
+
+/* merges the sorted runs [a, m) and [m, b) */
+static void cs_sym_merge(const cand_sort *d, int a, int m, int b)
+{
+    if (m - a == 1) { /* one element in front: binary search, then move it */
+        int i = m, j = b;
+        while (i < j) {
+            int h = (int)((unsigned)(i + j) >> 1);
+            if (cs_less(d, h, a)) i = h + 1;
+            else j = h;
+        }
+        for (int k = a; k < i - 1; k++) cs_swap(d, k, k + 1);
+        return;
+    }
+    if (b - m == 1) { /* one element behind */
+        int i = a, j = m;
+        while (i < j) {
+            int h = (int)((unsigned)(i + j) >> 1);
+            if (!cs_less(d, m, h)) i = h + 1;
+            else j = h;
+        }
+        for (int k = m; k > i; k--) cs_swap(d, k, k - 1);
+        return;
+    }
+    int mid = (int)((unsigned)(a + b) >> 1);
+    int n = mid + m, start, r;
+    if (m > mid) {
+        start = n - b;
+        r = mid;
+    } else {
+        start = a;
+        r = m;
+    }
+    int p = n - 1;
+    while (start < r) {
+        int c = (int)((unsigned)(start + r) >> 1);
+        if (!cs_less(d, p - c, c)) start = c + 1;
+        else r = c;
+    }
+    int end = n - start;
+    if (start < m && m < end) cs_rotate(d, start, m, end);
+    if (a < start && start < mid) cs_sym_merge(d, a, start, mid);
+    if (mid < end && end < b) cs_sym_merge(d, mid, end, b);
+}
+
+static void cs_stable(const cand_sort *d, int n)
+{
+    int block = 20, a = 0, b = block;
+    while (b <= n) {
+        cs_insertion(d, a, b);
+        a = b;
+        b += block;
+    }
+    cs_insertion(d, a, n);
+    while (block < n) {
+        a = 0;
+        b = 2 * block;
+        while (b <= n) {
+            cs_sym_merge(d, a, a + block, b);
+            a = b;
+            b += 2 * block;
+        }
+        if (a + block < n) cs_sym_merge(d, a, a + block, n);
+        block *= 2;
+    }
+}
+
+/* The candidate order sort.SliceStable leaves for scores s[0..n) (exported
+ * for the tests). */
+void gtmoe_oracle_go_stable_order(int n, const double *s, int *order)
+{
+    for (int e = 0; e < n; e++) order[e] = e;
+    cand_sort d = {order, s};
+    cs_stable(&d, n);
+}
+
 /* routedExperts (mixtureofexperts.go:98-112): stable sort by score descending
  * (ties keep the lower expert index first), take k, sort ascending. */
 static void routed_experts(int experts, int k, const double *affinities, const double *balance,
                            int32_t *chosen, int *scratch)
 {
-    for (int e = 0; e < experts; e++) scratch[e] = e;
-    /* stable insertion sort on score descending */
-    for (int i = 1; i < experts; i++) {
-        int cand = scratch[i];
-        double s = affinities[cand] + balance[cand];
-        int j = i - 1;
-        while (j >= 0 && affinities[scratch[j]] + balance[scratch[j]] < s) {
-            scratch[j + 1] = scratch[j];
-            j--;
-        }
-        scratch[j + 1] = cand;
-    }
+    double *score = (double *)malloc(sizeof(double) * (size_t)experts);
+    for (int e = 0; e < experts; e++) score[e] = affinities[e] + balance[e]; /* choiceScore */
+    gtmoe_oracle_go_stable_order(experts, score, scratch);
+    free(score);
     /* sort.Ints on the first k */
     for (int i = 0; i < k; i++) chosen[i] = scratch[i];
     for (int i = 1; i < k; i++) {

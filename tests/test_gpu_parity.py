@@ -95,6 +95,78 @@ def test_route_from_logits_bit_exact(ctx, E, k):
     assert np.array_equal(got.rows, d.rows)
 
 
+def same_gates(got, want):
+    """Bit-equal gates, NaN where the oracle's are NaN (a chosen expert with a
+    NaN affinity makes every gate of its token NaN)."""
+    nan = np.isnan(want)
+    return bool(np.array_equal(np.isnan(got), nan) and np.array_equal(got[~nan].view(np.int64),
+                                                                      want[~nan].view(np.int64)))
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (21, 3), (32, 4), (64, 6), (128, 8), (256, 8)])
+def test_route_from_logits_with_some_nan_scores(ctx, E, k):
+    """Rows with one to five NaN logits, and a NaN balance bias: no NaN
+    compares greater or less than anything, so the reference's choice is
+    whatever sort.SliceStable's block insertion sort and SymMerge leave
+    (mixtureofexperts.go:106).  The many-token top-k repeats that sort for
+    such rows: chosen experts, load and permutation bit-exact, gates bit-exact
+    or NaN where the oracle's are."""
+    say(f"route_from_logits with NaN scores E={E} k={k}")
+    rng = np.random.default_rng(500 + E + k)
+    T = 400
+    logits = rng.normal(0, 1.0, size=(T, E))
+    for t in range(T):
+        logits[t, rng.choice(E, size=1 + t % 5, replace=False)] = np.nan
+    logits[::7] = rng.normal(0, 1.0, size=logits[::7].shape)  # rows without NaN in between
+    bal = rng.normal(0, 0.05, size=E)
+    if E >= 32:
+        bal[E // 3] = np.nan
+    spec = make_moe(gt.encode_rows, d=4, h=4, E=E, k=k, seed=1)
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        m.balance_biases = bal
+        got = m.route_from_logits(logits)
+    finally:
+        m.destroy()
+    with np.errstate(invalid="ignore"):
+        want = oracle.route_from_logits(logits, k, bal)
+    assert np.array_equal(got.chosen, want.chosen)
+    assert same_gates(got.gates, want.gates)
+    d = oracle.dispatch(want.chosen, E)
+    assert np.array_equal(got.load, d.load)
+    assert np.array_equal(got.rows, d.rows)
+
+
+@pytest.mark.parametrize("E,k", [(32, 4), (64, 4), (96, 2), (256, 8)])
+def test_decode_routing_with_some_nan_scores(ctx, E, k):
+    """The decode routing kernel (one to eight workgroups per token) on rows
+    with NaN scores: a router of zero weights makes every logit its bias, three
+    biases are NaN and one balance bias is; chosen experts and gates against
+    the oracle's routing of the same float64 logits."""
+    say(f"decode routing with NaN scores E={E} k={k}")
+    d, T = 64, 6
+    rng = np.random.default_rng(600 + E)
+    spec = make_moe(gt.encode_rows, d=d, h=64, E=E, k=k, S=0, precision=INT8, seed=15)
+    spec.router.weights = gt.encode_rows(FLOAT32, np.zeros((E, d)))
+    bias = rng.normal(0, 1.0, size=E)
+    bias[rng.choice(E, size=3, replace=False)] = np.nan
+    spec.router.biases = bias
+    balance = rng.normal(0, 0.05, size=E)
+    balance[(E // 2 + 1) % E] = np.nan
+    x = rng.uniform(-1, 1, (T, d))
+    m = gt.MixtureOfExperts.from_spec(ctx, spec)
+    try:
+        m.balance_biases = balance
+        m.forward(x, path=gt.PATH_FP32)
+        r = m.last_routing()
+    finally:
+        m.destroy()
+    with np.errstate(invalid="ignore"):
+        want = oracle.route_from_logits(np.tile(bias, (T, 1)), k, balance)
+    assert np.array_equal(r.chosen, want.chosen)
+    assert same_gates(r.gates, want.gates)
+
+
 def test_hash_routing_matches_closed_form(ctx):
     say("hash routing forward")
     spec = make_moe(gt.encode_rows, d=32, h=48, E=8, k=3, S=1, seed=3, use_hash=True, precision=INT8)

@@ -265,6 +265,91 @@ def test_route_balance_bias_changes_choice_not_gates():
     assert r.gates[0].tolist() == [a[0] / (a[0] + a[3]), a[3] / (a[0] + a[3])]
 
 
+def insertion_order(s):
+    """One insertion sort over the whole row with the reference's less
+    function (score[i] > score[j]): what the restatement used before it
+    followed sort.SliceStable's blocks and merges."""
+    c = list(range(len(s)))
+    for i in range(1, len(c)):
+        j = i
+        while j > 0 and s[c[j]] > s[c[j - 1]]:
+            c[j], c[j - 1] = c[j - 1], c[j]
+            j -= 1
+    return c
+
+
+def test_go_stable_order_is_a_stable_sort_for_ordered_scores():
+    """sort.SliceStable (mixtureofexperts.go:106) on totally ordered scores,
+    many ties, across one block of 20, several, and ragged last blocks: the
+    order is numpy's stable argsort of -score."""
+    rng = np.random.default_rng(31)
+    for n in list(range(1, 45)) + [63, 64, 65, 100, 127, 128, 160, 255, 256]:
+        for _ in range(8):
+            s = rng.integers(0, 6, n).astype(np.float64) * rng.choice([1.0, -0.5])
+            s[rng.random(n) < 0.1] = -np.inf
+            assert oracle.go_stable_order(s).tolist() == np.argsort(-s, kind="stable").tolist(), (n, s)
+
+
+def test_go_stable_order_with_nan_inside_one_block():
+    """Up to 20 scores the sort is one insertion sort: a NaN compares neither
+    greater nor less than anything, so nothing moves past it; each run
+    between NaNs is stably sorted on its own and the NaNs stay in place."""
+    rng = np.random.default_rng(32)
+    for n in range(1, 21):
+        for _ in range(30):
+            s = rng.integers(0, 5, n).astype(np.float64)
+            s[rng.random(n) < 0.25] = np.nan
+            want, start = [], 0
+            for i in list(np.nonzero(np.isnan(s))[0]) + [n]:
+                seg = np.arange(start, i)
+                want += seg[np.argsort(-s[seg], kind="stable")].tolist()
+                if i < n:
+                    want.append(int(i))
+                start = i + 1
+            assert oracle.go_stable_order(s).tolist() == want
+    assert oracle.go_stable_order(np.full(77, np.nan)).tolist() == list(range(77))
+
+
+def test_go_stable_order_merge_traced_by_hand():
+    """22 scores: a sorted block 20, 19, ..., 1 and a block [NaN, 100].  The
+    insertion sort leaves the second block as it is (100 does not pass the
+    NaN); SymMerge(0, 20, 22) splits at mid 11, finds start 11 (NaN is never
+    less), recurses to (11, 20, 22), (16, 20, 22) and (19, 20, 22), whose
+    one-element case binary-searches [20, 22) for the first score not above
+    1 -- 100 is above it, so i = 22 -- and moves element 19 to the end:
+    0..18, then the NaN (20), then 100 (21), then element 19.  One insertion
+    sort over all 22 stops at the NaN too but moves nothing else."""
+    s = np.concatenate([np.arange(20, 0, -1).astype(np.float64), [np.nan, 100.0]])
+    assert oracle.go_stable_order(s).tolist() == list(range(19)) + [20, 21, 19]
+    assert insertion_order(s) == list(range(22))
+    # through the routing: k = 1 takes expert 0 (score 20), not expert 21
+    # (score 100)
+    logits = np.where(np.isnan(s), np.nan, 0.0)[None, :]
+    r = oracle.route_from_logits(logits, 1, np.where(np.isnan(s), 0.0, s))
+    assert r.chosen.tolist() == [[0]]
+
+
+def test_route_with_some_nan_scores_follows_the_reference_sort():
+    """Rows with a few NaN scores: the chosen experts are the first k of
+    sort.SliceStable's order, sorted ascending (mixtureofexperts.go:98-112),
+    and for rows past one block of 20 that order differs from one insertion
+    sort's in some rows (so the block and merge steps are what decide)."""
+    rng = np.random.default_rng(33)
+    differs = 0
+    for E, k in [(8, 2), (21, 3), (32, 4), (64, 6), (128, 8), (256, 8)]:
+        logits = rng.normal(0, 1.0, size=(40, E))
+        for t in range(40):
+            logits[t, rng.choice(E, size=1 + t % 5, replace=False)] = np.nan
+        bal = rng.normal(0, 0.1, size=E)
+        r = oracle.route_from_logits(logits, k, bal)
+        score = r.affinities + bal
+        for t in range(40):
+            order = oracle.go_stable_order(score[t]).tolist()
+            assert r.chosen[t].tolist() == sorted(order[:k])
+            differs += sorted(insertion_order(score[t])[:k]) != sorted(order[:k])
+    assert differs > 0
+
+
 def test_hash_route_closed_form():
     ids = np.array([0, 1, 2, 42, 9, 42, 2**40 + 7, 123456789], np.int64)
     for E, k in [(8, 2), (6, 3), (128, 8)]:
