@@ -24,6 +24,8 @@
 //
 // Gate/up fuse the SwiGLU epilogue (feedforward/gatedfeedforward.go:49-57):
 // hidden = act_g(gate + b_g) * act_u(up + b_u).  Down adds its bias.
+#include <algorithm>
+
 #include "common.h"
 
 namespace gtmoe {
@@ -310,10 +312,15 @@ __device__ __forceinline__ int slice_out_row(const GemvArgs &a, const SliceSrc &
     else return sl.s * a.T + sl.t0 + t;
 }
 
-// One slice of M <= 4*NQ tokens of group g against panel `panel`.
-template <int PREC, bool GATEUP, int NW, int NQ, int MODE>
-__device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, const SliceSrc &sl, int M, int panel)
+// One slice of M <= 4*NQ tokens of group g against panels panel0 ..
+// panel0 + PPW - 1: the NW waves are PPW sets of WPP = NW / PPW, set pi on
+// panel panel0 + pi, its waves splitting K; the sets share the staged tokens.
+template <int PREC, bool GATEUP, int NW, int NQ, int MODE, int PPW>
+__device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, const SliceSrc &sl, int M,
+                                          int panel0)
 {
+    static_assert(NW % PPW == 0, "whole sets of waves per panel");
+    constexpr int WPP = NW / PPW;
     constexpr int NT = 4 * NQ;
     constexpr int MATS = GATEUP ? 2 : 1;
     constexpr int CB = Chunk<PREC>::CB;
@@ -327,14 +334,17 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
     const int kp = a.nblocks * 16;
     const int ng8 = kp / 8;
 
-    // this wave's chunks of K; the first chunks' loads (and the epilogue's
-    // biases) are issued before the token rows are staged
+    // this wave's panel and chunks of K; the first chunks' loads (and the
+    // epilogue's biases) are issued before the token rows are staged
+    const int pi = wave / WPP, kw = wave - pi * WPP;
+    const int panel = panel0 + pi;
+    const bool in_matrix = panel * 64 < a.rows;  // the last workgroup's sets may lie past the rows
     const int nch = a.nblocks / CB;
-    const int c0 = wave * nch / NW, c1 = (wave + 1) * nch / NW;
+    const int c0 = kw * nch / WPP, c1 = (kw + 1) * nch / WPP;
     PanelSrc src[MATS];
     {
         const size_t wpanel = (size_t)panel * 64 * a.row_bytes;
-        const int wbytes = 64 * a.row_bytes;
+        const int wbytes = in_matrix ? 64 * a.row_bytes : 0;  // past the rows: every load reads zeros
         src[0].codes = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<char *>(reinterpret_cast<const char *>(a.w0)) + (size_t)g * a.w_group_stride + wpanel, 0, wbytes,
             kRawBufferWord3);
@@ -344,7 +354,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
                 wbytes, kRawBufferWord3);
         if constexpr (PREC != kFloat32) {
             const size_t spanel = (size_t)panel * 64 * a.nblocks;
-            const int sbytes = 64 * a.nblocks * 4;
+            const int sbytes = in_matrix ? 64 * a.nblocks * 4 : 0;
             src[0].scales = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float *>(a.s0) + (size_t)g * a.s_group_stride + spanel, 0, sbytes, kRawBufferWord3);
             if constexpr (GATEUP)
@@ -354,17 +364,19 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
     }
     const uint32_t vo = (uint32_t)lane * 16;
 
-    // The wave stages the slice's tokens for its own K range only (groups of
-    // 8 k-values [g0, g0 + gn)) as bf16 hi / lo, so no workgroup barrier is
-    // needed before the main loop.  Item i of a lane is token lane % NT
-    // (64 is a multiple of NT) at group g0 + (lane + 64 i) / NT: the lanes'
+    // The slice's tokens for this wave's K range (groups of 8 k-values
+    // [g0, g0 + gn)) are staged as bf16 hi / lo by the PPW waves that share
+    // the range: one wave (PPW = 1) needs no workgroup barrier before its
+    // main loop.  Item i of a lane is token lane % NT (64 is a multiple of
+    // NT) at group g0 + idx / NT, idx = lane + 64 (pi + PPW i): the lanes'
     // 16-byte LDS stores are contiguous.  The token loads are issued before
     // the weight prefetch, the conversion after it, so the wait for the
     // tokens overlaps the first weight chunks' latency.  Padding tokens
     // (t >= M) read past the input buffer and get zeros.
     const int g0 = c0 * CB * 2, gn = (c1 - c0) * CB * 2;
     const int items = NT * gn;
-    const int ipl = (items + 63) / 64;  // items per lane, <= NT
+    const int ipl = (items + 64 * PPW - 1) / (64 * PPW);  // items per lane
+    auto item = [&](int i) { return lane + 64 * (pi + PPW * i); };
     const int t = lane % NT;
     uint32_t rowoff = 0x80000000u;  // past the buffer: zeros
     if (t < M) rowoff = (uint32_t)slice_in_row<GATEUP, MODE>(a, sl, t) * (uint32_t)a.ld_in * 4u;
@@ -390,7 +402,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
 #pragma unroll
     for (int i = 0; i < kEarly; ++i) {
         if (i < ipl) {  // wave-uniform
-            const uint32_t off = token_off(lane + 64 * i);
+            const uint32_t off = token_off(item(i));
             xv[i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 0, 0));
             xv[i][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 16, 0));
         }
@@ -400,7 +412,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
     // in flight at the main loop's entry are the ring's alone, in ring order,
     // as on its back edge
     const int row = panel * 64 + lane;
-    const bool writer = wave < 4 && row < a.rows;
+    const bool writer = kw < 4 && row < a.rows;
     float bias[MATS];
 #pragma unroll
     for (int m = 0; m < MATS; ++m) bias[m] = writer ? (m == 0 ? a.b0 : a.b1)[(size_t)g * a.rows + row] : 0.f;
@@ -428,21 +440,25 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
     uint4 *xlo = xhi + (size_t)ng8 * NT;
 #pragma unroll
     for (int i = 0; i < kEarly; ++i) {
-        const int idx = lane + 64 * i;
+        const int idx = item(i);
         if (i < ipl && idx < items) stage(idx, xv[i][0], xv[i][1], xhi, xlo);
     }
     for (int i = kEarly; i < ipl; ++i) {
-        const int idx = lane + 64 * i;
+        const int idx = item(i);
         const uint32_t off = token_off(idx);
         const float4 v0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 0, 0));
         const float4 v1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xin, off, 16, 0));
         if (idx < items) stage(idx, v0, v1, xhi, xlo);
     }
-    // the wave reads back only what it wrote; LDS operations of a wave are
-    // performed in order, so a wait for its own stores is enough
+    // With one panel the wave reads back only what it wrote; LDS operations
+    // of a wave are performed in order, so a wait for its own stores is
+    // enough.  With several, every wave waits for its own stores and then
+    // for the other waves at a bare barrier (no wait for the weight loads in
+    // flight).  The fences keep the compiler from moving LDS accesses across.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
+    if constexpr (PPW == 1) __builtin_amdgcn_wave_barrier();
+    else __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     const Staged<NT> xs{xhi, xlo};
@@ -475,8 +491,9 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
     for (int j = 0; j + 1 < kDepth; ++j)
         if (ch + j < c1) compute_chunk<PREC, MATS, NQ>(r[j], xs, ch + j, tl, acc);
 
-    // sum the NW partial K ranges through LDS; wave v < 4 then finishes
-    // tokens 4q + v of every quad
+    // sum the partial K ranges of each panel through LDS; wave kw < 4 of the
+    // panel's set then finishes tokens 4q + v of every quad, v = kw, kw +
+    // WPP, ... < 4
     __syncthreads();  // all reads of the staged tokens are done
     float *red = reinterpret_cast<float *>(lds);
     auto slot = [&](int wv, int m, int q, int i) { return (((wv * MATS + m) * NQ + q) * 4 + i) * 64 + lane; };
@@ -488,16 +505,17 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
             for (int i = 0; i < 4; ++i) red[slot(wave, m, q, i)] = acc[m][q][i];
     __syncthreads();
     if (!writer) return;
+    for (int tq = kw; tq < 4; tq += WPP)
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-        const int t = 4 * q + wave;
+        const int t = 4 * q + tq;
         if (t >= M) continue;
         float v[MATS];
 #pragma unroll
         for (int m = 0; m < MATS; ++m) {
             float s = 0.f;
 #pragma unroll
-            for (int wv = 0; wv < NW; ++wv) s += red[slot(wv, m, q, wave)];
+            for (int wv = 0; wv < WPP; ++wv) s += red[slot(pi * WPP + wv, m, q, tq)];
             v[m] = s;
         }
         const size_t orow = (size_t)slice_out_row<MODE>(a, sl, t) * a.ld_out;
@@ -545,7 +563,7 @@ __device__ __forceinline__ void run_slice(const GemvArgs &a, char *lds, int g, c
 // blockIdx.x = panel of 64 output rows, blockIdx.y = token slice (the
 // dispatch wrote the slice count and a (group, first position, positions)
 // descriptor per slice; slices past the last exit).
-template <int PREC, bool GATEUP, int NW, bool SELF>
+template <int PREC, bool GATEUP, int NW, bool SELF, int PPW>
 __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -556,8 +574,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
         if (y >= nslices) return;    // workgroup-uniform
         const SliceSrc sl{kByPosition, dsc.y, nullptr, 0, 0};
         if (dsc.z <= 0) return;  // workgroup-uniform
-        if (dsc.z <= 4) run_slice<PREC, GATEUP, NW, 1, kByPosition>(a, lds, dsc.x, sl, dsc.z, blockIdx.x);
-        else run_slice<PREC, GATEUP, NW, 2, kByPosition>(a, lds, dsc.x, sl, dsc.z, blockIdx.x);
+        const int panel0 = blockIdx.x * PPW;
+        if (dsc.z <= 4) run_slice<PREC, GATEUP, NW, 1, kByPosition, PPW>(a, lds, dsc.x, sl, dsc.z, panel0);
+        else run_slice<PREC, GATEUP, NW, 2, kByPosition, PPW>(a, lds, dsc.x, sl, dsc.z, panel0);
         return;
     } else {
         const int nsh = a.S * a.shared_slices;
@@ -565,8 +584,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
             const int s = y / a.shared_slices;
             const SliceSrc sl{kShared, 0, nullptr, (y - s * a.shared_slices) * kGemvSlice, s};
             const int m = min(kGemvSlice, a.T - sl.t0);
-            if (m <= 4) run_slice<PREC, GATEUP, NW, 1, kShared>(a, lds, s, sl, m, blockIdx.x);
-            else run_slice<PREC, GATEUP, NW, 2, kShared>(a, lds, s, sl, m, blockIdx.x);
+            const int panel0 = blockIdx.x * PPW;
+            if (m <= 4) run_slice<PREC, GATEUP, NW, 1, kShared, PPW>(a, lds, s, sl, m, panel0);
+            else run_slice<PREC, GATEUP, NW, 2, kShared, PPW>(a, lds, s, sl, m, panel0);
             return;
         }
         // routed expert e: its entries in token order (the order of the
@@ -603,10 +623,10 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a)
         for (int first = par * kGemvSlice; first < c; first += 2 * kGemvSlice) {
             const SliceSrc sl{kByEntry, 0, list + first, 0, 0};
             const int m = min(kGemvSlice, c - first);
-            int g = a.S + e, panel = blockIdx.x;
-            asm volatile("" : "+s"(g), "+s"(panel));  // as for tid in run_slice
-            if (m <= 4) run_slice<PREC, GATEUP, NW, 1, kByEntry>(a, lds, g, sl, m, panel);
-            else run_slice<PREC, GATEUP, NW, 2, kByEntry>(a, lds, g, sl, m, panel);
+            int g = a.S + e, panel0 = blockIdx.x * PPW;
+            asm volatile("" : "+s"(g), "+s"(panel0));  // as for tid in run_slice
+            if (m <= 4) run_slice<PREC, GATEUP, NW, 1, kByEntry, PPW>(a, lds, g, sl, m, panel0);
+            else run_slice<PREC, GATEUP, NW, 2, kByEntry, PPW>(a, lds, g, sl, m, panel0);
             __syncthreads();  // the next pass re-stages the LDS
         }
     }
@@ -828,7 +848,7 @@ size_t gemv_lds_bytes(int nblocks, bool gateup, int nw)
     return staged > red ? staged : red;
 }
 
-template <int PREC, bool GATEUP, int NW>
+template <int PREC, bool GATEUP, int NW, int PPW = 1>
 hipError_t launch_nw(const GemvArgs &a0, int max_slices, hipStream_t s)
 {
     GemvArgs a = a0;
@@ -839,15 +859,16 @@ hipError_t launch_nw(const GemvArgs &a0, int max_slices, hipStream_t s)
         lds = (size_t)a.list_off + ((size_t)a.T * a.k + 1) * sizeof(int);
     }
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    const void *fn = a.self_dispatch ? reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW, true>)
-                                     : reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW, false>);
+    const void *fn = a.self_dispatch ? reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW, true, PPW>)
+                                     : reinterpret_cast<const void *>(&gemv_kernel<PREC, GATEUP, NW, false, PPW>);
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    const dim3 grid((a.rows + 63) / 64, max_slices);
-    if (a.self_dispatch) hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW, true>), grid, dim3(64 * NW), lds, s, a);
-    else hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW, false>), grid, dim3(64 * NW), lds, s, a);
+    const dim3 grid((a.rows + 64 * PPW - 1) / (64 * PPW), max_slices);
+    if (a.self_dispatch)
+        hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW, true, PPW>), grid, dim3(64 * NW), lds, s, a);
+    else hipLaunchKernelGGL((gemv_kernel<PREC, GATEUP, NW, false, PPW>), grid, dim3(64 * NW), lds, s, a);
     return hipGetLastError();
 }
 
@@ -870,6 +891,16 @@ hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
     // every busy workgroup at once; eight would leave some for a second round
     if (GATEUP && a.self_dispatch && a.nblocks / Chunk<PREC>::CB <= 32 && a.T * a.k >= a.E)
         return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
+    // Down over many workgroups: two panels per workgroup, which stages its
+    // tokens once for both (the staging was a fifth of the C5 decode down
+    // kernel: 30.0 -> 27.6 us per layer).  With fewer busy workgroups than
+    // two rounds' worth at the halved count the grid would no longer fill
+    // the GPU (a C2-sized layer: 14.5 -> 17.9 us), so those keep one panel.
+    if (!GATEUP && waves_for<PREC>(a) == 8 && a.rows >= 128) {
+        const long long busy = a.self_dispatch ? (long long)a.S * a.shared_slices + std::min(a.E, a.T * a.k)
+                                               : (long long)max_slices;
+        if ((long long)(a.rows / 128) * busy >= 1024) return launch_nw<PREC, GATEUP, 8, 2>(a, max_slices, s);
+    }
     if (waves_for<PREC>(a) == 8) return launch_nw<PREC, GATEUP, 8>(a, max_slices, s);
     return launch_nw<PREC, GATEUP, 4>(a, max_slices, s);
 }
