@@ -24,7 +24,10 @@
 // multiplyOrUseCPU does (gpu/device.go:722-739).  Weights are uploaded from
 // the layers' Rows snapshots on the first GPU forward of a mixture and again
 // whenever vectormath.WeightsVersion() has moved since (the reference's own
-// signal that weights changed, vectormath/weights.go:13-21).
+// signal that weights changed, vectormath/weights.go:13-21).  A mixture's
+// device copy lives until ReleaseGPU, CloseGPU, or the first GPU forward
+// after the mixture itself was garbage-collected (the table below holds it
+// by a weak pointer).
 //
 // This file has not been compiled: the environment it was written in has no
 // Go toolchain.  tests/test_go_binding.py checks its struct layouts against
@@ -38,6 +41,7 @@ import (
 	"os"
 	"sync"
 	"unsafe"
+	"weak"
 
 	"github.com/ebitengine/purego"
 	"github.com/javanhut/GoTransformers/activationfunction"
@@ -94,7 +98,7 @@ var (
 	libraryError error
 
 	gtmoeOpen             func(device int32, context *uintptr) int32
-	gtmoeClose            func(context uintptr) int32
+	gtmoeContextFree      func(context uintptr) int32
 	gtmoeLastError        func(context uintptr) string
 	gtmoeLayerCreate      func(context uintptr, desc *gtmoeLayerDesc, layer *uintptr) int32
 	gtmoeLayerDestroy     func(layer uintptr) int32
@@ -132,7 +136,7 @@ func loadLibrary() error {
 		}
 		functions := map[string]any{
 			"gtmoe_open":               &gtmoeOpen,
-			"gtmoe_close":              &gtmoeClose,
+			"gtmoe_context_free":       &gtmoeContextFree,
 			"gtmoe_last_error":         &gtmoeLastError,
 			"gtmoe_layer_create":       &gtmoeLayerCreate,
 			"gtmoe_layer_destroy":      &gtmoeLayerDestroy,
@@ -162,12 +166,43 @@ type gpuState struct {
 }
 
 // deviceLock serialises every call into libgtmoe, as gpu.Device's lock does
-// (gpu/device.go:40); a MixtureOfExperts itself has no lock.
+// (gpu/device.go:40); a MixtureOfExperts itself has no lock.  gpuStates is
+// keyed by weak pointers, so it keeps no mixture alive: the device layers of
+// mixtures that were collected are freed by the next GPU forward.
 var (
 	deviceLock    sync.Mutex
 	deviceContext uintptr
-	gpuStates     = map[*MixtureOfExperts]*gpuState{}
+	gpuStates     = map[weak.Pointer[MixtureOfExperts]]*gpuState{}
 )
+
+// releaseState frees one table entry's device layer (deviceLock held).
+func releaseState(key weak.Pointer[MixtureOfExperts]) {
+	if state := gpuStates[key]; state != nil {
+		if state.layer != 0 {
+			gtmoeLayerDestroy(state.layer)
+		}
+		delete(gpuStates, key)
+	}
+}
+
+// releaseCollected frees the device layers of mixtures the garbage
+// collector has taken (deviceLock held).
+func releaseCollected() {
+	for key := range gpuStates {
+		if key.Value() == nil {
+			releaseState(key)
+		}
+	}
+}
+
+// ReleaseGPU frees this mixture's device layer (its weights in HBM) now; a
+// later GPU forward uploads them again.  Mixtures that are simply dropped
+// have theirs freed by the next GPU forward of any mixture.
+func (mixture *MixtureOfExperts) ReleaseGPU() {
+	deviceLock.Lock()
+	defer deviceLock.Unlock()
+	releaseState(weak.Make(mixture))
+}
 
 // UseGPU opens GPU `device` for every MixtureOfExperts of the process
 // (gpu.Open's counterpart, gpu/device.go:90-130).  Without the library or
@@ -197,13 +232,10 @@ func CloseGPU() {
 	if deviceContext == 0 {
 		return
 	}
-	for mixture, state := range gpuStates {
-		if state.layer != 0 {
-			gtmoeLayerDestroy(state.layer)
-		}
-		delete(gpuStates, mixture)
+	for key := range gpuStates {
+		releaseState(key)
 	}
-	gtmoeClose(deviceContext)
+	gtmoeContextFree(deviceContext)
 	deviceContext = 0
 }
 
@@ -212,7 +244,7 @@ func CloseGPU() {
 func (mixture *MixtureOfExperts) LastGPUError() error {
 	deviceLock.Lock()
 	defer deviceLock.Unlock()
-	if state := gpuStates[mixture]; state != nil {
+	if state := gpuStates[weak.Make(mixture)]; state != nil {
 		return state.lastError
 	}
 	return nil
@@ -231,10 +263,12 @@ func (mixture *MixtureOfExperts) forwardOnGPU(inputs vectormath.Matrix, tokenIDs
 	if !eligible {
 		return vectormath.Matrix{}, false
 	}
-	state := gpuStates[mixture]
+	releaseCollected()
+	key := weak.Make(mixture)
+	state := gpuStates[key]
 	if state == nil {
 		state = &gpuState{}
-		gpuStates[mixture] = state
+		gpuStates[key] = state
 	}
 	fail := func(err error) (vectormath.Matrix, bool) {
 		state.lastError = err

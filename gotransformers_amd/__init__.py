@@ -28,7 +28,8 @@ ROLES = {("shared", "gate"): 1, ("shared", "up"): 2, ("shared", "down"): 3,
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOT_READY, ERR_OUT_OF_MEMORY = range(6)
 
 EXPORTED = [
-    "gtmoe_abi_version", "gtmoe_device_count", "gtmoe_open", "gtmoe_close", "gtmoe_last_error", "gtmoe_test_inject_failure",
+    "gtmoe_abi_version", "gtmoe_device_count", "gtmoe_open", "gtmoe_close", "gtmoe_context_free", "gtmoe_last_error",
+    "gtmoe_test_inject_failure", "gtmoe_test_device_allocations",
     "gtmoe_encode_rows", "gtmoe_layer_create", "gtmoe_layer_destroy", "gtmoe_upload_rows",
     "gtmoe_set_balance_biases", "gtmoe_get_balance_biases", "gtmoe_set_norm_weights", "gtmoe_forward",
     "gtmoe_forward_device", "gtmoe_forward_device_noalloc", "gtmoe_last_routing", "gtmoe_last_expert_load", "gtmoe_update_balance",
@@ -85,8 +86,10 @@ def library():
         "gtmoe_device_count": ([P], i32),
         "gtmoe_open": ([i32, P], i32),
         "gtmoe_close": ([P], i32),
+        "gtmoe_context_free": ([P], i32),
         "gtmoe_last_error": ([P], C.c_char_p),
         "gtmoe_test_inject_failure": ([C.c_char_p, i32], i32),
+        "gtmoe_test_device_allocations": ([P, P], i32),
         "gtmoe_encode_rows": ([i32, i32, i32, P, P, P], i32),
         "gtmoe_layer_create": ([P, C.POINTER(LayerDesc), P], i32),
         "gtmoe_layer_destroy": ([P], i32),
@@ -158,6 +161,14 @@ def inject_failure(entry_point, status):
     _check(library().gtmoe_test_inject_failure(entry_point.encode(), status))
 
 
+def device_allocations():
+    """(allocations, frees): the device allocations and frees the library has
+    made since it was loaded (a test hook)."""
+    a, f = C.c_int64(), C.c_int64()
+    _check(library().gtmoe_test_device_allocations(C.byref(a), C.byref(f)))
+    return a.value, f.value
+
+
 def device_count():
     n = C.c_int32(0)
     _check(library().gtmoe_device_count(C.byref(n)))
@@ -213,8 +224,10 @@ class Context:
         self.device = device
 
     def close(self):
+        """gtmoe_context_free: closes the context and gives up this handle
+        (layers made on it answer "the context is closed" until destroyed)."""
         if self.handle:
-            library().gtmoe_close(self.handle)
+            library().gtmoe_context_free(self.handle)
             self.handle = None
 
     def __enter__(self):

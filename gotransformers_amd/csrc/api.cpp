@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <functional>
 #include <initializer_list>
@@ -37,6 +38,23 @@ thread_local std::string g_open_error;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Every device allocation and free the library makes goes through these two,
+// which count them for gtmoe_test_device_allocations.
+std::atomic<long long> g_device_allocations{0}, g_device_frees{0};
+
+template <class T>
+hipError_t dev_malloc(T **p, size_t bytes)
+{
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(reinterpret_cast<void **>(p), bytes);
+}
+
+hipError_t dev_free(void *p)
+{
+    g_device_frees.fetch_add(1, std::memory_order_relaxed);
+    return hipFree(p);
+}
+
 }  // namespace
 
 struct TimingRecord {
@@ -56,6 +74,9 @@ struct gtmoe_context {
     std::vector<hipEvent_t> spare_events;
     std::map<std::string, std::pair<double, int>> totals;
     bool closed = false;      // gtmoe_close ran: the handle stays readable, every call answers an error
+    // references: the caller's handle (until gtmoe_context_free), every layer
+    // and every recorded graph; the last one to go frees the context
+    int refs = 1;
     void *scratch = nullptr;  // device address of the no-allocation forward's scratch area on this device
     std::string scratch_error;
 };
@@ -92,6 +113,17 @@ hipEvent_t take_event(gtmoe_context *ctx)
     hipEvent_t e = nullptr;
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
+}
+
+// Drops one reference to ctx (the caller holds no lock on it); the last frees it.
+void release_context(gtmoe_context *ctx)
+{
+    bool last;
+    {
+        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+        last = --ctx->refs == 0;
+    }
+    if (last) delete ctx;
 }
 
 // Launch one kernel through `fn`, bracketed by events when timing is on.
@@ -255,6 +287,10 @@ struct gtmoe_layer {
     int last_T = -1;
     int last_path = GTMOE_PATH_FP32;
     hipStream_t last_stream = nullptr;
+    // kernels of a device-API call (forward, stack, graph replay, relaunch)
+    // were enqueued on a caller's stream and may still run: a host-API call
+    // waits for them before it touches the workspace or the weights
+    bool device_work_pending = false;
     std::vector<int32_t> last_load;
     bool load_on_host = false;
     // the decode path's expert kernels found their own tokens: the dispatch
@@ -296,29 +332,29 @@ int32_t alloc_matrix(gtmoe_context *ctx, DeviceMatrix &m, int precision, int row
     m.row_bytes = precision == kInt8 ? m.kp : precision == kFP4 ? m.kp / 2 : m.kp * 4;
     m.groups = groups;
     const size_t vb = (size_t)groups * m.group_value_bytes();
-    HIP_TRY(ctx, hipMalloc(&m.values, vb));
+    HIP_TRY(ctx, dev_malloc(&m.values, vb));
     HIP_TRY(ctx, hipMemset(m.values, 0, vb));
     if (precision != kFloat32) {
         const size_t sb = (size_t)groups * m.group_scales() * sizeof(float);
-        HIP_TRY(ctx, hipMalloc(&m.scales, sb));
+        HIP_TRY(ctx, dev_malloc(&m.scales, sb));
         HIP_TRY(ctx, hipMemset(m.scales, 0, sb));
     } else {
         const size_t hb = (size_t)groups * m.group_bf16_bytes();
-        HIP_TRY(ctx, hipMalloc(&m.bf16, hb));
+        HIP_TRY(ctx, dev_malloc(&m.bf16, hb));
         HIP_TRY(ctx, hipMemset(m.bf16, 0, hb));
     }
     const size_t bb = (size_t)groups * rows * sizeof(float);
-    HIP_TRY(ctx, hipMalloc(&m.biases, bb));
+    HIP_TRY(ctx, dev_malloc(&m.biases, bb));
     HIP_TRY(ctx, hipMemset(m.biases, 0, bb));
     return GTMOE_OK;
 }
 
 void free_matrix(DeviceMatrix &m)
 {
-    if (m.values) (void)hipFree(m.values);
-    if (m.scales) (void)hipFree(m.scales);
-    if (m.biases) (void)hipFree(m.biases);
-    if (m.bf16) (void)hipFree(m.bf16);
+    if (m.values) (void)dev_free(m.values);
+    if (m.scales) (void)dev_free(m.scales);
+    if (m.biases) (void)dev_free(m.biases);
+    if (m.bf16) (void)dev_free(m.bf16);
     m.values = nullptr;
     m.scales = nullptr;
     m.biases = nullptr;
@@ -431,13 +467,13 @@ int32_t ensure_workspace(gtmoe_layer *L, int T)
     int cap = T < 64 ? 64 : T;
     if (L->ws.base) {
         HIP_TRY(ctx, hipDeviceSynchronize());
-        (void)hipFree(L->ws.base);
+        (void)dev_free(L->ws.base);
         L->ws = Workspace{};
     }
     Workspace w{};
     const size_t total = layout_workspace(L, cap, true, nullptr, w);
     void *base = nullptr;
-    HIP_TRY(ctx, hipMalloc(&base, total));
+    HIP_TRY(ctx, dev_malloc(&base, total));
     // zero once: padding columns of the activation buffers are never written.
     // hipMemset runs on the null stream, which does not order against the
     // non-blocking streams the forward runs on: wait for it here.
@@ -750,9 +786,22 @@ void mark_forward(gtmoe_layer *L, int T, int path, hipStream_t s)
     L->last_T = T;
     L->last_path = path;
     L->last_stream = s;
+    L->device_work_pending = s != L->ctx->stream;
     L->load_on_host = false;
     L->dispatch_pending = T > 0 && L->skipped_dispatch;
     L->adapter_T = -1;  // set again by the adapter path's forward
+}
+
+// Before a host-API call enqueues work on the context's stream, which does
+// not synchronise with a caller's streams: wait for any device-API work on
+// this layer (its kernels use the same workspace, routing state and weights).
+// The device is synchronised as a whole: the caller's stream may be gone.
+int32_t settle_device_work(gtmoe_layer *L)
+{
+    if (!L->device_work_pending) return GTMOE_OK;
+    HIP_TRY(L->ctx, hipDeviceSynchronize());
+    L->device_work_pending = false;
+    return GTMOE_OK;
 }
 
 // Build the dispatch tables of the last forward if its kernels skipped them
@@ -923,13 +972,13 @@ namespace {
 void free_adapter(AdapterSet &a)
 {
     for (void *p : {(void *)a.A, (void *)a.B, (void *)a.scale, (void *)a.dA, (void *)a.dB})
-        if (p) (void)hipFree(p);
+        if (p) (void)dev_free(p);
     a = AdapterSet{};
 }
 
 void free_train_workspace(TrainWorkspace &tw)
 {
-    for (void *p : tw.blocks) (void)hipFree(p);
+    for (void *p : tw.blocks) (void)dev_free(p);
     tw = TrainWorkspace{};
 }
 
@@ -969,11 +1018,11 @@ int32_t alloc_adapter(gtmoe_context *ctx, AdapterSet &a, int G, int width, int k
     a.rows = rows;
     a.R = std::min(rank, std::min(width, rows));
     const size_t na = (size_t)G * a.R * kin, nb = (size_t)G * rows * a.R;
-    HIP_TRY(ctx, hipMalloc(&a.A, na * sizeof(float)));
-    HIP_TRY(ctx, hipMalloc(&a.B, nb * sizeof(float)));
-    HIP_TRY(ctx, hipMalloc(&a.scale, G * sizeof(float)));
-    HIP_TRY(ctx, hipMalloc(&a.dA, na * sizeof(double)));
-    HIP_TRY(ctx, hipMalloc(&a.dB, nb * sizeof(double)));
+    HIP_TRY(ctx, dev_malloc(&a.A, na * sizeof(float)));
+    HIP_TRY(ctx, dev_malloc(&a.B, nb * sizeof(float)));
+    HIP_TRY(ctx, dev_malloc(&a.scale, G * sizeof(float)));
+    HIP_TRY(ctx, dev_malloc(&a.dA, na * sizeof(double)));
+    HIP_TRY(ctx, dev_malloc(&a.dB, nb * sizeof(double)));
     std::vector<float> A(na, 0.f);
     const double limit = 1.0 / std::sqrt((double)width);
     for (int g = 0; g < G; ++g)
@@ -1032,7 +1081,7 @@ int32_t ensure_train_workspace(gtmoe_layer *L, int T)
     const size_t R = std::max({L->ad_gate.R, L->ad_up.R, L->ad_down.R, L->ad_router.R, 1});
     auto get = [&](auto *&ptr, size_t count) -> int32_t {
         void *p = nullptr;
-        HIP_TRY(ctx, hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(*ptr)));
+        HIP_TRY(ctx, dev_malloc(&p, std::max<size_t>(count, 1) * sizeof(*ptr)));
         tw.blocks.push_back(p);
         ptr = static_cast<std::remove_reference_t<decltype(ptr)>>(p);
         return GTMOE_OK;
@@ -1384,11 +1433,9 @@ int32_t gtmoe_open(int32_t device, gtmoe_context **out)
     return GTMOE_OK;
 }
 
-int32_t gtmoe_close(gtmoe_context *ctx)
+static void close_locked(gtmoe_context *ctx)
 {
-    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    if (ctx->closed) return GTMOE_OK;  // closing twice does nothing (gpu/gpu_test.go:145-154)
+    if (ctx->closed) return;  // closing twice does nothing (gpu/gpu_test.go:145-154)
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
     for (auto &r : ctx->pending) {
@@ -1400,15 +1447,42 @@ int32_t gtmoe_close(gtmoe_context *ctx)
     ctx->spare_events.clear();
     (void)hipStreamDestroy(ctx->stream);
     ctx->stream = nullptr;
+    ctx->totals.clear();
     // The handle is not freed: a closed context keeps answering, as a closed
-    // gpu.Device does (gpu/device.go:729-731), with an error instead of work.
+    // gpu.Device does (gpu/device.go:729-731), with an error instead of work,
+    // until gtmoe_context_free lets it go.
     ctx->closed = true;
+}
+
+int32_t gtmoe_close(gtmoe_context *ctx)
+{
+    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    close_locked(ctx);
+    return GTMOE_OK;
+}
+
+int32_t gtmoe_context_free(gtmoe_context *ctx)
+{
+    if (!ctx) return GTMOE_ERR_INVALID_ARGUMENT;
+    {
+        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+        close_locked(ctx);
+    }
+    release_context(ctx);  // the handle's reference
     return GTMOE_OK;
 }
 
 const char *gtmoe_last_error(const gtmoe_context *ctx)
 {
     return ctx ? ctx->error.c_str() : g_open_error.c_str();
+}
+
+int32_t gtmoe_test_device_allocations(int64_t *allocations, int64_t *frees)
+{
+    if (allocations) *allocations = g_device_allocations.load(std::memory_order_relaxed);
+    if (frees) *frees = g_device_frees.load(std::memory_order_relaxed);
+    return GTMOE_OK;
 }
 
 int32_t gtmoe_test_inject_failure(const char *entry_point, int32_t status)
@@ -1452,6 +1526,7 @@ int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtm
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     gtmoe_layer *L = new gtmoe_layer;
     L->ctx = ctx;
+    ++ctx->refs;  // dropped by gtmoe_layer_destroy
     L->desc = D;
     L->d = D.vector_size;
     L->h = D.expert_hidden_size;
@@ -1469,13 +1544,13 @@ int32_t gtmoe_layer_create(gtmoe_context *ctx, const gtmoe_layer_desc *desc, gtm
     if (rc == GTMOE_OK) rc = alloc_matrix(ctx, L->down, D.precision, L->d, L->h, L->G);
     if (rc == GTMOE_OK) {
         const size_t rw = (size_t)L->E * L->dp * sizeof(float);
-        if (hipMalloc(&L->router_w, rw) != hipSuccess || hipMemset(L->router_w, 0, rw) != hipSuccess ||
-            hipMalloc(&L->router_b, sizeof(double) * L->E) != hipSuccess ||
+        if (dev_malloc(&L->router_w, rw) != hipSuccess || hipMemset(L->router_w, 0, rw) != hipSuccess ||
+            dev_malloc(&L->router_b, sizeof(double) * L->E) != hipSuccess ||
             hipMemset(L->router_b, 0, sizeof(double) * L->E) != hipSuccess ||
-            hipMalloc(&L->balance, sizeof(double) * L->E) != hipSuccess ||
+            dev_malloc(&L->balance, sizeof(double) * L->E) != hipSuccess ||
             hipMemset(L->balance, 0, sizeof(double) * L->E) != hipSuccess ||
-            hipMalloc(&L->norm_w, sizeof(float) * L->d) != hipSuccess ||
-            hipMalloc(&L->router_wn, rw) != hipSuccess || hipMemset(L->router_wn, 0, rw) != hipSuccess)
+            dev_malloc(&L->norm_w, sizeof(float) * L->d) != hipSuccess ||
+            dev_malloc(&L->router_wn, rw) != hipSuccess || hipMemset(L->router_wn, 0, rw) != hipSuccess)
             rc = fail(ctx, GTMOE_ERR_OUT_OF_MEMORY, "cannot allocate the router");
     }
     // the zeroing memsets above run on the null stream (see ensure_workspace)
@@ -1492,23 +1567,23 @@ int32_t gtmoe_layer_destroy(gtmoe_layer *L)
 {
     if (!L) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    if (L->live_graphs > 0)
-        return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "the layer is part of %d recorded graph(s); destroy them first",
-                    L->live_graphs);
-    (void)hipSetDevice(ctx->device);
-    (void)hipDeviceSynchronize();
-    free_adapters(L);
-    free_matrix(L->gate);
-    free_matrix(L->up);
-    free_matrix(L->down);
-    if (L->router_w) (void)hipFree(L->router_w);
-    if (L->router_b) (void)hipFree(L->router_b);
-    if (L->balance) (void)hipFree(L->balance);
-    if (L->norm_w) (void)hipFree(L->norm_w);
-    if (L->router_wn) (void)hipFree(L->router_wn);
-    if (L->ws.base) (void)hipFree(L->ws.base);
-    delete L;
+    {
+        std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+        if (L->live_graphs > 0)
+            return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT,
+                        "the layer is part of %d recorded graph(s); destroy them first", L->live_graphs);
+        (void)hipSetDevice(ctx->device);
+        (void)hipDeviceSynchronize();
+        free_adapters(L);
+        free_matrix(L->gate);
+        free_matrix(L->up);
+        free_matrix(L->down);
+        for (void *p : {(void *)L->router_w, (void *)L->router_b, (void *)L->balance, (void *)L->norm_w,
+                        (void *)L->router_wn, L->ws.base})
+            if (p) (void)dev_free(p);
+        delete L;
+    }
+    release_context(ctx);  // the layer's reference
     return GTMOE_OK;
 }
 
@@ -1520,6 +1595,10 @@ int32_t gtmoe_upload_rows(gtmoe_layer *L, int32_t role, int32_t index, const gtm
     if (!biases) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "biases are null");
     if (role < GTMOE_ROLE_ROUTER || role > GTMOE_ROLE_ROUTED_DOWN)
         return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "unknown role %d", role);
+    {
+        const int32_t rc0 = settle_device_work(L);  // a forward may still read the matrix
+        if (rc0 != GTMOE_OK) return rc0;
+    }
 
     if (role == GTMOE_ROLE_ROUTER) {
         int32_t rc = check_rows(ctx, rows, L->E, L->d);
@@ -1584,6 +1663,8 @@ int32_t gtmoe_set_balance_biases(gtmoe_layer *L, const double *biases)
     if (!L || !biases) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
     ENTER(ctx);
+    int32_t rc = settle_device_work(L);
+    if (rc != GTMOE_OK) return rc;
     L->balance_host.assign(biases, biases + L->E);
     HIP_TRY(ctx, hipMemcpy(L->balance, biases, sizeof(double) * L->E, hipMemcpyHostToDevice));
     return GTMOE_OK;
@@ -1601,6 +1682,8 @@ int32_t gtmoe_set_norm_weights(gtmoe_layer *L, const double *weights)
     if (!L || !weights) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
     ENTER(ctx);
+    int32_t rc = settle_device_work(L);
+    if (rc != GTMOE_OK) return rc;
     std::vector<float> w(weights, weights + L->d);
     HIP_TRY(ctx, hipMemcpy(L->norm_w, w.data(), sizeof(float) * L->d, hipMemcpyHostToDevice));
     L->norm_host.swap(w);
@@ -1630,7 +1713,8 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     const int path = choose_path(L, T, flags);
     if (path == GTMOE_PATH_FP32 && (L->dp > kMaxGemvK || L->hp > kMaxGemvK))
         return fail(ctx, GTMOE_ERR_UNSUPPORTED, "the fp32 path takes vector and hidden sizes up to %d", kMaxGemvK);
-    rc = ensure_workspace(L, T);
+    rc = settle_device_work(L);
+    if (rc == GTMOE_OK) rc = ensure_workspace(L, T);
     if (rc != GTMOE_OK) return rc;
     hipStream_t s = ctx->stream;
     if (T == 0) {
@@ -1853,7 +1937,8 @@ int32_t gtmoe_route_from_logits(gtmoe_layer *L, int32_t tokens, const double *lo
     ENTER(ctx);
     const int T = tokens;
     if (T < 0 || (T > 0 && !logits)) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "bad logits");
-    int32_t rc = ensure_workspace(L, T);
+    int32_t rc = settle_device_work(L);
+    if (rc == GTMOE_OK) rc = ensure_workspace(L, T);
     if (rc != GTMOE_OK) return rc;
     hipStream_t s = ctx->stream;
     Workspace &w = L->ws;
@@ -1990,6 +2075,10 @@ int32_t gtmoe_stack_forward(gtmoe_layer *const *layers, int32_t n_layers, int32_
                 return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "token ID %lld at row %d is negative",
                             (long long)token_ids[t], t);
     }
+    for (int l = 0; l < n_layers; ++l) {
+        rc = settle_device_work(layers[l]);
+        if (rc != GTMOE_OK) return rc;
+    }
     gtmoe_layer *L0 = layers[0];
     rc = ensure_workspace(L0, T);
     if (rc != GTMOE_OK) return rc;
@@ -2058,6 +2147,7 @@ int32_t gtmoe_graph_capture_forward(gtmoe_layer *L, int32_t tokens, const float 
         return rc;
     }
     g->skipped = {(char)L->skipped_dispatch};
+    ++ctx->refs;  // dropped by gtmoe_graph_destroy
     *graph = g;
     return GTMOE_OK;
 }
@@ -2096,6 +2186,7 @@ int32_t gtmoe_graph_capture_stack(gtmoe_layer *const *layers, int32_t n_layers, 
         return rc;
     }
     for (int l = 0; l < n_layers; ++l) g->skipped.push_back((char)layers[l]->skipped_dispatch);
+    ++ctx->refs;  // dropped by gtmoe_graph_destroy
     *graph = g;
     return GTMOE_OK;
 }
@@ -2123,6 +2214,7 @@ int32_t gtmoe_graph_destroy(gtmoe_graph *g)
         (void)hipSetDevice(ctx->device);
         free_graph(g);
     }
+    release_context(ctx);
     return GTMOE_OK;
 }
 
@@ -2193,6 +2285,7 @@ int32_t gtmoe_relaunch(gtmoe_layer *L, int32_t kernel, void *stream)
     if (L->last_T <= 0 || !L->relaunch_ready)
         return fail(ctx, GTMOE_ERR_NOT_READY, "no forward with tokens to launch again");
     hipStream_t s = (hipStream_t)stream;
+    L->device_work_pending = true;
     const bool gateup = kernel == GTMOE_KERNEL_GATEUP;
     if (L->last_path == GTMOE_PATH_FP32) {
         const GemvArgs &a = L->last_gemv[gateup ? 0 : 1];
@@ -2221,6 +2314,10 @@ int32_t gtmoe_layer_load_weights(gtmoe_layer *L, gtmoe_weights_file *f, const ch
     gtmoe_context *ctx = L->ctx;
     ENTER(ctx);
     if (!f || !name) return fail(ctx, GTMOE_ERR_INVALID_ARGUMENT, "weights file or layer name is null");
+    {
+        const int32_t rc0 = settle_device_work(L);
+        if (rc0 != GTMOE_OK) return rc0;
+    }
 
     // MixtureOfExperts.Parameters order (mixtureofexperts.go:312-324):
     // shared experts, routed experts, then the router unless hash routing

@@ -113,12 +113,19 @@ typedef struct gtmoe_rows {
  * gpu/gpu_test.go:145-154): a second gtmoe_close does nothing, any other call
  * on the context or its layers answers GTMOE_ERR_INVALID_ARGUMENT with "the
  * context is closed" in gtmoe_last_error, and gtmoe_layer_destroy still frees
- * a layer.  A closed context's own few hundred bytes stay allocated until the
- * process ends. */
+ * a layer.  A closed context's own few hundred bytes stay allocated until
+ * gtmoe_context_free. */
 int32_t gtmoe_abi_version(void);
 int32_t gtmoe_device_count(int32_t *count);
 int32_t gtmoe_open(int32_t device, gtmoe_context **out);
 int32_t gtmoe_close(gtmoe_context *ctx);
+/* No counterpart in the reference (a gpu.Device is garbage-collected):
+ * closes the context if it is open and gives up the caller's handle, which
+ * must not be used again.  The context's memory goes once the handle and
+ * every layer and graph made on it are gone (gtmoe_layer_destroy,
+ * gtmoe_graph_destroy); until then those still answer "the context is
+ * closed". */
+int32_t gtmoe_context_free(gtmoe_context *ctx);
 /* Text of the last failure on this context (Device.LastError,
  * gpu/device.go:749-753).  With ctx NULL: the last failure of gtmoe_open. */
 const char *gtmoe_last_error(const gtmoe_context *ctx);
@@ -130,6 +137,12 @@ const char *gtmoe_last_error(const gtmoe_context *ctx);
  * testing a caller's fallback (the CPU answer and lastError of
  * gpu/device.go:733-737).  Armed per thread; one failure at a time. */
 int32_t gtmoe_test_inject_failure(const char *entry_point, int32_t status);
+
+/* Test hook, no counterpart in the reference: how many device allocations
+ * (hipMalloc) and frees (hipFree) the library has made since it was loaded,
+ * over all contexts and threads (either pointer may be NULL).  For tests that
+ * a call allocates nothing, e.g. gtmoe_forward_device_noalloc. */
+int32_t gtmoe_test_device_allocations(int64_t *allocations, int64_t *frees);
 
 /* ---- quantization ---------------------------------------------------------
  * Rows.Append over `rows` rows of float64 values (lowprecision/rows.go:38-79,
