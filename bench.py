@@ -469,6 +469,58 @@ def rotated_bytes(c, r):
     return int(sum(per_layer) * c["copies"])
 
 
+def measure_host_api(gt, c, layers, reps=200):
+    """The drop-in's own call path, as go/mixtureofexperts/gpu_unix.go makes it
+    for every Forward: gtmoe_set_balance_biases, gtmoe_forward (float64 rows
+    in over PCIe, float64 rows out, blocking until they are back) and
+    gtmoe_last_routing of the cached routing state (chosen experts, gates,
+    load, rows for each expert and their offsets), through ctypes on
+    preallocated buffers, rotating over the resident layers.  Wall clock per
+    Forward, and per call when each is repeated alone."""
+    import ctypes as C
+    lib = gt.library()
+    T, d, k, E = c["T"], c["d"], c["k"], c["E"]
+    x = np.random.default_rng(1).standard_normal((T, d))
+    y = np.empty_like(x)
+    bal = np.zeros(E)
+    chosen, rows = np.empty(T * k, np.int32), np.empty(T * k, np.int32)
+    gates = np.empty(T * k)
+    load, offs = np.empty(E, np.int32), np.empty(E + 1, np.int32)
+    got = C.c_int32()
+    px, py, pb = x.ctypes.data, y.ctypes.data, bal.ctypes.data
+    pc, pg, pl, pr, po = (a.ctypes.data for a in (chosen, gates, load, rows, offs))
+    handles = [m.handle for m in layers]
+
+    def balance(h):
+        return lib.gtmoe_set_balance_biases(h, pb)
+
+    def forward(h):
+        return lib.gtmoe_forward(h, T, px, None, py, 0)
+
+    def routing(h):
+        return lib.gtmoe_last_routing(h, C.byref(got), pc, pg, pl, pr, po)
+
+    def run(calls, n):
+        for i in range(len(handles)):  # every layer once first
+            for f in calls:
+                assert f(handles[i]) == 0
+        t0 = time.perf_counter()
+        for i in range(n):
+            h = handles[i % len(handles)]
+            for f in calls:
+                if f(h) != 0:
+                    raise RuntimeError("host API call failed")
+        return (time.perf_counter() - t0) / n * 1e6
+
+    per_forward = run((balance, forward, routing), reps)
+    parts = {"set_balance_biases": run((balance,), reps), "forward": run((forward,), reps)}
+    # gtmoe_last_routing alone reads the same forward's state again (the
+    # dispatch tables, once built, are not rebuilt)
+    parts["last_routing_after_forward"] = per_forward - parts["set_balance_biases"] - parts["forward"]
+    return {"us_per_forward": per_forward, "us_per_call": parts, "layers_rotated": len(handles), "reps": reps,
+            "tokens_per_s": T / (per_forward / 1e6)}
+
+
 def run_detail(gt, torch, ctx, stream, keys, shared, args):
     """The other workloads, each on its own resident layers (the C5 decode
     chunk reuses the stack of the C5 prefill headline when it was built)."""
@@ -481,13 +533,20 @@ def run_detail(gt, torch, ctx, stream, keys, shared, args):
         reuse = shared.get(c.get("seed"), None) if key in ("c5d", "c5p") else None
         layers = reuse if reuse is not None else build_layers(gt, ctx, c, make_specs(gt, c))
         steps = 50 if c["layers"] > 1 or c["T"] * c["k"] > 8 * c["E"] else 200
+        host = None
         try:
             r = measure(gt, torch, ctx, c, key, layers, steps, max(5, c["copies"]), stream)
+            if key == "c2" and c["T"] in (1, 32) or key == "c5d":
+                # the Go drop-in's per-Forward calls on one layer of this shape
+                host = measure_host_api(gt, dict(c, layers=1), layers[:c["layers"] * c["copies"]])
+                host["device_us_per_layer"] = r["ms_median"] * 1e3 / c["layers"]
         finally:
             if reuse is None:
                 for m in layers:
                     m.destroy()
         s = summary(key, c, r)
+        if host:
+            s["host_api"] = host
         if key == "c4":
             load = np.sort(r["loads"][0])[::-1]
             s["realized_load_desc_first8"] = load[:8].tolist()

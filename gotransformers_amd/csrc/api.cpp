@@ -55,6 +55,19 @@ hipError_t dev_free(void *p)
     return hipFree(p);
 }
 
+// Pinned host memory (the host API's staging) is counted with them.
+hipError_t pinned_malloc(void **p, size_t bytes)
+{
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
+    return hipHostMalloc(p, bytes, hipHostMallocDefault);
+}
+
+hipError_t pinned_free(void *p)
+{
+    g_device_frees.fetch_add(1, std::memory_order_relaxed);
+    return hipHostFree(p);
+}
+
 }  // namespace
 
 struct TimingRecord {
@@ -306,6 +319,17 @@ struct gtmoe_layer {
     // recorded graphs that hold pointers into this layer's workspace: while
     // any exists the workspace is never reallocated
     int live_graphs = 0;
+    // pinned host staging of the host-API calls: their float64 rows and the
+    // routing state they copy back, so that every copy is one asynchronous
+    // DMA on the stream and a call waits for the device once
+    char *stage = nullptr;
+    char *stage_dev = nullptr;  // the same memory as the device addresses it
+    size_t stage_bytes = 0;
+    // the routing state of the last gtmoe_forward, copied back with its
+    // outputs: gtmoe_last_routing then answers from host memory
+    bool routing_on_host = false;
+    std::vector<int32_t> host_chosen, host_rows, host_offsets;
+    std::vector<double> host_gates;
 };
 
 namespace {
@@ -787,9 +811,30 @@ void mark_forward(gtmoe_layer *L, int T, int path, hipStream_t s)
     L->last_path = path;
     L->last_stream = s;
     L->device_work_pending = s != L->ctx->stream;
+    L->routing_on_host = false;
     L->load_on_host = false;
     L->dispatch_pending = T > 0 && L->skipped_dispatch;
     L->adapter_T = -1;  // set again by the adapter path's forward
+}
+
+// Pinned staging of at least `bytes` for a host-API call.
+int32_t ensure_stage(gtmoe_layer *L, size_t bytes)
+{
+    if (bytes <= L->stage_bytes) return GTMOE_OK;
+    if (L->stage) {
+        HIP_TRY(L->ctx, hipDeviceSynchronize());  // no copy into the old block is in flight
+        (void)pinned_free(L->stage);
+        L->stage = nullptr;
+        L->stage_bytes = 0;
+    }
+    bytes = std::max(bytes, (size_t)64 << 10);
+    void *p = nullptr, *dp = nullptr;
+    HIP_TRY(L->ctx, pinned_malloc(&p, bytes));
+    L->stage = static_cast<char *>(p);
+    L->stage_bytes = bytes;
+    HIP_TRY(L->ctx, hipHostGetDevicePointer(&dp, p, 0));
+    L->stage_dev = static_cast<char *>(dp);
+    return GTMOE_OK;
 }
 
 // Before a host-API call enqueues work on the context's stream, which does
@@ -1581,6 +1626,7 @@ int32_t gtmoe_layer_destroy(gtmoe_layer *L)
         for (void *p : {(void *)L->router_w, (void *)L->router_b, (void *)L->balance, (void *)L->norm_w,
                         (void *)L->router_wn, L->ws.base})
             if (p) (void)dev_free(p);
+        if (L->stage) (void)pinned_free(L->stage);
         delete L;
     }
     release_context(ctx);  // the layer's reference
@@ -1663,6 +1709,9 @@ int32_t gtmoe_set_balance_biases(gtmoe_layer *L, const double *biases)
     if (!L || !biases) return GTMOE_ERR_INVALID_ARGUMENT;
     gtmoe_context *ctx = L->ctx;
     ENTER(ctx);
+    // the Go side hands the biases over on every forward: unchanged values
+    // (bit for bit) need no copy
+    if (memcmp(L->balance_host.data(), biases, sizeof(double) * L->E) == 0) return GTMOE_OK;
     int32_t rc = settle_device_work(L);
     if (rc != GTMOE_OK) return rc;
     L->balance_host.assign(biases, biases + L->E);
@@ -1726,26 +1775,69 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     }
     if (L->has_adapters) return adapter_forward(L, T, inputs, token_ids, outputs);
     Workspace &w = L->ws;
-    HIP_TRY(ctx, hipMemcpyAsync(w.x64, inputs, sizeof(double) * T * L->d, hipMemcpyHostToDevice, s));
-    if (L->desc.use_hash_routing)
-        HIP_TRY(ctx, hipMemcpyAsync(w.ids, token_ids, sizeof(int64_t) * T, hipMemcpyHostToDevice, s));
-    rc = prepare_and_route(L, T, Inputs{w.x64, true, false}, w.ids, path, s);
+    // The host buffers are bridged by pinned staging that the kernels read
+    // and write across the bus themselves: the CPU copies the rows (and ids)
+    // in and the routing kernel reads them there; the combine writes the
+    // output rows there and one pack kernel the routing state; the call waits
+    // for the device once.  The routing state comes back with the outputs
+    // because the reference keeps it (LastExpertLoad, UpdateBalance,
+    // Backward) and the Go side reads it after every forward; the dispatch
+    // tables, which the few-token kernels did without, are built behind the
+    // expert kernels first.
+    const size_t rows_bytes = sizeof(double) * T * L->d;
+    const size_t tk = (size_t)T * L->k;
+    const int words[] = {L->E, (int)tk, (int)(2 * tk), (int)tk, L->E + 1};  // load, chosen, gates, rows, offsets
+    size_t route_bytes = 0;
+    for (int n : words) route_bytes += (size_t)(n + 15) / 16 * 64;
+    const size_t ids_bytes = align_up(sizeof(int64_t) * T, 64);
+    rc = ensure_stage(L, 2 * rows_bytes + ids_bytes + route_bytes);
+    if (rc != GTMOE_OK) return rc;
+    const size_t ox = 0, oy = rows_bytes, oid = 2 * rows_bytes, oroute = oid + ids_bytes;
+    memcpy(L->stage + ox, inputs, rows_bytes);
+    const int64_t *ids = nullptr;
+    if (L->desc.use_hash_routing) {
+        memcpy(L->stage + oid, token_ids, sizeof(int64_t) * T);
+        ids = reinterpret_cast<const int64_t *>(L->stage_dev + oid);
+    }
+    rc = prepare_and_route(L, T, Inputs{L->stage_dev + ox, true, false}, ids, path, s);
     if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
     RUN(ctx, s, "combine",
-        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos, w.gates32, nullptr, nullptr,
-                       w.y64, s));
-    HIP_TRY(ctx, hipMemcpyAsync(outputs, w.y64, sizeof(double) * T * L->d, hipMemcpyDeviceToHost, s));
-    // the load comes back with the outputs unless the dispatch was skipped
-    // (then it is built when read)
-    const bool load_now = !L->skipped_dispatch;
-    if (load_now) {
-        L->last_load.assign(L->E, 0);
-        HIP_TRY(ctx, hipMemcpyAsync(L->last_load.data(), w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost, s));
+        launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos,
+                       w.gates32, nullptr, nullptr, reinterpret_cast<double *>(L->stage_dev + oy), s));
+    if (L->skipped_dispatch)
+        RUN(ctx, s, "dispatch",
+            launch_dispatch(w.chosen, T, L->k, L->E, L->S, kGemvSlice, w.load, w.offsets, w.rows, w.pos, w.goff,
+                            w.tok, w.tile_off, w.tile_desc, w.chunk_cnt, s));
+    PackParts pp{};
+    const void *srcs[] = {w.load, w.chosen, w.gates, w.rows, w.offsets};
+    for (int i = 0; i < 5; ++i) {
+        pp.src[i] = static_cast<const uint32_t *>(srcs[i]);
+        pp.words[i] = words[i];
     }
+    pp.n = 5;
+    RUN(ctx, s, "pack_routing", launch_pack_words(pp, reinterpret_cast<uint32_t *>(L->stage_dev + oroute), s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
+    memcpy(outputs, L->stage + oy, rows_bytes);
     mark_forward(L, T, path, s);
-    L->load_on_host = load_now;
+    L->skipped_dispatch = false;
+    L->dispatch_pending = false;
+    const char *part = L->stage + oroute;
+    auto next = [&](int i) {
+        const char *p = part;
+        part += (size_t)(words[i] + 15) / 16 * 64;
+        return p;
+    };
+    const int32_t *hload = (const int32_t *)next(0), *hchosen = (const int32_t *)next(1);
+    const double *hgates = (const double *)next(2);
+    const int32_t *hrows = (const int32_t *)next(3), *hoffsets = (const int32_t *)next(4);
+    L->last_load.assign(hload, hload + L->E);
+    L->load_on_host = true;
+    L->host_chosen.assign(hchosen, hchosen + tk);
+    L->host_gates.assign(hgates, hgates + tk);
+    L->host_rows.assign(hrows, hrows + tk);
+    L->host_offsets.assign(hoffsets, hoffsets + L->E + 1);
+    L->routing_on_host = true;
     return GTMOE_OK;
 }
 
@@ -1885,17 +1977,47 @@ int32_t gtmoe_last_routing(gtmoe_layer *L, int32_t *tokens_out, int32_t *chosen,
         if (expert_offsets) memset(expert_offsets, 0, sizeof(int32_t) * (L->E + 1));
         return GTMOE_OK;
     }
+    const size_t tk = (size_t)T * L->k;
+    if (L->routing_on_host) {  // copied back by gtmoe_forward
+        if (chosen) memcpy(chosen, L->host_chosen.data(), tk * 4);
+        if (gates) memcpy(gates, L->host_gates.data(), tk * 8);
+        if (load) memcpy(load, L->last_load.data(), sizeof(int32_t) * L->E);
+        if (rows_for_expert) memcpy(rows_for_expert, L->host_rows.data(), tk * 4);
+        if (expert_offsets) memcpy(expert_offsets, L->host_offsets.data(), sizeof(int32_t) * (L->E + 1));
+        return GTMOE_OK;
+    }
     int32_t rc = ensure_dispatch(L);
     if (rc != GTMOE_OK) return rc;
-    HIP_TRY(ctx, hipStreamSynchronize(L->last_stream));
-    const size_t tk = (size_t)T * L->k;
+    // every table asked for comes back through pinned staging in
+    // asynchronous copies behind the forward's kernels, then one wait
     Workspace &w = L->ws;
-    if (chosen) HIP_TRY(ctx, hipMemcpy(chosen, w.chosen, tk * 4, hipMemcpyDeviceToHost));
-    if (gates) HIP_TRY(ctx, hipMemcpy(gates, w.gates, tk * 8, hipMemcpyDeviceToHost));
-    if (load) HIP_TRY(ctx, hipMemcpy(load, w.load, sizeof(int32_t) * L->E, hipMemcpyDeviceToHost));
-    if (rows_for_expert) HIP_TRY(ctx, hipMemcpy(rows_for_expert, w.rows, tk * 4, hipMemcpyDeviceToHost));
-    if (expert_offsets)
-        HIP_TRY(ctx, hipMemcpy(expert_offsets, w.offsets, sizeof(int32_t) * (L->E + 1), hipMemcpyDeviceToHost));
+    struct Part {
+        void *dst;
+        const void *src;
+        size_t bytes;
+    } parts[] = {{chosen, w.chosen, tk * 4},
+                 {gates, w.gates, tk * 8},
+                 {load, w.load, sizeof(int32_t) * L->E},
+                 {rows_for_expert, w.rows, tk * 4},
+                 {expert_offsets, w.offsets, sizeof(int32_t) * (L->E + 1)}};
+    size_t need = 0;
+    for (const Part &p : parts) need += p.dst ? align_up(p.bytes, 64) : 0;
+    rc = ensure_stage(L, need);
+    if (rc != GTMOE_OK) return rc;
+    hipStream_t s = L->last_stream;
+    size_t off = 0;
+    for (const Part &p : parts)
+        if (p.dst) {
+            HIP_TRY(ctx, hipMemcpyAsync(L->stage + off, p.src, p.bytes, hipMemcpyDeviceToHost, s));
+            off += align_up(p.bytes, 64);
+        }
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    off = 0;
+    for (const Part &p : parts)
+        if (p.dst) {
+            memcpy(p.dst, L->stage + off, p.bytes);
+            off += align_up(p.bytes, 64);
+        }
     return GTMOE_OK;
 }
 

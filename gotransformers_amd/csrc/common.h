@@ -272,6 +272,15 @@ hipError_t launch_combine(int T, int d, int S, int k, const void *slot_out, bool
                           const float *gates32, const float *residual, float *out32, double *out64, hipStream_t s,
                           const CombineNorm &norm = CombineNorm{});
 hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s);
+// Up to kMax device arrays of 4-byte words copied one after the other into
+// dst, each part starting at a multiple of 16 words.
+struct PackParts {
+    static constexpr int kMax = 6;
+    const uint32_t *src[kMax];
+    int words[kMax];
+    int n;
+};
+hipError_t launch_pack_words(const PackParts &p, uint32_t *dst, hipStream_t s);
 hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);
 
 // Adapter path (lora.hip, route.hip).

@@ -1,4 +1,6 @@
 // Input preparation, RMSNorm, the weighted combine, and small fills.
+#include <algorithm>
+
 #include "common.h"
 
 namespace gtmoe {
@@ -359,6 +361,31 @@ hipError_t launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t s)
 {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+// The routing state a host-API forward hands back, gathered into one block
+// (of pinned host memory, written across the bus by this kernel): the 4-byte
+// words of each part one after the other, every part starting at a multiple
+// of 16 words.
+__global__ __launch_bounds__(256) void pack_words_kernel(PackParts p, uint32_t *__restrict__ dst)
+{
+    uint32_t *out = dst;
+    for (int i = 0; i < PackParts::kMax; ++i) {
+        if (i >= p.n) break;
+        const uint32_t *src = p.src[i];
+        for (int j = blockIdx.x * 256 + threadIdx.x; j < p.words[i]; j += gridDim.x * 256) out[j] = src[j];
+        out += (p.words[i] + 15) / 16 * 16;
+    }
+}
+
+hipError_t launch_pack_words(const PackParts &p, uint32_t *dst, hipStream_t s)
+{
+    if (p.n < 0 || p.n > PackParts::kMax) return hipErrorInvalidValue;
+    long long most = 0;
+    for (int i = 0; i < p.n; ++i) most = std::max<long long>(most, p.words[i]);
+    const int blocks = (int)std::min<long long>(64, std::max<long long>(1, (most + 255) / 256));
+    hipLaunchKernelGGL(pack_words_kernel, dim3(blocks), dim3(256), 0, s, p, dst);
     return hipGetLastError();
 }
 
