@@ -196,10 +196,13 @@ def cpu_baseline(c, specs, budget_s):
     return allc
 
 
-# the sources a kernel's measured traffic depends on
+# the sources a kernel is built from (its measured traffic and profiles hold
+# for these bytes only); also the kernels' routing neighbours for the
+# decode profiles
 TRAFFIC_SOURCES = {
-    "mfma_gateup": ["experts_mfma.hip", "common.h"],
+    "mfma_gateup": ["experts_mfma.hip", "mfma.h", "common.h"],
     "gemv_gateup": ["experts_gemv.hip", "common.h"],
+    "route": ["route.hip", "kernels.h", "common.h", "mfma.h"],
 }
 
 

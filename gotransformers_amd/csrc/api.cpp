@@ -19,7 +19,7 @@
 #include <type_traits>
 #include <vector>
 
-#include "common.h"
+#include "kernels.h"
 #include "gtmoe.h"
 #include "weightfile.h"
 

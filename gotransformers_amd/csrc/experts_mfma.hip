@@ -36,7 +36,7 @@
 // them and found in that XCD's L2 by the other tiles.
 #include <type_traits>
 
-#include "common.h"
+#include "mfma.h"
 
 namespace gtmoe {
 

@@ -26,7 +26,7 @@
 //   DownGradients / UpGradients), scale[G] fp32.
 // Everything runs in fp32 with the reference's operation order where it has
 // one (block sums of a row times the block scale, bias after the adapter).
-#include "common.h"
+#include "kernels.h"
 
 namespace gtmoe {
 

@@ -1,7 +1,7 @@
 // Input preparation, RMSNorm, the weighted combine, and small fills.
 #include <algorithm>
 
-#include "common.h"
+#include "kernels.h"
 
 namespace gtmoe {
 

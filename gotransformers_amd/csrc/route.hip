@@ -4,7 +4,7 @@
 // Built with -ffp-contract=off: the affinity and gate arithmetic must round
 // exactly like the float64 CPU restatement (mixtureofexperts.go:153-173), so
 // nothing here may be fused unless written as an explicit fmaf.
-#include "common.h"
+#include "kernels.h"
 
 #include <math.h>
 
