@@ -12,14 +12,21 @@ combine and residual per block).
 
 `value` is tokens per second from the median of the per-step durations,
 each bracketed by a HIP event pair on the stream the kernels run on (the
-residual stream's reset before each step is outside the events).  The line
-also reports the mean over the same steps and the wall clock of all of them.
+residual stream's reset before each step is outside the events).  The steps
+are enqueued behind a bounded spin kernel, so they run back to back and the
+events time the device rather than the host's enqueue of few-microsecond
+launches.  The line also reports the mean over the same steps and the host's
+time to enqueue one step (which the spin hides: a step whose enqueue takes
+longer than its device time is host-bound without a captured graph).
 
 `roofline` is for the dominant kernel (the MFMA grouped gate/up GEMM on the
 prefill path, the dequant-GEMV gate/up on the decode path): achieved =
 algorithmic FLOPs or bytes per launch / mean launch time, the mean taken by
-one HIP event pair around a burst of back-to-back relaunches of that kernel
-over every resident layer; `step_frac` is the whole step's algorithmic work
+HIP event pairs around rotations of back-to-back relaunches of that kernel,
+each rotation behind a short spin: on the decode path one relaunch per
+resident layer per rotation (the pass over the layers a step makes, so the
+kernel runs as hot as in the steps), about 200 launches in all; on the
+prefill path one rotation of 20-24 launches; `step_frac` is the whole step's algorithmic work
 over the step time against the same peak.  `traffic` is the HBM bytes per
 launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes for the same
 workload, read from profiles/traffic.json and reported only when the
@@ -342,6 +349,20 @@ def build_layers(gt, ctx, c, specs):
     return layers
 
 
+# Shader-clock cycles of the spin kernel that holds a stream while the host
+# enqueues timed work behind it: the enqueue of a few-microsecond launch costs
+# the host about as long as the launch runs, so without it the events would
+# time the host (under a kernel tracer, several times as long).  About 33 ms
+# at 2.4 GHz ahead of the timed steps, 10 ms ahead of each relaunch rotation.
+HOLD_STEPS = 80_000_000
+HOLD_ROTATION = 25_000_000
+
+
+def hold_queue(torch, cycles=HOLD_STEPS):
+    """A bounded spin on the current stream."""
+    torch.cuda._sleep(cycles)
+
+
 def measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=False, n_detail=20):
     """One workload on resident layers: per-step event times, the dominant
     kernel's relaunch burst and the per-kernel breakdown."""
@@ -383,32 +404,50 @@ def measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=False, 
         path = layers[0].last_path
         loads = [m.last_expert_load() for m in layers[:c["layers"]]]
 
-        # timed steps: an event pair on the kernels' stream around each step
+        # timed steps: an event pair on the kernels' stream around each step,
+        # all enqueued behind a spin kernel so that the steps then run back to
+        # back, as a captured graph would run them (the host's enqueue time is
+        # outside the events; enqueue_ms is what it costs per step)
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         torch.cuda.synchronize()
+        hold_queue(torch)
         t0 = time.perf_counter()
         for i in range(steps):
             prepare(i)
             evs[i][0].record(stream)
             step(i)
             evs[i][1].record(stream)
+        enqueue_ms = (time.perf_counter() - t0) * 1e3 / steps
         torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
         step_ms = np.array([a.elapsed_time(b) for a, b in evs])
 
-        # the dominant kernel: a burst of relaunches of each layer's gate/up
-        # kernel of its last forward, rotating over every resident layer (so
-        # weight reads keep missing the Infinity Cache), one event pair
-        n_burst = max(len(layers), (200 if path == gt.PATH_FP32 else 20) // len(layers) * len(layers))
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # the dominant kernel: rotations of relaunches of each layer's gate/up
+        # kernel of its last forward over every resident layer (so weight
+        # reads keep missing the Infinity Cache), one event pair around each
+        # rotation, each rotation behind a short spin.  One rotation is one
+        # pass over the resident layers, as the steps make it: a long
+        # back-to-back burst of the kernel alone runs hotter than the steps
+        # do, and its later launches slow down (about 15% at C5 decode).
+        # (prefill: one rotation of at least 20 launches; its launches take
+        # hundreds of microseconds each)
+        if path == gt.PATH_FP32:
+            per_rot, rotations = len(layers), max(1, -(-200 // len(layers)))
+        else:
+            per_rot, rotations = max(len(layers), 20 // len(layers) * len(layers)), 1
         for m in layers:
             m.relaunch(gt.KERNEL_GATEUP, stream=sptr)
-        ev0.record(stream)
-        for i in range(n_burst):
-            layers[i % len(layers)].relaunch(gt.KERNEL_GATEUP, stream=sptr)
-        ev1.record(stream)
-        ev1.synchronize()
-        kmean_s = ev0.elapsed_time(ev1) / n_burst / 1e3
+        rot_ms = []
+        for _ in range(rotations):
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            hold_queue(torch, HOLD_ROTATION)
+            ev0.record(stream)
+            for i in range(per_rot):
+                layers[i % len(layers)].relaunch(gt.KERNEL_GATEUP, stream=sptr)
+            ev1.record(stream)
+            rot_ms.append((ev0, ev1))
+        torch.cuda.synchronize()
+        n_burst = rotations * per_rot
+        kmean_s = sum(a.elapsed_time(b) for a, b in rot_ms) / n_burst / 1e3
 
         # per-kernel breakdown: the library's event pair around every kernel
         ctx.timing(True)
@@ -447,7 +486,7 @@ def measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=False, 
     return {
         "path": path, "decode": decode, "loads": loads, "ms_median": med_s * 1e3,
         "ms_mean": float(step_ms.mean()), "ms_min": float(step_ms.min()), "ms_max": float(step_ms.max()),
-        "wall_ms": wall_ms, "value": T / med_s, "roofline": roof,
+        "enqueue_ms": enqueue_ms, "value": T / med_s, "roofline": roof,
         "kernel_ms_per_step": {k: v[0] / n_detail for k, v in sorted(times.items())},
     }
 
@@ -648,12 +687,12 @@ def main():
                    "expert_weights": f"{c['prec']} per-16 fp32 scales", "layers_per_step": c["layers"],
                    "weight_copies": c["copies"], "rotated_gateup_weight_bytes": rotated_bytes(c, r),
                    "path": "fp32 dequant-GEMV" if decode else "bf16 MFMA grouped GEMM",
-                   "hip_graph": bool(args.graph), "step_timing": "median of per-step HIP event pairs"},
+                   "hip_graph": bool(args.graph), "step_timing": "median of per-step HIP event pairs; steps enqueued behind a spin kernel, so they run back to back"},
         "roofline": r["roofline"],
         "cpu_baseline": cpu,
         "detail": {
             "ms_per_step_mean": r["ms_mean"], "ms_per_step_min": r["ms_min"], "ms_per_step_max": r["ms_max"],
-            "wall_ms_per_step": r["wall_ms"],
+            "host_enqueue_ms_per_step": r["enqueue_ms"],
             "kernel_ms_per_step_events": r["kernel_ms_per_step"],
             "active_experts_layer0": int(np.count_nonzero(r["loads"][0])),
             "workloads": detail_workloads,
