@@ -22,11 +22,11 @@ longer than its device time is host-bound without a captured graph).
 `roofline` is for the dominant kernel (the MFMA grouped gate/up GEMM on the
 prefill path, the dequant-GEMV gate/up on the decode path): achieved =
 algorithmic FLOPs or bytes per launch / mean launch time, the mean taken by
-HIP event pairs around rotations of back-to-back relaunches of that kernel,
-each rotation behind a short spin: on the decode path one relaunch per
-resident layer per rotation (the pass over the layers a step makes, so the
-kernel runs as hot as in the steps), about 200 launches in all; on the
-prefill path one rotation of 20-24 launches; `step_frac` is the whole step's algorithmic work
+HIP event pairs around rotations of back-to-back relaunches of that kernel:
+on the decode path one relaunch per resident layer per rotation (the pass
+over the layers a step makes, so the kernel runs as hot as in the steps),
+each rotation behind a short spin, about 200 launches in all; on the prefill
+path one rotation of 20-24 launches, no spin; `step_frac` is the whole step's algorithmic work
 over the step time against the same peak.  `traffic` is the HBM bytes per
 launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes for the same
 workload, read from profiles/traffic.json and reported only when the
@@ -428,8 +428,10 @@ def measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=False, 
         # pass over the resident layers, as the steps make it: a long
         # back-to-back burst of the kernel alone runs hotter than the steps
         # do, and its later launches slow down (about 15% at C5 decode).
-        # (prefill: one rotation of at least 20 launches; its launches take
-        # hundreds of microseconds each)
+        # (prefill: one rotation of at least 20 launches and no spin: its
+        # launches take hundreds of microseconds each, far longer than their
+        # enqueue, and a rotation right after a spin, with the chip idle
+        # meanwhile, measured 15-20% slower than the same kernel in the steps)
         if path == gt.PATH_FP32:
             per_rot, rotations = len(layers), max(1, -(-200 // len(layers)))
         else:
@@ -439,7 +441,8 @@ def measure(gt, torch, ctx, c, key, layers, steps, warmup, stream, graph=False, 
         rot_ms = []
         for _ in range(rotations):
             ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            hold_queue(torch, HOLD_ROTATION)
+            if path == gt.PATH_FP32:
+                hold_queue(torch, HOLD_ROTATION)
             ev0.record(stream)
             for i in range(per_rot):
                 layers[i % len(layers)].relaunch(gt.KERNEL_GATEUP, stream=sptr)

@@ -12,7 +12,9 @@
 // Four waves split the columns: each wave owns all 128 positions x 64
 // columns (4 x 2 MFMA tiles of 32 x 32; for gate/up its two column tiles are
 // gate and up of the same 32 neurons, so both values of a neuron land in
-// the same lane).  The activations reach LDS by LDS-DMA loads (three
+// the same lane).  The MFMAs take the weights as their first operand, so an
+// accumulator tile is the output's transpose: a lane holds one position and
+// four runs of four consecutive neurons, which leave as 8-byte pieces.  The activations reach LDS by LDS-DMA loads (three
 // buffers, K steps of 64, two steps ahead) and are read by all four waves;
 // each weight value is loaded and dequantized exactly once per workgroup, by
 // the wave that uses it, straight from the panel layout into MFMA operand
@@ -255,11 +257,9 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     // resources; columns past n read zeros and are not written
     GroupSrc bsrc[2];
     uint32_t bvo[2], bvs[2];
-    int ncol[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = GATEUP ? ntile * (BN / 2) + wave * 32 + col : ntile * BN + wave * 64 + j * 32 + col;
-        ncol[j] = n;
         const void *w = GATEUP ? (j ? a.w1 : a.w0) : a.w0;
         const float *sc = GATEUP ? (j ? a.s1 : a.s0) : a.s0;
         bsrc[j].codes = __builtin_amdgcn_make_buffer_rsrc(
@@ -279,13 +279,36 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
         }
     }
 
-    floatx16 acc[MI][2];
+    // Accumulator tile (i, j) holds output[position 32 i + col][neuron
+    // nbase[j] + nn(r)] in register r, nn(r) = 8 (r / 4) + 4 h + r % 4 (the
+    // weights are the MFMA's first operand).  The accumulators start at the
+    // neurons' biases: the epilogue has nothing to load.  The biases are
+    // requested here and copied in after the prologue, whose counted waits
+    // cover them (they are the oldest loads).
+    int nbase[2];
+    floatx16 binit[2], acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int j = 0; j < 2; ++j) {
+        nbase[j] = GATEUP ? ntile * (BN / 2) + wave * 32 : ntile * BN + wave * 64 + j * 32;
+        const float *bias = (GATEUP && j ? a.b1 : a.b0) + (size_t)g * a.n;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int q = 0; q < 4; ++q) {
+            const int n = nbase[j] + 8 * q + 4 * h;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a.n % 4 == 0) {
+                if (n < a.n) v = *reinterpret_cast<const float4 *>(bias + n);
+            } else {
+                if (n < a.n) v.x = bias[n];
+                if (n + 1 < a.n) v.y = bias[n + 1];
+                if (n + 2 < a.n) v.z = bias[n + 2];
+                if (n + 3 < a.n) v.w = bias[n + 3];
+            }
+            binit[j][4 * q] = v.x;
+            binit[j][4 * q + 1] = v.y;
+            binit[j][4 * q + 2] = v.z;
+            binit[j][4 * q + 3] = v.w;
+        }
+    }
 
     // Software pipeline: during step k the activations of step k + 2 are
     // on their way into LDS buffer (k + 2) % 3 (buffer (k + 2) % 3 was read
@@ -367,7 +390,7 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfp[j][s2], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfp[j][s2], af[i], acc[i][j], 0, 0, 0);
         }
     };
     auto interleave = [&]() {
@@ -426,6 +449,10 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     __builtin_amdgcn_sched_barrier(0);
     dequant_pair(bq[0], 0, bfa);
     end_step(std::integral_constant<int, kPrologueWait>{});
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = binit[j];
     int k = 0;
     for (; k + UNROLL <= nsteps; k += UNROLL) {
         step(std::integral_constant<int, 0>{}, k, loop_wait);
@@ -448,24 +475,19 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     end_step(full_wait);
 
     // epilogue: the tile's bf16 outputs are put in LDS (free now: every wave
-    // is past its last read of the activations and every load has landed)
-    // and leave in 16-byte stores of whole row pieces.  Lane holds column
-    // (lane & 31) of each 32x32 tile, rows 8*(r/4) + 4*(lane/32) + r%4 for
-    // accumulator register r; rows past the tile's M are computed from zero
-    // activations and not stored.  Row block i goes to half i / 2.
+    // is past its last read of the activations and every load has landed),
+    // four neurons of a position per 8-byte write, and leave in 16-byte
+    // stores of whole row pieces.  Lane holds position 32 i + col of row
+    // block i and neurons nn(r) of each column tile; rows past the tile's M
+    // are computed from zero activations and not stored.  Row block i goes
+    // to half i / 2, LDS column wave * 32 + nn.
     uint16_t *os0 = reinterpret_cast<uint16_t *>(b0), *os1 = reinterpret_cast<uint16_t *>(b1);
-    const int rq = h * 4;
-    auto put = [&](int i, int r, int c, uint32_t pair) {  // registers r, r + 1 (rows m, m + 1)
+    auto put4 = [&](int i, int q, uint32_t lo, uint32_t hi) {  // neurons 8 q + 4 h .. + 3
         uint16_t *os = i < 2 ? os0 : os1;
-        const int m = (i & 1) * 32 + 8 * (r >> 2) + rq + (r & 3);
-        os[m * OLD + c] = (uint16_t)pair;
-        os[(m + 1) * OLD + c] = (uint16_t)(pair >> 16);
+        const int m = (i & 1) * 32 + col;
+        *reinterpret_cast<uint2 *>(os + m * OLD + wave * 32 + 8 * q + 4 * h) = make_uint2(lo, hi);
     };
     if constexpr (GATEUP) {
-        const int n = ncol[0];
-        const bool has = n < a.n;
-        const float bg = has ? a.b0[(size_t)g * a.n + n] : 0.f, bu = has ? a.b1[(size_t)g * a.n + n] : 0.f;
-        const int c = wave * 32 + col;
         auto emit_all = [&](auto clamp_tag) {
             constexpr bool CL = decltype(clamp_tag)::value;
             auto swiglu = [&](float gv, float uv) {
@@ -478,10 +500,13 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; r += 2)
-                    put(i, r, c,
-                        pack_bf16(swiglu(acc[i][0][r] + bg, acc[i][1][r] + bu),
-                                  swiglu(acc[i][0][r + 1] + bg, acc[i][1][r + 1] + bu)));
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 4 * q;
+                    put4(i, q,
+                         pack_bf16(swiglu(acc[i][0][r], acc[i][1][r]), swiglu(acc[i][0][r + 1], acc[i][1][r + 1])),
+                         pack_bf16(swiglu(acc[i][0][r + 2], acc[i][1][r + 2]),
+                                   swiglu(acc[i][0][r + 3], acc[i][1][r + 3])));
+                }
         };
         if (a.clamp > 0.f) emit_all(std::true_type{});
         else emit_all(std::false_type{});
@@ -493,13 +518,13 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
         for (int j = 0; j < 2; ++j) {
             // one column tile of every wave per pass: tile column c is output
             // column ntile * 256 + (c / 32) * 64 + j * 32 + c % 32
-            const int n = ncol[j];
-            const float bd = n < a.n ? a.b0[(size_t)g * a.n + n] : 0.f;
-            const int c = wave * 32 + col;
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; r += 2) put(i, r, c, pack_bf16(acc[i][j][r] + bd, acc[i][j][r + 1] + bd));
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 4 * q;
+                    put4(i, q, pack_bf16(acc[i][j][r], acc[i][j][r + 1]), pack_bf16(acc[i][j][r + 2], acc[i][j][r + 3]));
+                }
             __syncthreads();
             store_tile(a, os0, os1, p0, M, [&](int c) { return ntile * BN + (c >> 5) * 64 + j * 32 + (c & 31); });
             if (j == 0) __syncthreads();  // the next pass rewrites the LDS tile
