@@ -623,6 +623,11 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
             launch_combine(T, pend->d, pend->S, pend->k, pend->slot, false, pend->pos, pend->gates,
                            (const float *)in.x, (float *)in.x, nullptr, s));
     if (zero_out) RUN(ctx, s, "zero_out", launch_fill_i32(reinterpret_cast<int32_t *>(zero_out), T * L->d, 0, s));
+    // the chunked dispatch's counts: cleared by the router, added up by the
+    // top-k (no count launch)
+    const bool counted = !hash && dispatch_chunked(T);
+    int32_t *cnt = counted ? w.chunk_cnt : nullptr;
+    const int ncnt = counted ? dispatch_chunks(T) * L->E : 0;
     if (prenormed) {
         // the previous layer's combine wrote the bf16 normalised rows and each
         // row's inverse RMS; the router reads the raw rows (stride d == dp)
@@ -630,15 +635,16 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         if (!hash) {
             RUN(ctx, s, "router",
                 launch_router((const float *)in.x, L->d, T, L->d, L->router_wn, L->dp, L->router_b, L->E, w.logits,
-                              s, w.inv));
-            RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
+                              s, w.inv, nullptr, 0, cnt, ncnt));
+            RUN(ctx, s, "topk",
+                launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s, cnt));
         } else {
             RUN(ctx, s, "hash_route",
                 launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
         }
         RUN(ctx, s, "dispatch",
             launch_dispatch(w.chosen, T, L->k, L->E, L->S, bm, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
-                            w.tile_off, w.tile_desc, w.chunk_cnt, s));
+                            w.tile_off, w.tile_desc, w.chunk_cnt, s, counted));
         return GTMOE_OK;
     }
     if (in.norm) {
@@ -656,12 +662,12 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         RUN(ctx, s, "hash_route", launch_hash_route(token_ids, T, L->E, L->k, w.chosen, w.gates, w.gates32, s));
     } else {
         RUN(ctx, s, "router", launch_router(xr, L->dp, T, L->d, L->router_w, L->dp, L->router_b, L->E, w.logits, s,
-                                            nullptr, router_xb, L->dp));
-        RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s));
+                                            nullptr, router_xb, L->dp, cnt, ncnt));
+        RUN(ctx, s, "topk", launch_topk(w.logits, T, L->E, L->k, L->balance, w.chosen, w.gates, w.gates32, s, cnt));
     }
     RUN(ctx, s, "dispatch",
         launch_dispatch(w.chosen, T, L->k, L->E, L->S, bm, w.load, w.offsets, w.rows, w.pos, w.goff, w.tok,
-                        w.tile_off, w.tile_desc, w.chunk_cnt, s));
+                        w.tile_off, w.tile_desc, w.chunk_cnt, s, counted));
     return GTMOE_OK;
 }
 

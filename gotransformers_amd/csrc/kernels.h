@@ -93,22 +93,29 @@ hipError_t launch_rmsnorm(const float *x, int T, int d, const float *w, float *x
 // inverse RMS of a row whose norm weights are folded into w).  xb (optional,
 // rows of ldb >= d bf16 values, x unpadded: ldx == d, d % 64 == 0): also
 // write x as bf16, as the input conversion would.
+// zero (optional): nzero ints cleared by the router kernel, for the top-k
+// after it to count into (the chunked dispatch's chunk_cnt).
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
                          double *logits, hipStream_t s, const float *row_scale = nullptr, uint16_t *xb = nullptr,
-                         int ldb = 0);
+                         int ldb = 0, int32_t *zero = nullptr, int nzero = 0);
+// chunk_cnt (optional, zero on entry): the chunked dispatch's per-chunk
+// expert counts, added up by the top-k (launch_dispatch then with counted).
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
-                       double *gates, float *gates32, hipStream_t s);
+                       double *gates, float *gates32, hipStream_t s, int32_t *chunk_cnt = nullptr);
 hipError_t launch_hash_route(const int64_t *ids, int T, int E, int k, int32_t *chosen, double *gates,
                              float *gates32, hipStream_t s);
 bool fused_route_fits(int T, int k, int kp);
 hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, bool dispatch, hipStream_t s);
-// Dispatch: one workgroup up to 1024 tokens, else a count and a placement
-// launch over chunks of 256 tokens using chunk_cnt [dispatch_chunks(T)][E]
-// as scratch.
+// Dispatch: one workgroup up to 1024 tokens, else (dispatch_chunked) a
+// count and a placement launch over chunks of tokens using chunk_cnt
+// [dispatch_chunks(T)][E]; counted: the top-k already made the counts, only
+// the placement runs.
 int dispatch_chunks(int T);
+bool dispatch_chunked(int T);
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
                            int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
-                           int32_t *tile_off, int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s);
+                           int32_t *tile_off, int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s,
+                           bool counted = false);
 // The next stack layer's RMSNorm done by the combine (bf16 slot rows, d <=
 // 2048, d % 8 == 0, with a residual, fp32 output of stride d): w its norm
 // weights [d], xb its bf16 rows [T][ldb], inv the rows' inverse RMS [T].

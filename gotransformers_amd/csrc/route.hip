@@ -148,6 +148,18 @@ __device__ double affinity(double logit)
 // Router logits: logits[t][e] = double(sum_i x[t][i] * w[e][i]) + bias[e].
 // ---------------------------------------------------------------------------
 
+// zero[0 .. nzero) cleared by the whole grid (any grid shape): the chunked
+// dispatch's per-chunk expert counts, which the top-k after the router adds
+// up (the clearing must be a kernel, not a memset, where the launch may be
+// captured into a graph).
+__device__ __forceinline__ void clear_counts(int32_t *__restrict__ zero, int nzero)
+{
+    if (zero == nullptr) return;
+    const int wg = blockIdx.y * gridDim.x + blockIdx.x;
+    const int stride = gridDim.x * gridDim.y * blockDim.x;
+    for (int i = wg * blockDim.x + threadIdx.x; i < nzero; i += stride) zero[i] = 0;
+}
+
 // Few tokens: one wave per (token, expert) dot product; lanes read float4
 // runs of the zero-padded rows (x row stride ldx, router row stride ldw, both
 // multiples of 64 floats) and reduce across the wave.
@@ -155,8 +167,10 @@ __global__ __launch_bounds__(256) void router_small_kernel(const float *__restri
                                                            const float *__restrict__ w, int ldw,
                                                            const double *__restrict__ bias, int E,
                                                            double *__restrict__ logits,
-                                                           const float *__restrict__ row_scale)
+                                                           const float *__restrict__ row_scale,
+                                                           int32_t *__restrict__ zero, int nzero)
 {
+    clear_counts(zero, nzero);
     const int lane = threadIdx.x & 63;
     const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (pair >= T * E) return;  // wave-uniform
@@ -194,9 +208,11 @@ __global__ __launch_bounds__(64 * NW) void router_mfma_kernel(const float *__res
                                                               const float *__restrict__ w, int ldw,
                                                               const double *__restrict__ bias, int E,
                                                               double *__restrict__ logits,
-                                                              const float *__restrict__ row_scale)
+                                                              const float *__restrict__ row_scale,
+                                                              int32_t *__restrict__ zero, int nzero)
 {
     __shared__ float red[NW][16 * NE][64];
+    clear_counts(zero, nzero);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32 * NE;
     const int r = lane & 31, h = lane >> 5;
@@ -440,8 +456,10 @@ __global__ __launch_bounds__(512) void router_lds_kernel(const float *__restrict
                                                          const double *__restrict__ bias, int E,
                                                          double *__restrict__ logits,
                                                          const float *__restrict__ row_scale,
-                                                         uint16_t *__restrict__ xb, int ldb)
+                                                         uint16_t *__restrict__ xb, int ldb,
+                                                         int32_t *__restrict__ zero, int nzero)
 {
+    clear_counts(zero, nzero);
     // four separate arrays, so that the compiler tracks the loads into each
     __shared__ __attribute__((aligned(16))) char s0[router_lds_buf<NE>()];
     __shared__ __attribute__((aligned(16))) char s1[router_lds_buf<NE>()];
@@ -455,7 +473,8 @@ __global__ __launch_bounds__(512) void router_lds_kernel(const float *__restrict
 }
 
 hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, int ldw, const double *bias, int E,
-                         double *logits, hipStream_t s, const float *row_scale, uint16_t *xb, int ldb)
+                         double *logits, hipStream_t s, const float *row_scale, uint16_t *xb, int ldb, int32_t *zero,
+                         int nzero)
 {
     if (T <= 0) return hipSuccess;
     // xb (optional): the bf16 copy of the rows, written by the staged kernel
@@ -470,7 +489,7 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
         const int kp = (d + 63) / 64 * 64;
         dim3 grid((T * E + 3) / 4);
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
-                           row_scale);
+                           row_scale, zero, nzero);
     } else {
         const int kp = (d + 63) / 64 * 64;
         // two expert tiles per workgroup (each token row read half as
@@ -484,12 +503,12 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
         if (staged && E > 32 && tiles2 >= kRouterStagedWgs) {
             dim3 grid((T + 31) / 32, (E + 63) / 64);
             hipLaunchKernelGGL((router_lds_kernel<2>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
-                               row_scale, xb, ldb);
+                               row_scale, xb, ldb, zero, nzero);
             return hipGetLastError();
         } else if (staged && tiles1 >= kRouterStagedWgs) {
             dim3 grid((T + 31) / 32, (E + 31) / 32);
             hipLaunchKernelGGL((router_lds_kernel<1>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E, logits,
-                               row_scale, xb, ldb);
+                               row_scale, xb, ldb, zero, nzero);
             return hipGetLastError();
         }
         if (hipError_t e = convert_first()) return e;
@@ -497,14 +516,14 @@ hipError_t launch_router(const float *x, int ldx, int T, int d, const float *w, 
             dim3 grid((T + 31) / 32, (E + 63) / 64);
             if (tiles2 * 4 >= kRouterWaves)
                 hipLaunchKernelGGL((router_mfma_kernel<2, 4>), grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E,
-                                   logits, row_scale);
+                                   logits, row_scale, zero, nzero);
             else
                 hipLaunchKernelGGL((router_mfma_kernel<2, 8>), grid, dim3(512), 0, s, x, ldx, T, kp, w, ldw, bias, E,
-                                   logits, row_scale);
+                                   logits, row_scale, zero, nzero);
         } else {
             dim3 grid((T + 31) / 32, (E + 31) / 32);
             hipLaunchKernelGGL((router_mfma_kernel<1, 4>), grid, dim3(256), 0, s, x, ldx, T, kp, w, ldw, bias, E,
-                               logits, row_scale);
+                               logits, row_scale, zero, nzero);
         }
     }
     return hipGetLastError();
@@ -676,9 +695,9 @@ __device__ __forceinline__ void load_balance(const double *__restrict__ balance,
 // Top-k of one token by one wave (EPL experts per lane; bal[j] is the
 // balance bias of expert lane + 64 j, loaded ahead by the caller).  Writes
 // chosen and gates (float64 and fp32) for token t; scr: LDS of the wave, used
-// only when a score is NaN.
+// only when a score is NaN.  Returns, in lane i < k, the expert of slot i.
 template <int EPL>
-__device__ __forceinline__ void topk_token(const double *__restrict__ logit_row, int t, int E, int k,
+__device__ __forceinline__ int topk_token(const double *__restrict__ logit_row, int t, int E, int k,
                                            const double (&bal)[EPL], int lane, int32_t *__restrict__ chosen,
                                            double *__restrict__ gates, float *__restrict__ gates32,
                                            const TopkScratch &scr)
@@ -776,6 +795,7 @@ __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row,
 #pragma unroll
     for (int i = 0; i < kMaxK; ++i)
         if (i < k) total += list_a[i];
+    int mine = -1;
 #pragma unroll
     for (int i = 0; i < kMaxK; ++i) {
         if (i < k && lane == i) {
@@ -783,14 +803,25 @@ __device__ __forceinline__ void topk_token(const double *__restrict__ logit_row,
             chosen[(size_t)t * k + i] = list_e[i];
             gates[(size_t)t * k + i] = g;
             gates32[(size_t)t * k + i] = (float)g;
+            mine = list_e[i];
         }
     }
+    return mine;
 }
 
+// Tokens per chunk of the many-token dispatch, whose counts are per chunk
+// and expert.
+constexpr int kChunk = 128;
+
+// chunk_cnt (optional, [chunks][E], zero on entry): each (token, slot) adds
+// one to its chunk's count of its expert.  The counts do not depend on the
+// order of the adds, so the dispatch built from them is the same as from
+// dispatch_count_kernel.
 template <int EPL>
 __global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ logits, int T, int E, int k,
                                                    const double *__restrict__ balance, int32_t *__restrict__ chosen,
-                                                   double *__restrict__ gates, float *__restrict__ gates32)
+                                                   double *__restrict__ gates, float *__restrict__ gates32,
+                                                   int32_t *__restrict__ chunk_cnt)
 {
     __shared__ double score[4][kMaxExperts];
     __shared__ int cand[4][kMaxExperts];
@@ -800,21 +831,25 @@ __global__ __launch_bounds__(256) void topk_kernel(const double *__restrict__ lo
     if (t >= T) return;  // wave-uniform
     double bal[EPL];
     load_balance<EPL>(balance, E, lane, bal);
-    topk_token<EPL>(logits + (size_t)t * E, t, E, k, bal, lane, chosen, gates, gates32,
-                    TopkScratch{score[wave], cand[wave], stk[wave]});
+    const int mine = topk_token<EPL>(logits + (size_t)t * E, t, E, k, bal, lane, chosen, gates, gates32,
+                                     TopkScratch{score[wave], cand[wave], stk[wave]});
+    if (chunk_cnt != nullptr && lane < k) atomicAdd(chunk_cnt + (size_t)(t / kChunk) * E + mine, 1);
 }
 
 hipError_t launch_topk(const double *logits, int T, int E, int k, const double *balance, int32_t *chosen,
-                       double *gates, float *gates32, hipStream_t s)
+                       double *gates, float *gates32, hipStream_t s, int32_t *chunk_cnt)
 {
     if (T <= 0) return hipSuccess;
     dim3 grid((T + 3) / 4);
     if (E <= 64)
-        hipLaunchKernelGGL(topk_kernel<1>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32);
+        hipLaunchKernelGGL(topk_kernel<1>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32,
+                           chunk_cnt);
     else if (E <= 128)
-        hipLaunchKernelGGL(topk_kernel<2>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32);
+        hipLaunchKernelGGL(topk_kernel<2>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32,
+                           chunk_cnt);
     else
-        hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32);
+        hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(256), 0, s, logits, T, E, k, balance, chosen, gates, gates32,
+                           chunk_cnt);
     return hipGetLastError();
 }
 
@@ -1024,10 +1059,11 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
 //   scan:    one workgroup: per-expert totals, offsets, the group tables, and
 //            every chunk's starting position per expert -> chunk_cnt[c][e]
 //   scatter: per chunk, wave ranks + the chunk's base  -> rows, pos, tok
-// 128 tokens per chunk: twice the workgroups of 256 for a shorter
+// kChunk = 128 tokens per chunk: twice the workgroups of 256 for a shorter
 // per-workgroup chain (C3 dispatch 16.5 → 15.6 µs); every placement
-// workgroup reads all chunks' counts, so the chunks are not made smaller
-constexpr int kChunk = 128;
+// workgroup reads all chunks' counts, so the chunks are not made smaller.
+// The counts come from the top-k when it runs just before (launch_topk with
+// chunk_cnt), else from dispatch_count_kernel.
 
 __global__ __launch_bounds__(kChunk) void dispatch_count_kernel(const int32_t *__restrict__ chosen, int T, int k, int E,
                                                                 int32_t *__restrict__ chunk_cnt)
@@ -1138,18 +1174,19 @@ __global__ __launch_bounds__(1024) void dispatch_place_kernel(const int32_t *__r
 }
 
 int dispatch_chunks(int T) { return (T + kChunk - 1) / kChunk; }
+bool dispatch_chunked(int T) { return T > 1024; }
 
 hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load, int32_t *offsets,
                            int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok, int32_t *tile_off,
-                           int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s)
+                           int4 *tile_desc, int32_t *chunk_cnt, hipStream_t s, bool counted)
 {
-    if (T <= 1024) {  // one workgroup: token-waves x experts over its 16 waves
+    if (!dispatch_chunked(T)) {  // one workgroup: token-waves x experts over its 16 waves
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows,
                            pos, goff, tok, tile_off, tile_desc);
         return hipGetLastError();
     }
     const int chunks = dispatch_chunks(T);
-    hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, chunk_cnt);
+    if (!counted) hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(kChunk), 0, s, chosen, T, k, E, chunk_cnt);
     hipLaunchKernelGGL(dispatch_place_kernel, dim3(chunks), dim3(1024), 0, s, chosen, T, k, E, S, bm, chunks,
                        chunk_cnt, load, offsets, rows, pos, goff, tok, tile_off, tile_desc);
     return hipGetLastError();
