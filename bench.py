@@ -621,7 +621,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
-              f"(the path is measured at one GPU's share; DESIGN.md describes how it would shard)",
+              f"(the path is measured at one GPU's share: a layer's experts, router and shared experts on one "
+              f"device)",
               file=sys.stderr)
         sys.exit(2)
 
