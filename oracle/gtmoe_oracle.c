@@ -4,8 +4,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the parity oracle and the timed CPU
  * baseline.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
- * leg may load it, and only as the checker; the product library never links,
- * calls or falls back to it.
+ * leg may load it, and only to check or time against; the product library
+ * never links, calls or falls back to it.
  *
  * Every function follows the reference in float64 with the reference's loop
  * order.  Build with -ffp-contract=off: the reference's default amd64 build
