@@ -1,6 +1,6 @@
 """ctypes front end of the CPU oracle (oracle/gtmoe_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: the parity checker and the timed CPU baseline.  Only
+TEST INFRASTRUCTURE ONLY: the parity oracle and the timed CPU baseline.  Only
 tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
 module; the product never does.
 

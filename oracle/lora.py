@@ -1,7 +1,7 @@
 """Float64 restatement of a mixture of experts with low-rank adapters on every
 layer, forward and backward, in numpy.
 
-TEST INFRASTRUCTURE ONLY (the parity checker): only tests/ import this
+TEST INFRASTRUCTURE ONLY (the parity oracle): only tests/ import this
 module; the product never does.
 
 Follows, step for step in what it computes:
