@@ -544,6 +544,44 @@ __device__ __forceinline__ bool better(double s1, int e1, double s2, int e2)
     return s1 > s2 || (s1 == s2 && e1 < e2);
 }
 
+// One level of the wave arg-max: this lane's (score, expert) against the one
+// of the lane that the DPP pattern CTRL (a permutation within each row of 16
+// lanes) names.  Every lane of a row takes part, so no lane reads outside it.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(double &bs, int &be)
+{
+    const unsigned long long u = (unsigned long long)__double_as_longlong(bs);
+    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xF, 0xF, false);
+    const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+    const int oe = __builtin_amdgcn_update_dpp(0, be, CTRL, 0xF, 0xF, false);
+    const double os = __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+    if (better(os, oe, bs, be)) {
+        bs = os;
+        be = oe;
+    }
+}
+
+// The best of the four rows' bests (every lane of a row holds its row's),
+// read from lanes 0, 16, 32 and 48: the wave's winner, the same in every lane.
+__device__ __forceinline__ int argmax_rows(double bs, int be)
+{
+    const unsigned long long u = (unsigned long long)__double_as_longlong(bs);
+    double ws = 0.0;
+    int we = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, 16 * r);
+        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), 16 * r);
+        const int re = __builtin_amdgcn_readlane(be, 16 * r);
+        const double rs = __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+        if (r == 0 || better(rs, re, ws, we)) {
+            ws = rs;
+            we = re;
+        }
+    }
+    return we;
+}
+
 // sort.SliceStable(candidates, score descending) of mixtureofexperts.go:106,
 // step for step, for a row with NaN scores: Go's stable sort (package sort:
 // insertion sort of blocks of 20, then SymMerge of neighbouring runs of 20,
@@ -733,14 +771,14 @@ __device__ __forceinline__ int topk_token(const double *__restrict__ logit_row, 
                     be = e;
                 }
             }
-            for (int off = 32; off > 0; off >>= 1) {
-                const double os = __shfl_xor(bs, off);
-                const int oe = __shfl_xor(be, off);
-                if (better(os, oe, bs, be)) {
-                    bs = os;
-                    be = oe;
-                }
-            }
+            // within each row of 16 lanes by DPP moves (pairs, quads, eights,
+            // the row), then across the four rows by lane reads: the same
+            // total order, so the same winner as any other reduction tree
+            argmax_dpp<0xB1>(bs, be);   // quad_perm [1, 0, 3, 2]
+            argmax_dpp<0x4E>(bs, be);   // quad_perm [2, 3, 0, 1]
+            argmax_dpp<0x141>(bs, be);  // row_half_mirror
+            argmax_dpp<0x140>(bs, be);  // row_mirror
+            be = argmax_rows(bs, be);
 #pragma unroll
             for (int j = 0; j < EPL; ++j)
                 if (lane + 64 * j == be) taken[j] = true;
