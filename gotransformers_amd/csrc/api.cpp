@@ -538,6 +538,7 @@ struct Inputs {
     const void *x;
     bool f64;
     bool norm;
+    bool host = false;  // the rows are in pinned host memory: converted once, never read in place
 };
 
 // A stack layer's combine left for the next layer's routing kernel to do.
@@ -564,7 +565,7 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
     // fp32 rows for the router: an fp32 input whose rows are already a
     // multiple of 64 wide is read in place on the bf16 path
     const float *xr = w.xf;
-    if (path == GTMOE_PATH_BF16 && !in.f64 && !in.norm && L->d == L->dp) {
+    if (path == GTMOE_PATH_BF16 && !in.f64 && !in.norm && !in.host && L->d == L->dp) {
         xf = nullptr;
         xr = (const float *)in.x;
     }
@@ -1782,15 +1783,19 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     if (L->has_adapters) return adapter_forward(L, T, inputs, token_ids, outputs);
     Workspace &w = L->ws;
     // The host buffers are bridged by pinned staging that the kernels read
-    // and write across the bus themselves: the CPU copies the rows (and ids)
-    // in and the routing kernel reads them there; the combine writes the
-    // output rows there and one pack kernel the routing state; the call waits
+    // and write across the bus themselves.  The CPU rounds the float64 rows
+    // to fp32 into it (every kernel's first step for float64 rows, so the
+    // results are the same, and half the bytes cross the bus) and copies the
+    // ids; the routing kernel reads the rows there.  The combine, which adds
+    // in fp32, writes the fp32 output rows there and the CPU widens them
+    // (exactly); one pack kernel writes the routing state; the call waits
     // for the device once.  The routing state comes back with the outputs
     // because the reference keeps it (LastExpertLoad, UpdateBalance,
     // Backward) and the Go side reads it after every forward; the dispatch
     // tables, which the few-token kernels did without, are built behind the
     // expert kernels first.
-    const size_t rows_bytes = sizeof(double) * T * L->d;
+    const size_t nvals = (size_t)T * L->d;
+    const size_t rows_bytes = align_up(sizeof(float) * nvals, 64);
     const size_t tk = (size_t)T * L->k;
     const int words[] = {L->E, (int)tk, (int)(2 * tk), (int)tk, L->E + 1};  // load, chosen, gates, rows, offsets
     size_t route_bytes = 0;
@@ -1799,18 +1804,19 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     rc = ensure_stage(L, 2 * rows_bytes + ids_bytes + route_bytes);
     if (rc != GTMOE_OK) return rc;
     const size_t ox = 0, oy = rows_bytes, oid = 2 * rows_bytes, oroute = oid + ids_bytes;
-    memcpy(L->stage + ox, inputs, rows_bytes);
+    float *hx = reinterpret_cast<float *>(L->stage + ox);
+    for (size_t i = 0; i < nvals; ++i) hx[i] = (float)inputs[i];
     const int64_t *ids = nullptr;
     if (L->desc.use_hash_routing) {
         memcpy(L->stage + oid, token_ids, sizeof(int64_t) * T);
         ids = reinterpret_cast<const int64_t *>(L->stage_dev + oid);
     }
-    rc = prepare_and_route(L, T, Inputs{L->stage_dev + ox, true, false}, ids, path, s);
+    rc = prepare_and_route(L, T, Inputs{L->stage_dev + ox, false, false, true}, ids, path, s);
     if (rc == GTMOE_OK) rc = run_experts(L, T, path, s);
     if (rc != GTMOE_OK) return rc;
     RUN(ctx, s, "combine",
         launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos,
-                       w.gates32, nullptr, nullptr, reinterpret_cast<double *>(L->stage_dev + oy), s));
+                       w.gates32, nullptr, reinterpret_cast<float *>(L->stage_dev + oy), nullptr, s));
     if (L->skipped_dispatch)
         RUN(ctx, s, "dispatch",
             launch_dispatch(w.chosen, T, L->k, L->E, L->S, kGemvSlice, w.load, w.offsets, w.rows, w.pos, w.goff,
@@ -1824,7 +1830,8 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     pp.n = 5;
     RUN(ctx, s, "pack_routing", launch_pack_words(pp, reinterpret_cast<uint32_t *>(L->stage_dev + oroute), s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
-    memcpy(outputs, L->stage + oy, rows_bytes);
+    const float *hy = reinterpret_cast<const float *>(L->stage + oy);
+    for (size_t i = 0; i < nvals; ++i) outputs[i] = (double)hy[i];
     mark_forward(L, T, path, s);
     L->skipped_dispatch = false;
     L->dispatch_pending = false;
