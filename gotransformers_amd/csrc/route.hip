@@ -1288,9 +1288,65 @@ __device__ __forceinline__ float4 in4(const double *row, int i)
 // (s_waitcnt vmcnt(0)).  A release/acquire pair would give the same ordering
 // through a whole-L2 write-back per workgroup and an L2 invalidation per
 // token; measured, that cost more than the split saved.
+//
+// The grid's workgroups past the T * P routing ones (router routing only)
+// warm the L2 of their XCD with the router rows its routing workgroups will
+// read, while those are still loading and combining the token rows: a
+// stack's layer reads its router once per step, and the expert weights
+// streamed in between leave none of it in any L2.  The dispatcher deals a
+// 1-D grid's workgroups to the 8 XCDs in turn, so workgroup b runs on XCD
+// b % 8, and with P dividing 8 the routing workgroups there are all of part
+// (b % 8) % P; otherwise every XCD warms all E rows.  Warming workgroup
+// 8 j + x of the nw = 8 Q takes slice j of Q of its XCD's rows, one 16-byte
+// load per lane per 16 KiB, and keeps nothing.
+__device__ __forceinline__ void warm_router(const FusedArgs &a)
+{
+    const int P = a.parts;
+    const int nroute = a.T * P;
+    const int i = blockIdx.x - nroute, nq = (gridDim.x - nroute) / 8;
+    const int xcd = blockIdx.x & 7;
+    int r0 = 0, r1 = a.E;
+    if (8 % P == 0) {
+        const int epp = (a.E + P - 1) / P;
+        r0 = min(a.E, (xcd % P) * epp);
+        r1 = min(a.E, r0 + epp);
+    }
+    const size_t n16 = (size_t)(r1 - r0) * a.kp / 4;  // 16-byte units of those rows
+    const uint4 *base = reinterpret_cast<const uint4 *>(a.w + (size_t)r0 * a.kp);
+    const int j = i / 8;
+    const size_t b0 = n16 * j / nq, b1 = n16 * (j + 1) / nq;
+    uint32_t acc = 0;
+    for (size_t u0 = b0; u0 < b1; u0 += 4096) {
+        uint4 v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const size_t u = u0 + threadIdx.x + 1024 * r;
+            v[r] = u < b1 ? base[u] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc ^= v[r].x ^ v[r].y ^ v[r].z ^ v[r].w;
+    }
+    asm volatile("" ::"v"(acc));  // the loads are kept, and waited for before the wave ends
+}
+
+// Warming workgroups for a router routing launch whose routing workgroups
+// fit the GPU at once (a later round would find the rows warm anyway): 8 per
+// 16 KiB of the rows one XCD reads, at most 16 per XCD.
+static int route_warm_blocks(int T, int E, int kp, int parts, bool hash)
+{
+    if (hash || T * parts > 256) return 0;
+    const int rows = 8 % parts == 0 ? (E + parts - 1) / parts : E;
+    const long long n16 = (long long)rows * kp / 4;
+    return 8 * (int)std::min<long long>(16, std::max<long long>(1, (n16 + 1023) / 1024));
+}
+
 template <typename InT, bool NORM, bool HASH, int EPL, int NX>
 __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
+    if (!HASH && (int)blockIdx.x >= a.T * a.parts) {
+        warm_router(a);
+        return;
+    }
     __shared__ double lg[kMaxExperts];
     __shared__ int cand[kMaxExperts];  // the top-k's candidate list and merge stack (NaN rows)
     __shared__ int stk[3 * kSortStack];
@@ -1496,7 +1552,7 @@ int route_fused_parts(int T, int E, bool hash)
 template <typename InT, bool NORM, int NX>
 static hipError_t launch_token_nx(const FusedArgs &a, bool hash, hipStream_t s)
 {
-    dim3 grid(a.T * a.parts);
+    dim3 grid(a.T * a.parts + route_warm_blocks(a.T, a.E, a.kp, a.parts, hash));
     if (hash) hipLaunchKernelGGL((route_token_kernel<InT, NORM, true, 1, NX>), grid, dim3(1024), 0, s, a);
     else if (a.E <= 64) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 1, NX>), grid, dim3(1024), 0, s, a);
     else if (a.E <= 128) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 2, NX>), grid, dim3(1024), 0, s, a);
