@@ -809,9 +809,10 @@ __device__ __forceinline__ int topk_token(const double *__restrict__ logit_row, 
                 if (lane + 64 * j == ce) taken[j] = true;
         }
     }
-    // chosen experts in ascending order, with their affinities
-    int list_e[kMaxK];
-    double list_a[kMaxK];
+    // chosen experts in ascending order, with their affinities (read from
+    // the owning lane: b is the same in every lane)
+    int list_e[kMaxK] = {};
+    double list_a[kMaxK] = {};
     int n = 0;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
@@ -819,7 +820,10 @@ __device__ __forceinline__ int topk_token(const double *__restrict__ logit_row, 
         while (m) {
             const int b = __builtin_ctzll(m);
             m &= m - 1;
-            const double av = __shfl(a[j], b);
+            const unsigned long long u = (unsigned long long)__double_as_longlong(a[j]);
+            const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, b);
+            const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), b);
+            const double av = __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
 #pragma unroll
             for (int i = 0; i < kMaxK; ++i)
                 if (i == n) {
@@ -833,16 +837,22 @@ __device__ __forceinline__ int topk_token(const double *__restrict__ logit_row, 
 #pragma unroll
     for (int i = 0; i < kMaxK; ++i)
         if (i < k) total += list_a[i];
+    // lane i < k takes slot i; the k divisions run side by side
     int mine = -1;
+    double my_a = 0.0;
 #pragma unroll
-    for (int i = 0; i < kMaxK; ++i) {
-        if (i < k && lane == i) {
-            const double g = list_a[i] / total;
-            chosen[(size_t)t * k + i] = list_e[i];
-            gates[(size_t)t * k + i] = g;
-            gates32[(size_t)t * k + i] = (float)g;
+    for (int i = 0; i < kMaxK; ++i)
+        if (lane == i) {
             mine = list_e[i];
+            my_a = list_a[i];
         }
+    if (lane < k) {
+        const double g = my_a / total;
+        chosen[(size_t)t * k + lane] = mine;
+        gates[(size_t)t * k + lane] = g;
+        gates32[(size_t)t * k + lane] = (float)g;
+    } else {
+        mine = -1;
     }
     return mine;
 }
@@ -1359,44 +1369,14 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     const InT *xr = reinterpret_cast<const InT *>(a.x) + (size_t)t * a.d;
     const bool vec = (a.d & 3) == 0;
 
-    if constexpr (sizeof(InT) == 4) {
-        if (a.pend_slot) {  // the previous layer's combine (combine_kernel's arithmetic)
-            const float *xin_row = reinterpret_cast<const float *>(xr);
-            float *x = a.x_out ? a.x_out + (size_t)t * a.d : const_cast<float *>(xin_row);
-            // the routed rows and gates of this token (at most 8; slots past
-            // pend_k re-read slot 0 and are not added), all requested before
-            // the adds, which keep the reference's order
-            const float *row[8];
-            float g[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int ii = i < a.pend_k ? i : 0;
-                const int q = a.pend_pos ? a.pend_pos[(size_t)t * a.pend_k + ii] : t * a.pend_k + ii;
-                row[i] = a.pend_slot + (size_t)(a.pend_S * a.T + q) * a.d;
-                g[i] = a.pend_gates[(size_t)t * a.pend_k + ii];
-            }
-            for (int c = threadIdx.x; c < a.d; c += 1024) {
-                float v8[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v8[i] = row[i][c];
-                const float xc = xin_row[c];
-                float acc = 0.f;
-                for (int s = 0; s < a.pend_S; ++s) acc += a.pend_slot[((size_t)s * a.T + t) * a.d + c];
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    if (i < a.pend_k) acc = fmaf(g[i], v8[i], acc);
-                const float v = xc + acc;
-                if (part == 0) x[c] = v;
-                comb[c] = v;
-            }
-            __syncthreads();
-            xr = reinterpret_cast<const InT *>(comb);  // this token's row, from LDS from here on
-        }
-    }
-
-    // router bias of expert wave + 16 j in lane j; balance biases (wave 0)
-    double bias_l = 0.0;
-    double bal[EPL];
+    // Each phase below issues all of its loads before it uses any of them, so
+    // that a wave waits for one round trip per phase: addresses are clamped
+    // into the row (never a branch around a load) and what lies past the row
+    // is masked after the load.
+    // the small operands (router and balance biases, norm weights), requested
+    // first: the combine or the row's loads cover their latency
+    double bias_l = 0.0;  // router bias of expert wave + 16 j in lane j
+    double bal[EPL];      // balance biases (wave 0)
     if (!HASH) {
         if (eb + wave + 16 * lane < ee) bias_l = a.bias[eb + wave + 16 * lane];
         if (wave == 0) load_balance<EPL>(a.balance, a.E, lane, bal);
@@ -1405,26 +1385,137 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     if (NORM && vec && wave < NX && 4 * lane + 256 * wave < a.d)
         nv = *reinterpret_cast<const float4 *>(a.norm + 4 * lane + 256 * wave);
 
-    float4 xv[NX];
-    float ss = 0.f;
+    bool from_comb = false;  // the token's row is in comb (LDS)
+    if constexpr (sizeof(InT) == 4) {
+        if (a.pend_slot) {  // the previous layer's combine (combine_kernel's arithmetic)
+            const float *xin_row = reinterpret_cast<const float *>(xr);
+            float *x = a.x_out ? a.x_out + (size_t)t * a.d : const_cast<float *>(xin_row);
+            // the routed rows and gates of this token (at most 8; slots past
+            // pend_k re-read slot 0 and are not added), all requested before
+            // the adds, which keep the reference's order.  Without a pos
+            // table the rows' addresses need no load, and the gates are
+            // requested after the rows.
+            const float *row[8];
+            if (a.pend_pos) {
 #pragma unroll
-    for (int j = 0; j < NX; ++j) {
-        const int i = 4 * lane + 256 * j;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (vec) {
-            if (i < a.d) v = in4(xr, i);
-        } else {
+                for (int i = 0; i < 8; ++i) {
+                    const int q = a.pend_pos[(size_t)t * a.pend_k + (i < a.pend_k ? i : 0)];
+                    row[i] = a.pend_slot + (size_t)(a.pend_S * a.T + q) * a.d;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    row[i] = a.pend_slot + (size_t)(a.pend_S * a.T + t * a.pend_k + (i < a.pend_k ? i : 0)) * a.d;
+            }
+            float g[8];
+            auto load_gates = [&]() {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) g[i] = a.pend_gates[(size_t)t * a.pend_k + (i < a.pend_k ? i : 0)];
+            };
+            // the first four shared experts' rows (past pend_S: shared row 0,
+            // or with no shared experts a routed row, not added)
+            const float *srow[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) srow[s] = a.pend_slot + ((size_t)(s < a.pend_S ? s : 0) * a.T + t) * a.d;
+            if (vec) {  // four values per lane (d <= 4096)
+                const int c = 4 * (int)threadIdx.x;
+                if (c < a.d) {
+                    float4 v8[8], sh[4];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v8[i] = *reinterpret_cast<const float4 *>(row[i] + c);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) sh[s] = *reinterpret_cast<const float4 *>(srow[s] + c);
+                    const float4 xc = *reinterpret_cast<const float4 *>(xin_row + c);
+                    load_gates();
+                    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        if (s < a.pend_S) {
+                            acc.x += sh[s].x;
+                            acc.y += sh[s].y;
+                            acc.z += sh[s].z;
+                            acc.w += sh[s].w;
+                        }
+                    for (int s = 4; s < a.pend_S; ++s) {
+                        const float4 u = *reinterpret_cast<const float4 *>(a.pend_slot + ((size_t)s * a.T + t) * a.d + c);
+                        acc.x += u.x;
+                        acc.y += u.y;
+                        acc.z += u.z;
+                        acc.w += u.w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (i < a.pend_k) {
+                            acc.x = fmaf(g[i], v8[i].x, acc.x);
+                            acc.y = fmaf(g[i], v8[i].y, acc.y);
+                            acc.z = fmaf(g[i], v8[i].z, acc.z);
+                            acc.w = fmaf(g[i], v8[i].w, acc.w);
+                        }
+                    const float4 v = make_float4(xc.x + acc.x, xc.y + acc.y, xc.z + acc.z, xc.w + acc.w);
+                    if (part == 0) *reinterpret_cast<float4 *>(x + c) = v;
+                    *reinterpret_cast<float4 *>(comb + c) = v;
+                }
+            } else {
+                load_gates();
+                for (int c = threadIdx.x; c < a.d; c += 1024) {
+                    float v8[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v8[i] = row[i][c];
+                    const float xc = xin_row[c];
+                    float acc = 0.f;
+                    for (int s = 0; s < a.pend_S; ++s) acc += a.pend_slot[((size_t)s * a.T + t) * a.d + c];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (i < a.pend_k) acc = fmaf(g[i], v8[i], acc);
+                    const float v = xc + acc;
+                    if (part == 0) x[c] = v;
+                    comb[c] = v;
+                }
+            }
+            __syncthreads();
+            from_comb = true;
+        }
+    }
+
+    // the row, zero past d
+    float4 xv[NX];
+    if (from_comb) {
+#pragma unroll
+        for (int j = 0; j < NX; ++j) xv[j] = *reinterpret_cast<const float4 *>(comb + 4 * lane + 256 * j);
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            const int i = 4 * lane + 256 * j;
+            if (i >= a.d) xv[j].x = 0.f;
+            if (i + 1 >= a.d) xv[j].y = 0.f;
+            if (i + 2 >= a.d) xv[j].z = 0.f;
+            if (i + 3 >= a.d) xv[j].w = 0.f;
+        }
+    } else if (vec) {
+#pragma unroll
+        for (int j = 0; j < NX; ++j) xv[j] = in4(xr, min(4 * lane + 256 * j, a.d - 4));
+#pragma unroll
+        for (int j = 0; j < NX; ++j)
+            if (4 * lane + 256 * j >= a.d) xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            const int i = 4 * lane + 256 * j;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < a.d) v.x = in_at(xr, i);
             if (i + 1 < a.d) v.y = in_at(xr, i + 1);
             if (i + 2 < a.d) v.z = in_at(xr, i + 2);
             if (i + 3 < a.d) v.w = in_at(xr, i + 3);
+            xv[j] = v;
         }
-        xv[j] = v;
-        if (NORM) {
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
+    }
+    float ss = 0.f;
+    if (NORM) {
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            ss = fmaf(xv[j].x, xv[j].x, ss);
+            ss = fmaf(xv[j].y, xv[j].y, ss);
+            ss = fmaf(xv[j].z, xv[j].z, ss);
+            ss = fmaf(xv[j].w, xv[j].w, ss);
         }
     }
     float inv = 1.0f;
@@ -1433,6 +1524,46 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
         inv = 1.0f / sqrtf(ss / (float)a.d + 1e-6f);
     }
 
+    // prepared row (part 0); up to d = 2048 it is written before the
+    // products, so that the norm weights need no register across them
+    auto write_prepared = [&]() {
+        if (part != 0) {
+        } else if (vec) {
+#pragma unroll
+            for (int j = 0; j < NX; ++j) {
+                const int i = 4 * lane + 256 * j;
+                if (j == wave && i < a.kp) {  // i < d, or padding (xv holds zeros there)
+                    float4 v = xv[j];
+                    if (NORM) {
+                        v.x = v.x * inv * nv.x;
+                        v.y = v.y * inv * nv.y;
+                        v.z = v.z * inv * nv.z;
+                        v.w = v.w * inv * nv.w;
+                        if (i >= a.d) v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+                    if (a.xf) *reinterpret_cast<float4 *>(a.xf + (size_t)t * a.kp + i) = v;
+                    if (a.xb) {
+                        const uint2 b = make_uint2((uint32_t)bf16_bits(v.x) | ((uint32_t)bf16_bits(v.y) << 16),
+                                                   (uint32_t)bf16_bits(v.z) | ((uint32_t)bf16_bits(v.w) << 16));
+                        *reinterpret_cast<uint2 *>(a.xb + (size_t)t * a.kp + i) = b;
+                    }
+                }
+            }
+        } else {
+            for (int i = threadIdx.x; i < a.kp; i += 1024) {
+                float v = 0.f;
+                if (i < a.d) {
+                    v = from_comb ? comb[i] : in_at(xr, i);
+                    if (NORM) v = v * inv * a.norm[i];
+                }
+                if (a.xf) a.xf[(size_t)t * a.kp + i] = v;
+                if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
+            }
+        }
+        if (a.zero_out && part == 0)
+            for (int i = threadIdx.x; i < a.d; i += 1024) a.zero_out[(size_t)t * a.d + i] = 0.f;
+    };
+    if constexpr (NX <= 8) write_prepared();
     if (!HASH) {
         for (int e0 = eb + wave; e0 < ee; e0 += 32) {
             const int e1 = e0 + 16;
@@ -1440,21 +1571,33 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
             const float *w0 = a.w + (size_t)e0 * a.kp;
             const float *w1 = a.w + (size_t)(two ? e1 : e0) * a.kp;
             float d0 = 0.f, d1 = 0.f;
+            // a group of runs of both rows in flight (64 registers up to d = 2048,
+            // 16 above, where the row itself holds 64), then their products
+            constexpr int G = NX <= 8 ? NX : 2;
 #pragma unroll
-            for (int j = 0; j < NX; ++j) {
-                const int i = 4 * lane + 256 * j;
-                if (i < a.kp) {
-                    const float4 p = *reinterpret_cast<const float4 *>(w0 + i);
-                    const float4 q = *reinterpret_cast<const float4 *>(w1 + i);
-                    d0 = fmaf(xv[j].x, p.x, d0);
-                    d0 = fmaf(xv[j].y, p.y, d0);
-                    d0 = fmaf(xv[j].z, p.z, d0);
-                    d0 = fmaf(xv[j].w, p.w, d0);
-                    d1 = fmaf(xv[j].x, q.x, d1);
-                    d1 = fmaf(xv[j].y, q.y, d1);
-                    d1 = fmaf(xv[j].z, q.z, d1);
-                    d1 = fmaf(xv[j].w, q.w, d1);
+            for (int jb = 0; jb < NX; jb += G) {
+                float4 p[G], q[G];
+#pragma unroll
+                for (int j = 0; j < G; ++j) {
+                    const int ic = min(4 * lane + 256 * (jb + j), a.kp - 4);
+                    p[j] = *reinterpret_cast<const float4 *>(w0 + ic);
+                    q[j] = *reinterpret_cast<const float4 *>(w1 + ic);
                 }
+#pragma unroll
+                for (int j = 0; j < G; ++j) {
+                    if (4 * lane + 256 * (jb + j) < a.kp) {
+                        const float4 x4 = xv[jb + j];
+                        d0 = fmaf(x4.x, p[j].x, d0);
+                        d0 = fmaf(x4.y, p[j].y, d0);
+                        d0 = fmaf(x4.z, p[j].z, d0);
+                        d0 = fmaf(x4.w, p[j].w, d0);
+                        d1 = fmaf(x4.x, q[j].x, d1);
+                        d1 = fmaf(x4.y, q[j].y, d1);
+                        d1 = fmaf(x4.z, q[j].z, d1);
+                        d1 = fmaf(x4.w, q[j].w, d1);
+                    }
+                }
+                if constexpr (G < NX) __builtin_amdgcn_sched_barrier(0);  // one group in flight at a time
             }
             for (int off = 32; off > 0; off >>= 1) {
                 d0 += __shfl_xor(d0, off);
@@ -1469,42 +1612,7 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
             }
         }
     }
-    // prepared row (part 0)
-    if (part != 0) {
-    } else if (vec) {
-#pragma unroll
-        for (int j = 0; j < NX; ++j) {
-            const int i = 4 * lane + 256 * j;
-            if (j == wave && i < a.kp) {  // i < d, or padding (xv holds zeros there)
-                float4 v = xv[j];
-                if (NORM) {
-                    v.x = v.x * inv * nv.x;
-                    v.y = v.y * inv * nv.y;
-                    v.z = v.z * inv * nv.z;
-                    v.w = v.w * inv * nv.w;
-                    if (i >= a.d) v = make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-                if (a.xf) *reinterpret_cast<float4 *>(a.xf + (size_t)t * a.kp + i) = v;
-                if (a.xb) {
-                    const uint2 b = make_uint2((uint32_t)bf16_bits(v.x) | ((uint32_t)bf16_bits(v.y) << 16),
-                                               (uint32_t)bf16_bits(v.z) | ((uint32_t)bf16_bits(v.w) << 16));
-                    *reinterpret_cast<uint2 *>(a.xb + (size_t)t * a.kp + i) = b;
-                }
-            }
-        }
-    } else {
-        for (int i = threadIdx.x; i < a.kp; i += 1024) {
-            float v = 0.f;
-            if (i < a.d) {
-                v = in_at(xr, i);
-                if (NORM) v = v * inv * a.norm[i];
-            }
-            if (a.xf) a.xf[(size_t)t * a.kp + i] = v;
-            if (a.xb) a.xb[(size_t)t * a.kp + i] = bf16_bits(v);
-        }
-    }
-    if (a.zero_out && part == 0)
-        for (int i = threadIdx.x; i < a.d; i += 1024) a.zero_out[(size_t)t * a.d + i] = 0.f;
+    if constexpr (NX > 8) write_prepared();
     __syncthreads();
     if (wave != 0) return;
     if (HASH) {
