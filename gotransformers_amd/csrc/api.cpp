@@ -1817,10 +1817,6 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     RUN(ctx, s, "combine",
         launch_combine(T, L->d, L->S, L->k, w.slot_out, path == GTMOE_PATH_BF16, L->skipped_dispatch ? nullptr : w.pos,
                        w.gates32, nullptr, reinterpret_cast<float *>(L->stage_dev + oy), nullptr, s));
-    if (L->skipped_dispatch)
-        RUN(ctx, s, "dispatch",
-            launch_dispatch(w.chosen, T, L->k, L->E, L->S, kGemvSlice, w.load, w.offsets, w.rows, w.pos, w.goff,
-                            w.tok, w.tile_off, w.tile_desc, w.chunk_cnt, s));
     PackParts pp{};
     const void *srcs[] = {w.load, w.chosen, w.gates, w.rows, w.offsets};
     for (int i = 0; i < 5; ++i) {
@@ -1828,7 +1824,18 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
         pp.words[i] = words[i];
     }
     pp.n = 5;
-    RUN(ctx, s, "pack_routing", launch_pack_words(pp, reinterpret_cast<uint32_t *>(L->stage_dev + oroute), s));
+    uint32_t *route_dst = reinterpret_cast<uint32_t *>(L->stage_dev + oroute);
+    if (L->skipped_dispatch && !dispatch_chunked(T))  // the dispatch packs the state in the same launch
+        RUN(ctx, s, "dispatch",
+            launch_dispatch_packed(w.chosen, T, L->k, L->E, L->S, kGemvSlice, w.load, w.offsets, w.rows, w.pos,
+                                   w.goff, w.tok, w.tile_off, w.tile_desc, pp, route_dst, s));
+    else {
+        if (L->skipped_dispatch)
+            RUN(ctx, s, "dispatch",
+                launch_dispatch(w.chosen, T, L->k, L->E, L->S, kGemvSlice, w.load, w.offsets, w.rows, w.pos, w.goff,
+                                w.tok, w.tile_off, w.tile_desc, w.chunk_cnt, s));
+        RUN(ctx, s, "pack_routing", launch_pack_words(pp, route_dst, s));
+    }
     HIP_TRY(ctx, hipStreamSynchronize(s));
     const float *hy = reinterpret_cast<const float *>(L->stage + oy);
     for (size_t i = 0; i < nvals; ++i) outputs[i] = (double)hy[i];

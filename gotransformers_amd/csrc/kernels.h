@@ -139,6 +139,12 @@ struct PackParts {
     int n;
 };
 hipError_t launch_pack_words(const PackParts &p, uint32_t *dst, hipStream_t s);
+// The one-workgroup dispatch (T <= 1024) followed, in the same launch, by the
+// gathering of p into dst that launch_pack_words does.
+hipError_t launch_dispatch_packed(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
+                                  int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
+                                  int32_t *tile_off, int4 *tile_desc, const PackParts &p, uint32_t *dst,
+                                  hipStream_t s);
 hipError_t launch_f32_to_f64(const float *x, double *y, long long n, hipStream_t s);
 
 // Adapter path (lora.hip, route.hip).

@@ -1092,14 +1092,27 @@ __device__ void dispatch_block(const int32_t *chosen, int T, int k, int E, int S
     }
 }
 
+// With pack.n > 0 the same workgroup then gathers pack's parts into
+// pack_dst as pack_words_kernel does (the routing state of a host-API
+// forward), one launch fewer.
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ chosen, int T, int k, int E, int S,
                                                         int bm, int32_t *__restrict__ load, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ rows, int32_t *__restrict__ pos,
                                                         int32_t *__restrict__ goff, int32_t *__restrict__ tok,
-                                                        int32_t *__restrict__ tile_off, int4 *__restrict__ tile_desc)
+                                                        int32_t *__restrict__ tile_off, int4 *__restrict__ tile_desc,
+                                                        PackParts pack, uint32_t *__restrict__ pack_dst)
 {
     __shared__ DispatchShared sh;
     dispatch_block(chosen, T, k, E, S, bm, load, offsets, rows, pos, goff, tok, tile_off, tile_desc, sh);
+    if (pack.n <= 0) return;
+    __syncthreads();  // the tables this workgroup wrote are visible to all of it
+    uint32_t *out = pack_dst;
+    for (int i = 0; i < PackParts::kMax; ++i) {
+        if (i >= pack.n) break;
+        const uint32_t *src = pack.src[i];
+        for (int j = threadIdx.x; j < pack.words[i]; j += 1024) out[j] = src[j];
+        out += (pack.words[i] + 15) / 16 * 16;
+    }
 }
 
 // Many tokens: chunks of kChunk tokens per workgroup.
@@ -1221,6 +1234,17 @@ __global__ __launch_bounds__(1024) void dispatch_place_kernel(const int32_t *__r
     }
 }
 
+hipError_t launch_dispatch_packed(const int32_t *chosen, int T, int k, int E, int S, int bm, int32_t *load,
+                                  int32_t *offsets, int32_t *rows, int32_t *pos, int32_t *goff, int32_t *tok,
+                                  int32_t *tile_off, int4 *tile_desc, const PackParts &pack, uint32_t *dst,
+                                  hipStream_t s)
+{
+    if (T > 1024 || pack.n < 1 || pack.n > PackParts::kMax) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows, pos,
+                       goff, tok, tile_off, tile_desc, pack, dst);
+    return hipGetLastError();
+}
+
 int dispatch_chunks(int T) { return (T + kChunk - 1) / kChunk; }
 bool dispatch_chunked(int T) { return T > 1024; }
 
@@ -1230,7 +1254,7 @@ hipError_t launch_dispatch(const int32_t *chosen, int T, int k, int E, int S, in
 {
     if (!dispatch_chunked(T)) {  // one workgroup: token-waves x experts over its 16 waves
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, chosen, T, k, E, S, bm, load, offsets, rows,
-                           pos, goff, tok, tile_off, tile_desc);
+                           pos, goff, tok, tile_off, tile_desc, PackParts{}, nullptr);
         return hipGetLastError();
     }
     const int chunks = dispatch_chunks(T);
@@ -1690,7 +1714,7 @@ hipError_t launch_route_fused(const FusedArgs &a, bool input_f64, bool hash, boo
     else e = a.norm ? launch_token_typed<float, true>(a, hash, s) : launch_token_typed<float, false>(a, hash, s);
     if (e != hipSuccess || !dispatch) return e;
     hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a.chosen, a.T, a.k, a.E, a.S, a.bm, a.load,
-                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off, a.tile_desc);
+                       a.offsets, a.rows, a.pos, a.goff, a.tok, a.tile_off, a.tile_desc, PackParts{}, nullptr);
     return hipGetLastError();
 }
 
