@@ -1788,7 +1788,8 @@ int32_t gtmoe_forward(gtmoe_layer *L, int32_t tokens, const double *inputs, cons
     // results are the same, and half the bytes cross the bus) and copies the
     // ids; the routing kernel reads the rows there.  The combine, which adds
     // in fp32, writes the fp32 output rows there and the CPU widens them
-    // (exactly); one pack kernel writes the routing state; the call waits
+    // (exactly); the routing state is gathered there by the one-workgroup
+    // dispatch when that runs here, else by a pack kernel; the call waits
     // for the device once.  The routing state comes back with the outputs
     // because the reference keeps it (LastExpertLoad, UpdateBalance,
     // Backward) and the Go side reads it after every forward; the dispatch
