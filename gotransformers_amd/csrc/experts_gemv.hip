@@ -668,8 +668,11 @@ __global__ __launch_bounds__(256) void gemv_few_kernel(GemvArgs a)
     const int in_row = GATEUP ? t : y;
     const int out_row = y;
     const float4 *xin = reinterpret_cast<const float4 *>(a.in + (size_t)in_row * a.ld_in);
-    // K <= 4096: at most four float4 per thread, loaded unconditionally (the
-    // index clamped; the extra copies are not stored) so they stay in registers
+    // K <= 4096: four float4 per thread, loaded unconditionally (the index
+    // clamped) and stored unconditionally into a 16 KiB row buffer (the
+    // copies past K are never read): with a store under a branch the
+    // compiler moved each load into the branch, behind the weight loads and
+    // with a wait of its own
     float4 xv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) xv[i] = xin[min(tid + 256 * i, K / 4 - 1)];
@@ -743,8 +746,7 @@ __global__ __launch_bounds__(256) void gemv_few_kernel(GemvArgs a)
     load_units(0);
     // the input row into LDS (K fp32 values, K a multiple of 64)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (tid + 256 * i < K / 4) reinterpret_cast<float4 *>(xs)[tid + 256 * i] = xv[i];
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float4 *>(xs)[tid + 256 * i] = xv[i];
     __syncthreads();
     for (int j0 = 0;;) {
 #pragma unroll
@@ -910,11 +912,13 @@ hipError_t launch_prec(const GemvArgs &a, int max_slices, hipStream_t s)
 // slice of up to 8 tokens, and measured faster up to 6 tokens (C2 and a C5
 // block; about even at 8).
 constexpr int kFewTokens = 6;
+// LDS of the few-token kernel: its row buffer, four float4 per thread
+constexpr size_t kFewRowBytes = 4 * 256 * sizeof(float4);
 
 template <bool GATEUP, int PREC, int R>
 hipError_t launch_few(const GemvArgs &a, hipStream_t s)
 {
-    const size_t lds = (size_t)a.nblocks * 16 * sizeof(float);  // the token row; >= the reduction's 4 x 2 x R
+    const size_t lds = kFewRowBytes;  // the token row (K <= 4096 values); >= the reduction's 4 x 2 x R floats
     const dim3 grid((a.rows + R - 1) / R, a.S + a.k, a.T);
     hipLaunchKernelGGL((gemv_few_kernel<PREC, GATEUP, R>), grid, dim3(256), lds, s, a);
     return hipGetLastError();
