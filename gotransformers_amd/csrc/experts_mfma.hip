@@ -244,12 +244,20 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
         const_cast<uint16_t *>(a.a), 0, (int)(a.a_rows * a.lda * 2), kRawBufferWord3);
     // (R / 2) % 8 == (4 (w % 2) + l / 16) for this lane's rows R
     const int arow = lane >> 3, achunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
+    // gate/up gathers rows by token: the MI token numbers are loaded together,
+    // the position clamped into the tile (a load under the r < M condition
+    // made the compiler wait for each before issuing the next)
     uint32_t aoff[MI];
+    int arow_src[MI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
         const int r = 32 * i + 8 * wave + arow;
-        aoff[i] = r < M ? ((uint32_t)(GATEUP ? a.tok[p0 + r] : p0 + r) * (uint32_t)a.lda + achunk * 8) * 2u
-                        : 0x80000000u;
+        arow_src[i] = GATEUP ? a.tok[p0 + min(r, M - 1)] : p0 + r;
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        const int r = 32 * i + 8 * wave + arow;
+        aoff[i] = r < M ? ((uint32_t)arow_src[i] * (uint32_t)a.lda + achunk * 8) * 2u : 0x80000000u;
     }
 
     // weights: the wave's two column tiles (gate/up: the same 32 neurons of
