@@ -246,7 +246,8 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     const int arow = lane >> 3, achunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
     // gate/up gathers rows by token: the MI token numbers are loaded together,
     // the position clamped into the tile (a load under the r < M condition
-    // made the compiler wait for each before issuing the next)
+    // made the compiler wait for each before issuing the next); the row
+    // offsets are formed in the prologue, after the first weight loads
     uint32_t aoff[MI];
     int arow_src[MI];
 #pragma unroll
@@ -254,11 +255,13 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
         const int r = 32 * i + 8 * wave + arow;
         arow_src[i] = GATEUP ? a.tok[p0 + min(r, M - 1)] : p0 + r;
     }
+    auto form_aoff = [&]() {
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-        const int r = 32 * i + 8 * wave + arow;
-        aoff[i] = r < M ? ((uint32_t)arow_src[i] * (uint32_t)a.lda + achunk * 8) * 2u : 0x80000000u;
-    }
+        for (int i = 0; i < MI; ++i) {
+            const int r = 32 * i + 8 * wave + arow;
+            aoff[i] = r < M ? ((uint32_t)arow_src[i] * (uint32_t)a.lda + achunk * 8) * 2u : 0x80000000u;
+        }
+    };
 
     // weights: the wave's two column tiles (gate/up: the same 32 neurons of
     // gate and up; down: 64 consecutive rows), a group's matrices as buffer
@@ -441,6 +444,7 @@ __device__ __forceinline__ void gemm_tile(const MfmaArgs &a, char *b0, char *b1,
     // stages the weights of step 2, with two those of step 1)
     load_b(bq[0], 0);
     __builtin_amdgcn_sched_barrier(0);
+    form_aoff();
     dma_a(b0, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (NS == 3) {
