@@ -582,6 +582,36 @@ __device__ __forceinline__ int argmax_rows(double bs, int be)
     return we;
 }
 
+// Sum of a float over the wave, the same in every lane: DPP moves add
+// within each row of 16 lanes (pairs, quads, eights, the row), then the four
+// rows' sums are read from lanes 0, 16, 32 and 48 and added in a fixed order.
+template <int CTRL>
+__device__ __forceinline__ float add_dpp(float v)
+{
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// A double of lane l (l the same in every lane), read without LDS.
+__device__ __forceinline__ double lane_double(double v, int l)
+{
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = add_dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v = add_dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v = add_dpp<0x141>(v);  // row_half_mirror
+    v = add_dpp<0x140>(v);  // row_mirror
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // sort.SliceStable(candidates, score descending) of mixtureofexperts.go:106,
 // step for step, for a row with NaN scores: Go's stable sort (package sort:
 // insertion sort of blocks of 20, then SymMerge of neighbouring runs of 20,
@@ -1544,7 +1574,7 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
     }
     float inv = 1.0f;
     if (NORM) {
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        ss = wave_sum(ss);
         inv = 1.0f / sqrtf(ss / (float)a.d + 1e-6f);
     }
 
@@ -1623,13 +1653,11 @@ __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
                 }
                 if constexpr (G < NX) __builtin_amdgcn_sched_barrier(0);  // one group in flight at a time
             }
-            for (int off = 32; off > 0; off >>= 1) {
-                d0 += __shfl_xor(d0, off);
-                d1 += __shfl_xor(d1, off);
-            }
+            d0 = wave_sum(d0);
+            d1 = wave_sum(d1);
             // e0 = eb + wave + 16 (2 it), e1 = e0 + 16: lanes 2 it and 2 it + 1
             const int j0 = (e0 - eb - wave) / 16;
-            const double b0 = __shfl(bias_l, j0), b1 = __shfl(bias_l, j0 + 1);
+            const double b0 = lane_double(bias_l, j0), b1 = lane_double(bias_l, j0 + 1);
             if (lane == 0) {
                 lg[e0] = (double)(d0 * inv) + b0;
                 if (two) lg[e1] = (double)(d1 * inv) + b1;
