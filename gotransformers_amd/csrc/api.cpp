@@ -33,6 +33,10 @@ constexpr int kMaxGemvK = 4096;
 // AUTO takes the dequant-GEMV path while routed tokens per expert stay at or
 // below this many (decode batches); above it the MFMA grouped GEMM.
 constexpr int kGemvTokensPerExpert = 8;
+// The decode routing's read-ahead of the next kernel's gate/up rows: bytes
+// (whole expert groups) and workgroups.
+constexpr size_t kReadAheadBytes = 16u << 20;
+constexpr int kReadAheadBlocks = 128;
 
 thread_local std::string g_open_error;
 
@@ -615,6 +619,28 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         }
         // the fp32 path's kernels find their own tokens from the choices
         L->skipped_dispatch = path == GTMOE_PATH_FP32 && T <= kSelfDispatchMaxTokens;
+        // When the batch reaches most experts, the gate/up kernel that
+        // follows streams nearly every group's rows, shared groups first and
+        // then routed experts in order: the routing launch reads the first
+        // groups ahead while its own work leaves HBM idle.
+        if (L->skipped_dispatch && !hash && T * L->k >= 2 * L->E) {
+            const DeviceMatrix &gm = L->gate, &um = L->up;
+            const size_t per_group = gm.group_value_bytes() + um.group_value_bytes() +
+                                     (gm.scales ? gm.group_scales() * sizeof(float) : 0) +
+                                     (um.scales ? um.group_scales() * sizeof(float) : 0);
+            const size_t groups = std::min<size_t>(gm.groups, kReadAheadBytes / per_group);
+            if (groups > 0) {
+                f.ra[0] = gm.values;
+                f.ra_bytes[0] = groups * gm.group_value_bytes();
+                f.ra[1] = um.values;
+                f.ra_bytes[1] = groups * um.group_value_bytes();
+                f.ra[2] = gm.scales;
+                f.ra_bytes[2] = gm.scales ? groups * gm.group_scales() * sizeof(float) : 0;
+                f.ra[3] = um.scales;
+                f.ra_bytes[3] = um.scales ? groups * um.group_scales() * sizeof(float) : 0;
+                f.ra_blocks = kReadAheadBlocks;
+            }
+        }
         RUN(ctx, s, "route_small", launch_route_fused(f, in.f64, hash, !L->skipped_dispatch, s));
         return GTMOE_OK;
     }

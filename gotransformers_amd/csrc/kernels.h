@@ -75,6 +75,14 @@ struct FusedArgs {
     // zero between launches); the last to arrive runs the top-k.
     int parts;
     int32_t *part_cnt;
+    // read-ahead (not with hash routing): ra_blocks workgroups past the
+    // routing and router-warming ones read the first ra_bytes[r] bytes
+    // (multiples of 16) of ra[r] and keep nothing, so that the rows the next
+    // kernel streams first are in the memory-side cache when it starts
+    const void *ra[4];
+    size_t ra_bytes[4];
+    int ra_blocks;
+    int warm_blocks;  // set by the launcher
 };
 
 // Workgroups per token of the few-token routing: more than one only for

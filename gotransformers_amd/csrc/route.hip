@@ -1367,7 +1367,7 @@ __device__ __forceinline__ void warm_router(const FusedArgs &a)
 {
     const int P = a.parts;
     const int nroute = a.T * P;
-    const int i = blockIdx.x - nroute, nq = (gridDim.x - nroute) / 8;
+    const int i = blockIdx.x - nroute, nq = a.warm_blocks / 8;
     const int xcd = blockIdx.x & 7;
     int r0 = 0, r1 = a.E;
     if (8 % P == 0) {
@@ -1393,6 +1393,30 @@ __device__ __forceinline__ void warm_router(const FusedArgs &a)
     asm volatile("" ::"v"(acc));  // the loads are kept, and waited for before the wave ends
 }
 
+// Read-ahead workgroup i of n: slice i of n of each region, one 16-byte
+// load per lane per 16 KiB (four in flight), nothing kept.
+__device__ __forceinline__ void read_ahead(const FusedArgs &a, int i, int n)
+{
+    uint32_t acc = 0;
+#pragma unroll 1
+    for (int r = 0; r < 4; ++r) {
+        const size_t n16 = a.ra_bytes[r] / 16;
+        const uint4 *base = reinterpret_cast<const uint4 *>(a.ra[r]);
+        const size_t b0 = n16 * i / n, b1 = n16 * (i + 1) / n;
+        for (size_t u0 = b0; u0 < b1; u0 += 4096) {
+            uint4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const size_t u = u0 + threadIdx.x + 1024 * q;
+                v[q] = u < b1 ? base[u] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc ^= v[q].x ^ v[q].y ^ v[q].z ^ v[q].w;
+        }
+    }
+    asm volatile("" ::"v"(acc));  // the loads are kept, and waited for before the wave ends
+}
+
 // Warming workgroups for a router routing launch whose routing workgroups
 // fit the GPU at once (a later round would find the rows warm anyway): 8 per
 // 16 KiB of the rows one XCD reads, at most 16 per XCD.
@@ -1408,7 +1432,9 @@ template <typename InT, bool NORM, bool HASH, int EPL, int NX>
 __global__ __launch_bounds__(1024) void route_token_kernel(FusedArgs a)
 {
     if (!HASH && (int)blockIdx.x >= a.T * a.parts) {
-        warm_router(a);
+        const int j = blockIdx.x - a.T * a.parts - a.warm_blocks;
+        if (j < 0) warm_router(a);
+        else read_ahead(a, j, a.ra_blocks);
         return;
     }
     __shared__ double lg[kMaxExperts];
@@ -1710,9 +1736,12 @@ int route_fused_parts(int T, int E, bool hash)
 }
 
 template <typename InT, bool NORM, int NX>
-static hipError_t launch_token_nx(const FusedArgs &a, bool hash, hipStream_t s)
+static hipError_t launch_token_nx(const FusedArgs &fa, bool hash, hipStream_t s)
 {
-    dim3 grid(a.T * a.parts + route_warm_blocks(a.T, a.E, a.kp, a.parts, hash));
+    FusedArgs a = fa;
+    a.warm_blocks = route_warm_blocks(a.T, a.E, a.kp, a.parts, hash);
+    if (hash) a.ra_blocks = 0;
+    dim3 grid(a.T * a.parts + a.warm_blocks + a.ra_blocks);
     if (hash) hipLaunchKernelGGL((route_token_kernel<InT, NORM, true, 1, NX>), grid, dim3(1024), 0, s, a);
     else if (a.E <= 64) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 1, NX>), grid, dim3(1024), 0, s, a);
     else if (a.E <= 128) hipLaunchKernelGGL((route_token_kernel<InT, NORM, false, 2, NX>), grid, dim3(1024), 0, s, a);
