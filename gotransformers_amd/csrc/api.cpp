@@ -619,11 +619,11 @@ int32_t prepare_and_route(gtmoe_layer *L, int T, const Inputs &in, const int64_t
         }
         // the fp32 path's kernels find their own tokens from the choices
         L->skipped_dispatch = path == GTMOE_PATH_FP32 && T <= kSelfDispatchMaxTokens;
-        // When the batch reaches most experts, the gate/up kernel that
-        // follows streams nearly every group's rows, shared groups first and
-        // then routed experts in order: the routing launch reads the first
-        // groups ahead while its own work leaves HBM idle.
-        if (L->skipped_dispatch && !hash && T * L->k >= 2 * L->E) {
+        // When the batch holds at least one entry per expert, the gate/up
+        // kernel that follows streams most groups' rows, shared groups first
+        // and then routed experts in order: the routing launch reads the
+        // first groups ahead while its own work leaves HBM idle.
+        if (L->skipped_dispatch && !hash && T * L->k >= L->E) {
             const DeviceMatrix &gm = L->gate, &um = L->up;
             const size_t per_group = gm.group_value_bytes() + um.group_value_bytes() +
                                      (gm.scales ? gm.group_scales() * sizeof(float) : 0) +
